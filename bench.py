@@ -1,0 +1,319 @@
+#!/usr/bin/env python3
+"""Throughput of the quantized linear-layer matmul on one MI355X.
+
+Workload (one "step"): the linears of the Whisper large-v3 encoder at one
+30 s window, M = 1500 rows, weights in Q5_1 -- 32 layers x {q, k, v, out
+[1280x1280], fc1 [5120x1280], fc2 [1280x5120]}, with biases where Whisper has
+them (no bias on k).  Each layer quantizes its three distinct inputs (the
+attention-block input shared by q/k/v, the attention output, the MLP input)
+and the fc1 output, then runs the six products.  Weights are seeded N(0, 0.02)
+quantized to Q5_1 (472 MB resident, more than the 256 MB MALL); activations
+are seeded N(0, 1) and resident in HBM before timing starts.
+
+Reported: whole-step int8 TOPS (2*M*N*K per linear), the GEMM kernel's own
+rate against the MI355X int8 MFMA peak (HIP events around each launch), the
+decode-GEMV bandwidth for the large-v3 decoder linear set at M = 5 in Q5_0,
+and the reference CPU path (oracle/cpu_baseline.c, AVX-512 VNNI / AVX2
+restatement of matmul_t_q) timed on this host on one encoder layer.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Q-matmul TOPS @M=1500 encoder; decode GEMV HBM GB/s @M=5 (large-v3 Q5_1)"
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+HBM_PEAK_GBS = 8000.0    # MI355X HBM3E
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def encoder_workload(A, synth, torch, dtype: int, m: int, seed0: int):
+    cfg = synth.LARGE_V3
+    d, fc, layers = cfg["d"], cfg["fc"], cfg["layers"]
+    shapes = synth.encoder_layer_shapes(d, fc)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed0)
+    layers_w = []
+    t0 = time.time()
+    workers = min(16, os.cpu_count() or 1)
+    for layer in range(layers):
+        specs = [(dtype, n, k, seed0 + 100 * layer + i) for i, (_, n, k) in enumerate(shapes)]
+        raws = synth.normal_weights_many(specs, workers)
+        layers_w.append({name: A.DeviceWeight(dtype, n, k, raw) for (name, n, k), raw in zip(shapes, raws)})
+    log(f"encoder weights uploaded ({layers} layers, {time.time() - t0:.1f} s)")
+    inputs = {
+        "qkv": torch.randn(m, d, device=dev, generator=g),
+        "attn": torch.randn(m, d, device=dev, generator=g),
+        "mlp": torch.randn(m, d, device=dev, generator=g),
+        "h": torch.randn(m, fc, device=dev, generator=g),
+    }
+    bias = {name: (None if name == "k" else torch.randn(n, device=dev, generator=g) * 0.1)
+            for name, n, _ in shapes}
+    outs = {name: torch.empty(m, n, device=dev) for name, n, _ in shapes}
+    wsz = {key: A.workspace_size(m, t.shape[1]) for key, t in inputs.items()}
+    wsp = {key: torch.empty(wsz[key], dtype=torch.uint8, device=dev) for key in inputs}
+    ops = layers * sum(2 * m * n * k for _, n, k in shapes)
+    return dict(layers=layers_w, inputs=inputs, bias=bias, outs=outs, wsz=wsz, wsp=wsp, ops=ops, shapes=shapes,
+                m=m, d=d, fc=fc)
+
+SRC = {"q": "qkv", "k": "qkv", "v": "qkv", "out": "attn", "fc1": "mlp", "fc2": "h"}
+
+
+def encoder_step(A, W, stream):
+    m = W["m"]
+    for lw in W["layers"]:
+        for key in ("qkv", "attn", "mlp", "h"):
+            t = W["inputs"][key]
+            A.quantize_dev(t, m, t.shape[1], W["wsp"][key], W["wsz"][key], stream)
+        for name, _, _ in W["shapes"]:
+            lw[name].matmul_prequant_dev(W["wsp"][SRC[name]], m, W["outs"][name], W["bias"][name], stream)
+
+
+def time_encoder(A, torch, W, steps: int, warmup: int, stream):
+    for _ in range(warmup):
+        encoder_step(A, W, stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        encoder_step(A, W, stream)
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(end) / steps
+    return ms, wall
+
+
+def time_gemm_kernel(A, torch, W, stream, reps: int = 2):
+    """Average k_gemm launch duration with HIP events around every launch
+    (events on torch's current stream, the stream the kernels run on)."""
+    m = W["m"]
+    for key in ("qkv", "attn", "mlp", "h"):
+        t = W["inputs"][key]
+        A.quantize_dev(t, m, t.shape[1], W["wsp"][key], W["wsz"][key], stream)
+    pairs = []
+    ops = 0
+    for _ in range(reps):
+        for lw in W["layers"]:
+            for name, n, k in W["shapes"]:
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                lw[name].matmul_prequant_dev(W["wsp"][SRC[name]], m, W["outs"][name], W["bias"][name], stream)
+                e1.record()
+                pairs.append((e0, e1))
+                ops += 2 * m * n * k
+    torch.cuda.synchronize()
+    total_ms = sum(a.elapsed_time(b) for a, b in pairs)
+    return total_ms / len(pairs), ops / len(pairs), len(pairs)
+
+
+def decode_workload(A, synth, torch, dtype: int, m: int, seed0: int):
+    cfg = synth.LARGE_V3
+    d, fc, layers, vocab = cfg["d"], cfg["fc"], cfg["layers"], cfg["n_vocab"]
+    shapes = synth.decoder_layer_shapes(d, fc) * layers + [("logits", vocab, d)]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed0)
+    t0 = time.time()
+    items, keep = [], []
+    wbytes = 0
+    io_bytes = 0
+    workers = min(16, os.cpu_count() or 1)
+    for c0 in range(0, len(shapes), 16):
+        chunk = shapes[c0:c0 + 16]
+        raws = synth.normal_weights_many([(dtype, n, k, seed0 + c0 + j) for j, (_, n, k) in enumerate(chunk)],
+                                         workers)
+        for (name, n, k), raw in zip(chunk, raws):
+            items.append(_decode_item(A, torch, dev, g, dtype, name, n, k, raw, m, keep))
+            wbytes += n * (k // 32) * synth.BLOCK_BYTES[dtype]
+            io_bytes += 4 * m * k + 4 * m * n
+    arr = A.make_linears(items)
+    wsz = A.grouped_workspace_size(arr)
+    ws = torch.empty(wsz, dtype=torch.uint8, device=dev)
+    log(f"decoder weights uploaded ({len(shapes)} linears, {wbytes / 1e6:.1f} MB, {time.time() - t0:.1f} s)")
+    return dict(arr=arr, ws=ws, wsz=wsz, keep=keep, bytes=wbytes + io_bytes, wbytes=wbytes, count=len(shapes))
+
+
+def _decode_item(A, torch, dev, g, dtype, name, n, k, raw, m, keep):
+    w = A.DeviceWeight(dtype, n, k, raw)
+    a = torch.randn(m, k, device=dev, generator=g)
+    b = None if name.endswith(".k") or name == "logits" else torch.randn(n, device=dev, generator=g) * 0.1
+    o = torch.empty(m, n, device=dev)
+    keep += [w, a, b, o]
+    return (w, a, b, o, m)
+
+
+def time_decode(A, torch, D, steps: int, warmup: int, stream):
+    for _ in range(warmup):
+        A.matmul_grouped_dev(D["arr"], D["ws"], D["wsz"], stream)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        A.matmul_grouped_dev(D["arr"], D["ws"], D["wsz"], stream)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def cpu_baseline(synth, dtype: int, m: int, budget_s: float):
+    """The reference CPU path (oracle/cpu_baseline.c) on one large-v3 encoder
+    layer: each of the six linears on its first call (cold path, as the
+    encoder runs in production), median of repeated runs."""
+    import numpy as np
+
+    import oracle as O
+
+    cfg = synth.LARGE_V3
+    shapes = synth.encoder_layer_shapes(cfg["d"], cfg["fc"])
+    threads = O.cpu_threads()
+    cap = os.environ.get("OMP_NUM_THREADS")
+    if cap and cap.isdigit():
+        threads = min(threads, int(cap))
+    rng = np.random.default_rng(7)
+    raws = [synth.normal_weights(dtype, n, k, seed=900 + i) for i, (_, n, k) in enumerate(shapes)]
+    acts = {k: rng.standard_normal((m, k)).astype(np.float32) for k in {k for _, _, k in shapes}}
+    per_linear = [[] for _ in shapes]
+    t_start = time.time()
+    reps = 0
+    while reps < 5 and (reps < 1 or time.time() - t_start < budget_s):
+        for i, (_, n, k) in enumerate(shapes):
+            t = O.CpuQTensor(dtype, n, k, raws[i])
+            t0 = time.perf_counter()
+            t.matmul(acts[k], threads=threads)
+            per_linear[i].append(time.perf_counter() - t0)
+            tier = t.tier_used
+            t.close()
+        reps += 1
+    layer_s = sum(statistics.median(v) for v in per_linear)
+    ops = sum(2 * m * n * k for _, n, k in shapes)
+    tier_name = {0: "avx512-vnni", 1: "avx2", 2: "f32"}[tier]
+    return {
+        "value": round(ops / layer_s / 1e12, 4),
+        "unit": "TOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"one large-v3 encoder layer (6 Q5_1 linears, M={m}), cold path, median of {reps} runs "
+                  f"per linear, tier {tier_name}, {threads} threads",
+        "layer_ms": round(layer_s * 1e3, 2),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--m", type=int, default=1500)
+    ap.add_argument("--quant", default="Q5_1")
+    ap.add_argument("--decode-quant", default="Q5_0")
+    ap.add_argument("--decode-m", type=int, default=5)
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from rusty_whisper_amd import _abi as A
+    from rusty_whisper_amd import synth
+
+    A.init(0)
+    torch.cuda.set_device(0)
+    stream = torch.cuda.current_stream().cuda_stream
+    dtype = synth.BY_NAME[args.quant]
+
+    W = encoder_workload(A, synth, torch, dtype, args.m, seed0=1)
+    ms, wall = time_encoder(A, torch, W, args.steps, args.warmup, stream)
+    tops = W["ops"] / (ms * 1e-3) / 1e12
+    log(f"encoder step {ms:.3f} ms  ({tops:.1f} TOPS, wall {wall:.2f} s for {args.steps} steps)")
+
+    gemm_ms, gemm_ops, launches = time_gemm_kernel(A, torch, W, stream)
+    gemm_tops = gemm_ops / (gemm_ms * 1e-3) / 1e12
+    log(f"k_gemm average launch {gemm_ms * 1e3:.1f} us over {launches} launches -> {gemm_tops:.1f} TOPS")
+
+    result = {
+        "metric": METRIC,
+        "value": round(tops, 3),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i8",
+        "data": "synthetic",
+        "config": {
+            "workload": f"large-v3 encoder linears, {args.quant}, M={args.m}: 32 layers x "
+                        f"(q,k,v,out 1280x1280; fc1 5120x1280; fc2 1280x5120), activations quantized on device",
+            "m": args.m,
+            "layers": 32,
+            "quant": args.quant,
+            "ops_per_step": W["ops"],
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(gemm_tops, 3),
+            "peak": INT8_PEAK_TOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gemm_tops / INT8_PEAK_TOPS, 4),
+            "traffic": None,
+            "kernel": f"k_gemm<{args.quant}> (int8 ops 2*M*N*K per launch; unit is tera-ops for int8)",
+            "avg_launch_us": round(gemm_ms * 1e3, 2),
+        },
+    }
+    del W
+    torch.cuda.empty_cache()
+
+    if not args.no_decode:
+        D = decode_workload(A, synth, torch, synth.BY_NAME[args.decode_quant], args.decode_m, seed0=5000)
+        dms = time_decode(A, torch, D, max(3, args.steps // 2), 1, stream)
+        gbs = D["bytes"] / (dms * 1e-3) / 1e9
+        log(f"decode set {dms:.3f} ms ({gbs:.1f} GB/s)")
+        result["decode"] = {
+            "metric": f"decode GEMV HBM GB/s @M={args.decode_m}",
+            "workload": f"large-v3 decoder linears, {args.decode_quant}, M={args.decode_m}: 32 layers x 10 "
+                        f"linears + logits [51866x1280], {D['count']} independent linears per step",
+            "value": round(gbs, 2),
+            "unit": "GB/s",
+            "ms_per_step": round(dms, 4),
+            "bytes_per_step": D["bytes"],
+            "peak": HBM_PEAK_GBS,
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+        }
+        del D
+        torch.cuda.empty_cache()
+
+    if not args.no_cpu:
+        cb = cpu_baseline(synth, dtype, args.m, args.cpu_seconds)
+        log(f"cpu baseline {cb['value']} TOPS ({cb['sample']})")
+        result["cpu_baseline"] = cb
+
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,172 @@
+/*
+ * rw_rocm.h -- C ABI of librw_rocm.so, the MI355X (gfx950) implementation of
+ * rusty_whisper's quantized linear-layer matmul.
+ *
+ * The reference computes y = x W^T (+ b) with W held in ggml blocks
+ * (Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q8_0, 32 elements per block) and x an f32
+ * Tensor, through:
+ *   QTensor::new            src/quant.rs:553-563
+ *   QTensor::{row_f32,to_dense}  src/quant.rs:566-576
+ *   matmul_t_q              src/quant.rs:754-1051
+ *   linear_w                src/quant.rs:1054-1063
+ * Each entry below names the reference function it replaces.  Arithmetic is
+ * the reference's: activations are quantized per 32-block to int8 exactly as
+ * quantize_acts_i8 (src/quant.rs:691-716) does, the per-block integer sums
+ * sum(q_a*q_b) are exact, and each output is
+ *     sum_bl d_a*d_b*S + m_b*d_a*sum(q_a)   (+ bias, added last)
+ * combined in f32.
+ *
+ * Conventions (the crate's existing C ABI, src/wasm.rs:25-110, returns an
+ * i32 status and keeps error text separately):
+ *   - every function returns RW_OK (0) or a negative RW_E* code;
+ *   - rw_rocm_last_error() copies the calling thread's last error text;
+ *   - no function aborts the process on bad input; the reference panics on
+ *     the same conditions (src/quant.rs:757-758, 129), and its Rust binding
+ *     turns a non-zero status back into that panic.
+ * Thread safety: every entry point may be called concurrently from several
+ * threads on shared rw_weight handles (the reference shares &Model across
+ * transcription threads, src/transcribe.rs:1525-1552).  Host-pointer entries
+ * are synchronous.  Device-pointer entries are asynchronous on the stream
+ * passed in.
+ */
+#ifndef RW_ROCM_H
+#define RW_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RW_OK 0
+#define RW_EINVAL (-1)  /* bad dtype, k % 32 != 0, shape or length mismatch, NULL */
+#define RW_ENODEV (-2)  /* no usable gfx950 device / bad device index */
+#define RW_EHIP (-3)    /* a HIP runtime call failed */
+#define RW_ENOMEM (-4)  /* device allocation failed */
+
+/* ggml dtype ids (src/quant.rs:43-52) */
+#define RW_Q4_0 2
+#define RW_Q4_1 3
+#define RW_Q5_0 6
+#define RW_Q5_1 7
+#define RW_Q8_0 8
+
+typedef struct rw_weight rw_weight;
+
+/* Library version, e.g. 0x000100 for 0.1.0. */
+int rw_rocm_version(void);
+
+/* Number of visible devices this library can run on (gfx950 only), or a
+ * negative RW_E* code. */
+int rw_rocm_device_count(void);
+
+/* Select and initialise `device` for the calling thread.  Fails with
+ * RW_ENODEV when it is absent or not gfx950.  Replaces nothing in the
+ * reference (the CPU path needs no set-up); the Rust binding calls it once,
+ * from the OnceLock that guards device use. */
+int rw_rocm_init(int device);
+
+/* Bytes per ggml block of `dtype` (18/20/22/24/34), or RW_EINVAL.
+ * Replaces block_bytes, src/quant.rs:43-52. */
+int rw_rocm_block_bytes(int dtype);
+
+/* Upload an [n, k] ggml-quantized matrix (n rows of k/32 consecutive blocks,
+ * src/quant.rs:493-494) to the current device.  The blocks are repacked once,
+ * on the device, into the resident layout the kernels read; they stay in HBM
+ * until rw_rocm_weight_free.  raw_len must equal n*(k/32)*block_bytes(dtype).
+ * Replaces QTensor::new (src/quant.rs:553-563) plus its lazily packed int8
+ * cache (src/quant.rs:589-639). */
+int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, size_t raw_len,
+                          rw_weight **out);
+
+/* Release a weight (the Rust Drop of the device handle). NULL is a no-op. */
+int rw_rocm_weight_free(rw_weight *w);
+
+/* dtype, rows, cols and resident device bytes of an uploaded weight. */
+int rw_rocm_weight_info(const rw_weight *w, int *dtype, size_t *n, size_t *k, size_t *device_bytes);
+
+/* out[m, n] = a[m, k] W^T (+ bias[n] when bias != NULL), host pointers,
+ * synchronous.  Replaces matmul_t_q (src/quant.rs:754-1051) and, with a
+ * bias, linear_w's Quant arm (src/quant.rs:1054-1063).  m == 0 is valid and
+ * writes nothing. */
+int rw_rocm_matmul_t_q(const rw_weight *w, const float *a, size_t m, size_t k, const float *bias,
+                       float *out);
+
+/* Device-resident form of rw_rocm_matmul_t_q: a, bias and out are device
+ * pointers on the weight's device; the work is queued on `stream` (a
+ * hipStream_t; NULL = the default stream) and the call returns without
+ * waiting.  `workspace` (device memory, >= rw_rocm_matmul_workspace_size(m,
+ * k) bytes) holds the quantized activations; NULL makes the library use a
+ * buffer of its own for this stream (grown as needed, so it may allocate).
+ * Has no reference counterpart as such: it is matmul_t_q without the host
+ * copies, for callers that keep activations on the device. */
+int rw_rocm_matmul_t_q_dev(const rw_weight *w, const float *a, size_t m, size_t k,
+                           const float *bias, float *out, void *workspace, size_t workspace_len,
+                           void *stream);
+
+/* Workspace bytes rw_rocm_matmul_t_q_dev needs for an [m, k] activation. */
+size_t rw_rocm_matmul_workspace_size(size_t m, size_t k);
+
+/* The two halves of rw_rocm_matmul_t_q_dev, for callers that reuse one
+ * quantized activation across several weights.  rw_rocm_quantize_dev runs
+ * quantize_acts_i8 (src/quant.rs:691-716) on device a[m, k] into `workspace`;
+ * rw_rocm_matmul_prequant_dev then computes out = a W^T (+ bias) from that
+ * workspace (same m, and W's k must equal the k it was quantized with).
+ * The reference quantizes inside every matmul_t_q call
+ * (src/quant.rs:766); its Q, K and V projections share their input
+ * (src/encoder.rs:130-141, src/decoder.rs:148-158), so quantizing once and
+ * running three products gives bitwise the same three results. */
+int rw_rocm_quantize_dev(const float *a, size_t m, size_t k, void *workspace, size_t workspace_len,
+                         void *stream);
+int rw_rocm_matmul_prequant_dev(const rw_weight *w, const void *workspace, size_t m, const float *bias,
+                                float *out, void *stream);
+
+/* One entry of a grouped launch: out_g[m_g, n_g] = a_g W_g^T (+ bias_g). */
+typedef struct rw_linear {
+    const rw_weight *w;
+    const float *a;    /* device [m, k] */
+    const float *bias; /* device [n] or NULL */
+    float *out;        /* device [m, n] */
+    size_t m;
+} rw_linear;
+
+/* Run `count` independent linears in as few launches as their shapes allow
+ * (all entries must share m <= 8, the decode-GEMV regime).  Device pointers,
+ * asynchronous on `stream`.  Each result is bitwise identical to the same
+ * linear run alone through rw_rocm_matmul_t_q_dev.  Replaces a sequence of
+ * independent linear_w calls with the same activation row count (the Q/K/V
+ * projections of src/decoder.rs:148-158 share x; the cross K/V of every layer
+ * at src/decoder.rs:44-53 are independent). */
+int rw_rocm_matmul_grouped_dev(const rw_linear *items, size_t count, void *workspace,
+                               size_t workspace_len, void *stream);
+
+/* Workspace bytes rw_rocm_matmul_grouped_dev needs for these items. */
+size_t rw_rocm_grouped_workspace_size(const rw_linear *items, size_t count);
+
+/* Dequantize rows [row0, row0+nrows) of W to f32 into host `out`
+ * (nrows*k floats): x = d*q + m exactly as dequant_row_scalar
+ * (src/quant.rs:528-537), bit for bit.  Replaces QTensor::row_f32
+ * (src/quant.rs:566-570) and, over all rows, QTensor::to_dense
+ * (src/quant.rs:572-576). */
+int rw_rocm_dequant_rows(const rw_weight *w, size_t row0, size_t nrows, float *out);
+
+/* Validation entry: quantize host activations a[m, k] on the device and
+ * return q[m*k] (natural element order), d[m*k/32], sum[m*k/32] -- the QActs
+ * of quantize_acts_i8 (src/quant.rs:679-716), bit for bit. */
+int rw_rocm_quantize_acts(const float *a, size_t m, size_t k, int8_t *q, float *d, int32_t *sum);
+
+/* Validation entry: the exact per-block integer sums
+ * S[i, j, bl] = sum_e qa[i, bl*32+e] * q_b[j, bl*32+e] for host int8
+ * activations qa[m, k] (natural order) against W, computed with the same
+ * int8 MFMA tiles as the matmul.  S is host [m, n, k/32]. */
+int rw_rocm_block_dots(const rw_weight *w, const int8_t *qa, size_t m, int32_t *S);
+
+/* Copy the calling thread's last error text (NUL-terminated, truncated to
+ * len).  Returns the full text length. */
+int rw_rocm_last_error(char *buf, size_t len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

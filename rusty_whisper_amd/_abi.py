@@ -1,0 +1,231 @@
+"""ctypes binding of librw_rocm.so (the C ABI declared in include/rw_rocm.h).
+
+This is the thin, typed layer every Python caller goes through.  A non-zero
+status becomes RwError carrying the library's error text; the reference
+panics on the same conditions (src/quant.rs:757-758, 129).  There is no CPU
+fallback: if the library or a gfx950 device is missing, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librw_rocm.so")
+HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "rw_rocm.h")
+
+RW_OK, RW_EINVAL, RW_ENODEV, RW_EHIP, RW_ENOMEM = 0, -1, -2, -3, -4
+CODE_NAMES = {RW_EINVAL: "RW_EINVAL", RW_ENODEV: "RW_ENODEV", RW_EHIP: "RW_EHIP", RW_ENOMEM: "RW_ENOMEM"}
+Q4_0, Q4_1, Q5_0, Q5_1, Q8_0 = 2, 3, 6, 7, 8
+DTYPES = (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0)
+QK = 32
+GEMV_MAX_M = 8
+
+
+class RwError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{CODE_NAMES.get(code, code)}: {message}")
+        self.code = code
+        self.message = message
+
+
+class rw_linear(C.Structure):
+    _fields_ = [
+        ("w", C.c_void_p),
+        ("a", C.c_void_p),
+        ("bias", C.c_void_p),
+        ("out", C.c_void_p),
+        ("m", C.c_size_t),
+    ]
+
+
+_SIGNATURES = {
+    "rw_rocm_version": (C.c_int, []),
+    "rw_rocm_device_count": (C.c_int, []),
+    "rw_rocm_init": (C.c_int, [C.c_int]),
+    "rw_rocm_block_bytes": (C.c_int, [C.c_int]),
+    "rw_rocm_weight_upload": (C.c_int, [C.c_int, C.c_size_t, C.c_size_t, C.c_void_p, C.c_size_t,
+                                        C.POINTER(C.c_void_p)]),
+    "rw_rocm_weight_free": (C.c_int, [C.c_void_p]),
+    "rw_rocm_weight_info": (C.c_int, [C.c_void_p, C.POINTER(C.c_int), C.POINTER(C.c_size_t),
+                                      C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
+    "rw_rocm_matmul_t_q": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p,
+                                     C.c_void_p]),
+    "rw_rocm_matmul_t_q_dev": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p,
+                                         C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "rw_rocm_matmul_workspace_size": (C.c_size_t, [C.c_size_t, C.c_size_t]),
+    "rw_rocm_quantize_dev": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_size_t,
+                                       C.c_void_p]),
+    "rw_rocm_matmul_prequant_dev": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p,
+                                              C.c_void_p]),
+    "rw_rocm_matmul_grouped_dev": (C.c_int, [C.POINTER(rw_linear), C.c_size_t, C.c_void_p, C.c_size_t,
+                                             C.c_void_p]),
+    "rw_rocm_grouped_workspace_size": (C.c_size_t, [C.POINTER(rw_linear), C.c_size_t]),
+    "rw_rocm_dequant_rows": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]),
+    "rw_rocm_quantize_acts": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p,
+                                        C.c_void_p]),
+    "rw_rocm_block_dots": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "rw_rocm_last_error": (C.c_int, [C.c_char_p, C.c_size_t]),
+}
+
+_lib = None
+
+
+def header_symbols() -> list[str]:
+    """Every function include/rw_rocm.h declares."""
+    text = open(HEADER_PATH).read()
+    return sorted(set(re.findall(r"\b(rw_rocm_\w+)\s*\(", text)))
+
+
+def lib() -> C.CDLL:
+    """Load librw_rocm.so (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RwError(RW_ENODEV, f"{LIB_PATH} is not built (run __graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    buf = C.create_string_buffer(1024)
+    lib().rw_rocm_last_error(buf, len(buf))
+    return buf.value.decode(errors="replace")
+
+
+def check(rc: int) -> int:
+    if rc < 0:
+        raise RwError(rc, last_error())
+    return rc
+
+
+def _ptr(a) -> int | None:
+    if a is None:
+        return None
+    if isinstance(a, np.ndarray):
+        return a.ctypes.data
+    if hasattr(a, "data_ptr"):  # torch.Tensor on the device
+        return a.data_ptr()
+    return int(a)
+
+
+def init(device: int = 0) -> None:
+    check(lib().rw_rocm_init(device))
+
+
+def device_count() -> int:
+    return lib().rw_rocm_device_count()
+
+
+def block_bytes(dtype: int) -> int:
+    return check(lib().rw_rocm_block_bytes(dtype))
+
+
+class DeviceWeight:
+    """A quantized [n, k] matrix resident in HBM (rw_weight*)."""
+
+    def __init__(self, dtype: int, n: int, k: int, raw: np.ndarray):
+        raw = np.ascontiguousarray(raw, dtype=np.uint8)
+        h = C.c_void_p()
+        check(lib().rw_rocm_weight_upload(dtype, n, k, raw.ctypes.data, raw.nbytes, C.byref(h)))
+        self.handle = h.value
+        self.dtype, self.n, self.k = dtype, n, k
+
+    def info(self):
+        dt, n, k, nbytes = C.c_int(), C.c_size_t(), C.c_size_t(), C.c_size_t()
+        check(lib().rw_rocm_weight_info(self.handle, C.byref(dt), C.byref(n), C.byref(k), C.byref(nbytes)))
+        return dt.value, n.value, k.value, nbytes.value
+
+    def matmul(self, a: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
+        """Host arrays in, host array out (rw_rocm_matmul_t_q)."""
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        if a.ndim != 2:
+            raise ValueError("activations must be 2-D [m, k]")
+        m, k = a.shape
+        out = np.empty((m, self.n), dtype=np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        if b is not None and b.shape != (self.n,):
+            raise ValueError(f"bias must have shape ({self.n},)")
+        check(lib().rw_rocm_matmul_t_q(self.handle, a.ctypes.data, m, k, _ptr(b), out.ctypes.data))
+        return out
+
+    def matmul_dev(self, a, m: int, out, bias=None, workspace=None, workspace_len: int = 0,
+                   stream: int | None = None) -> None:
+        """Device pointers (ints or torch tensors), queued on `stream`."""
+        check(lib().rw_rocm_matmul_t_q_dev(self.handle, _ptr(a), m, self.k, _ptr(bias), _ptr(out),
+                                           _ptr(workspace), workspace_len, stream))
+
+    def matmul_prequant_dev(self, workspace, m: int, out, bias=None, stream: int | None = None) -> None:
+        """out = (activations quantized into `workspace`) W^T (+ bias)."""
+        check(lib().rw_rocm_matmul_prequant_dev(self.handle, _ptr(workspace), m, _ptr(bias), _ptr(out),
+                                                stream))
+
+    def dequant_rows(self, row0: int = 0, nrows: int | None = None) -> np.ndarray:
+        nrows = self.n - row0 if nrows is None else nrows
+        out = np.empty((nrows, self.k), dtype=np.float32)
+        check(lib().rw_rocm_dequant_rows(self.handle, row0, nrows, out.ctypes.data))
+        return out
+
+    def block_dots(self, qa: np.ndarray) -> np.ndarray:
+        qa = np.ascontiguousarray(qa, dtype=np.int8)
+        m = qa.shape[0]
+        S = np.empty((m, self.n, self.k // QK), dtype=np.int32)
+        check(lib().rw_rocm_block_dots(self.handle, qa.ctypes.data, m, S.ctypes.data))
+        return S
+
+    def free(self) -> None:
+        if getattr(self, "handle", None):
+            check(lib().rw_rocm_weight_free(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def workspace_size(m: int, k: int) -> int:
+    return lib().rw_rocm_matmul_workspace_size(m, k)
+
+
+def quantize_dev(a, m: int, k: int, workspace, workspace_len: int, stream: int | None = None) -> None:
+    """Quantize device activations a[m, k] into `workspace` (queued on `stream`)."""
+    check(lib().rw_rocm_quantize_dev(_ptr(a), m, k, _ptr(workspace), workspace_len, stream))
+
+
+def quantize_acts(a: np.ndarray):
+    """Device quantize_acts_i8 -> (q int8 [m,k], d f32 [m,nb], sum i32 [m,nb])."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    m, k = a.shape
+    nb = k // QK
+    q = np.empty((m, k), dtype=np.int8)
+    d = np.empty((m, nb), dtype=np.float32)
+    s = np.empty((m, nb), dtype=np.int32)
+    check(lib().rw_rocm_quantize_acts(a.ctypes.data, m, k, q.ctypes.data, d.ctypes.data, s.ctypes.data))
+    return q, d, s
+
+
+def make_linears(items) -> "C.Array":
+    """items: iterable of (DeviceWeight, a_ptr, bias_ptr_or_None, out_ptr, m)."""
+    items = list(items)
+    arr = (rw_linear * len(items))()
+    for i, (w, a, b, o, m) in enumerate(items):
+        arr[i] = rw_linear(w.handle, _ptr(a), _ptr(b), _ptr(o), m)
+    return arr
+
+
+def grouped_workspace_size(arr) -> int:
+    return lib().rw_rocm_grouped_workspace_size(arr, len(arr))
+
+
+def matmul_grouped_dev(arr, workspace=None, workspace_len: int = 0, stream: int | None = None) -> None:
+    check(lib().rw_rocm_matmul_grouped_dev(arr, len(arr), _ptr(workspace), workspace_len, stream))

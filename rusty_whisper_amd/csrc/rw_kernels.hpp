@@ -1,0 +1,465 @@
+// rw_kernels.hpp -- gfx950 device code for the quantized linear-layer matmul.
+//
+// Kernels (the arithmetic of src/quant.rs, restated for CDNA4):
+//   k_repack        ggml blocks -> resident planes (once per weight)
+//   k_dequant       planes -> f32 rows, bit-exact with dequant_row_scalar
+//                   (src/quant.rs:528-537)
+//   k_quantize      f32 activations -> int8 blocks + d_a + sums, bit-exact
+//                   with quantize_acts_i8 (src/quant.rs:691-716)
+//   k_block_dots    exact per-block integer sums via int8 MFMA (validation)
+//   k_gemm          encoder shape (m > 8): v_mfma_i32_32x32x32_i8, one MFMA
+//                   per 32x32 output tile per block, f32 combine on the VALU
+//   k_gemv          decoder shape (m <= 8): one lane per weight row,
+//                   v_dot4_i32_i8 against activations held in SGPRs
+//
+// One combine rule for every output element, in every kernel:
+//     acc  = fma(d_a*d_b, float(S), acc)      over blocks in order
+//     accm = fma(m_b, pa, accm)               (_1 formats only)
+//     y    = acc (+ accm) (+ bias)
+// so a row's result does not depend on m within a kernel family.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "rw_layout.hpp"
+
+namespace rw {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+// ------------------------------------------------------------ scalar helpers
+
+// IEEE half -> single with the exact bit rules of model.rs:68-86 (NaN payload
+// kept as frac << 13); used where the f32 bits are the product (dequant).
+__device__ inline float h2f_exact(uint32_t h) {
+  uint32_t sign = (h >> 15) & 1u, exp = (h >> 10) & 0x1fu, frac = h & 0x3ffu, bits;
+  if (exp == 0 && frac == 0) {
+    bits = sign << 31;
+  } else if (exp == 0) {
+    uint32_t p = 31u - (uint32_t)__clz(frac);
+    bits = (sign << 31) | ((p + 103u) << 23) | (((frac << (10u - p)) & 0x3ffu) << 13);
+  } else if (exp == 0x1f) {
+    bits = (sign << 31) | 0x7f800000u | (frac << 13);
+  } else {
+    bits = (sign << 31) | ((exp + 112u) << 23) | (frac << 13);
+  }
+  return __uint_as_float(bits);
+}
+
+// hardware conversion: identical to h2f_exact for every non-NaN code
+__device__ inline float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+
+// Rust `(x).round().clamp(-127.0, 127.0) as i32` (NaN -> 0)
+__device__ inline int round_clamp_i8(float v) {
+  float r = roundf(v);
+  if (r != r) return 0;
+  r = r < -127.0f ? -127.0f : r;
+  r = r > 127.0f ? 127.0f : r;
+  return (int)r;
+}
+
+// bytes of a packed-nibble word minus `c` (0 <= byte < 128, c <= byte+128)
+__device__ inline uint32_t sub_bytes(uint32_t x, uint32_t c) {
+  return ((x | 0x80808080u) - c * 0x01010101u) ^ 0x80808080u;
+}
+
+__device__ inline uint32_t rotl(uint32_t x, int t) { return t == 0 ? x : (x << t) | (x >> (32 - t)); }
+
+// --------------------------------------------------------------- k_repack
+
+template <int DT>
+__device__ inline void read_block(const uint8_t *p, uint16_t &d, uint16_t &m, uint32_t &qh, uint8_t *q) {
+  auto u16 = [&](int o) { return (uint16_t)(p[o] | (p[o + 1] << 8)); };
+  auto u32 = [&](int o) {
+    return (uint32_t)p[o] | ((uint32_t)p[o + 1] << 8) | ((uint32_t)p[o + 2] << 16) | ((uint32_t)p[o + 3] << 24);
+  };
+  d = u16(0);
+  m = 0;
+  qh = 0;
+  int qo;
+  if (DT == 2) {
+    qo = 2;
+  } else if (DT == 3) {
+    m = u16(2);
+    qo = 4;
+  } else if (DT == 6) {
+    qh = u32(2);
+    qo = 6;
+  } else if (DT == 7) {
+    m = u16(2);
+    qh = u32(4);
+    qo = 8;
+  } else {
+    qo = 2;
+  }
+  const int nq = DT == 8 ? 32 : 16;
+  for (int i = 0; i < nq; ++i) q[i] = p[qo + i];
+}
+
+// one thread per (row, block) of the padded matrix
+template <int DT>
+__global__ __launch_bounds__(256) void k_repack(const uint8_t *__restrict__ raw, int n, int nb, uint8_t *qs,
+                                                uint32_t *qh, uint16_t *dd, uint16_t *mm, int nb_pad, int noct,
+                                                int ngroups) {
+  constexpr int BB = DT == 2 ? 18 : DT == 3 ? 20 : DT == 6 ? 22 : DT == 7 ? 24 : 34;
+  constexpr int QSB = DT == 8 ? 32 : 16;
+  size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t total = (size_t)ngroups * RG * nb_pad;
+  if (t >= total) return;
+  int bl = (int)(t % nb_pad);
+  int j = (int)(t / nb_pad);
+  uint16_t d = 0, m = 0;
+  uint32_t h = 0;
+  uint8_t q[32];
+  for (int i = 0; i < 32; ++i) q[i] = 0;
+  if (j < n && bl < nb) read_block<DT>(raw + ((size_t)j * nb + bl) * BB, d, m, h, q);
+  WeightView w{nullptr, nullptr, nullptr, nullptr, nb, nb_pad, noct, ngroups};
+  int g = j / RG, r = j % RG;
+  uint8_t *dst = qs + qs_slot(w, g, bl, r) * QSB;
+  if (DT == 8) {
+    for (int p = 0; p < 32; ++p) dst[p] = q[mfma_pos(p)];
+  } else {
+    for (int p = 0; p < 16; ++p) dst[p] = q[p];
+  }
+  size_t si = sc_index(w, g, bl, r);
+  dd[si] = d;
+  if (has_min(DT)) mm[si] = m;
+  if (has_high(DT)) {
+    uint32_t x = 0;
+    for (int e = 0; e < 32; ++e) x |= ((h >> e) & 1u) << qh_bit(e);
+    qh[si] = x;
+  }
+}
+
+// -------------------------------------------------------------- k_dequant
+
+// Element e of block (g, bl, r) as the centered int8 of unpack_block
+// (src/quant.rs:98-131).
+template <int DT>
+__device__ inline int weight_q(const WeightView &w, int g, int bl, int r, int e) {
+  if (DT == 8) return (int)(int8_t)w.qs[qs_slot(w, g, bl, r) * 32 + mfma_pos(e)];
+  uint8_t byte = w.qs[qs_slot(w, g, bl, r) * 16 + (e & 15)];
+  int q = e < 16 ? (byte & 0xf) : (byte >> 4);
+  if (has_high(DT)) q |= (int)((w.qh[sc_index(w, g, bl, r)] >> qh_bit(e)) & 1u) << 4;
+  if (DT == 2) q -= 8;
+  if (DT == 6) q -= 16;
+  return q;
+}
+
+// one thread per (row, block); x = d*q (exact) + m, one rounding
+template <int DT>
+__global__ __launch_bounds__(256) void k_dequant(WeightView w, int row0, int nrows, float *__restrict__ out) {
+  size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (size_t)nrows * w.nb) return;
+  int bl = (int)(t % w.nb);
+  int j = row0 + (int)(t / w.nb);
+  int g = j / RG, r = j % RG;
+  size_t si = sc_index(w, g, bl, r);
+  float d = h2f_exact(w.d[si]);
+  float m = has_min(DT) ? h2f_exact(w.m[si]) : 0.0f;
+  float *o = out + (size_t)(j - row0) * ((size_t)w.nb * QK) + (size_t)bl * QK;
+  for (int e = 0; e < QK; ++e) o[e] = __fadd_rn(__fmul_rn(d, (float)weight_q<DT>(w, g, bl, r, e)), m);
+}
+
+// ------------------------------------------------------------- k_quantize
+
+// 8 lanes per (row, block), 4 elements per lane; a wavefront covers 8
+// consecutive rows of one row group for one block.  Padded rows (i >= m)
+// are written as zeros.
+__global__ __launch_bounds__(256) void k_quantize(const float *__restrict__ a, int m, int k, int nb, int mgroups,
+                                                  int8_t *__restrict__ qa, float *__restrict__ da,
+                                                  float *__restrict__ pa, int32_t *__restrict__ sa) {
+  size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t rb = t >> 3;
+  int lt = (int)(t & 7);
+  if (rb >= (size_t)mgroups * RG * nb) return;  // whole wavefronts exit together
+  int r = (int)(rb % RG);
+  size_t gb = rb / RG;
+  int bl = (int)(gb % nb);
+  int g = (int)(gb / nb);
+  int i = g * RG + r;
+  float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (i < m) x = *reinterpret_cast<const float4 *>(a + (size_t)i * k + (size_t)bl * QK + 4 * lt);
+  float amax = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  amax = fmaxf(amax, __shfl_xor(amax, 4));
+  float d = __fdiv_rn(amax, 127.0f);
+  float inv = d > 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+  int q0 = round_clamp_i8(__fmul_rn(x.x, inv));
+  int q1 = round_clamp_i8(__fmul_rn(x.y, inv));
+  int q2 = round_clamp_i8(__fmul_rn(x.z, inv));
+  int q3 = round_clamp_i8(__fmul_rn(x.w, inv));
+  int s = q0 + q1 + q2 + q3;
+  s += __shfl_xor(s, 1);
+  s += __shfl_xor(s, 2);
+  s += __shfl_xor(s, 4);
+  uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+                    ((uint32_t)(q3 & 0xff) << 24);
+  size_t slot = act_slot(nb, g, bl, r);
+  *reinterpret_cast<uint32_t *>(qa + slot * QK + mfma_pos(4 * lt)) = packed;
+  if (lt == 0) {
+    da[slot] = d;
+    pa[slot] = __fmul_rn(d, (float)s);
+    sa[slot] = s;
+  }
+}
+
+// --------------------------------------------------- MFMA operand unpack
+
+// The B operand (weights) of one 32x32x32 MFMA for lane half h and row slot
+// r of row group g, block bl; also returns the block's d_b and m_b.
+template <int DT>
+__device__ inline v4i weight_operand(const WeightView &w, int g, int bl, int r, int h, float &db, float &mb) {
+  size_t slot = qs_slot(w, g, bl, r);
+  size_t si = sc_index(w, g, bl, r);
+  db = h2f(w.d[si]);
+  mb = has_min(DT) ? h2f(w.m[si]) : 0.0f;
+  if (DT == 8) return *reinterpret_cast<const v4i *>(w.qs + slot * 32 + 16 * h);
+  uint2 q = *reinterpret_cast<const uint2 *>(w.qs + slot * 16 + 8 * h);
+  uint32_t w0 = q.x & 0x0f0f0f0fu, w1 = q.y & 0x0f0f0f0fu;
+  uint32_t w2 = (q.x >> 4) & 0x0f0f0f0fu, w3 = (q.y >> 4) & 0x0f0f0f0fu;
+  if (has_high(DT)) {
+    uint32_t x = w.qh[si];
+    // natural dwords 2h, 2h+1 (elements 8h..8h+7) and 4+2h, 5+2h (16+8h..)
+    w0 |= rotl(x, 2 * h) & 0x10101010u;
+    w1 |= rotl(x, 2 * h + 1) & 0x10101010u;
+    w2 |= rotl(x, 4 + 2 * h) & 0x10101010u;
+    w3 |= rotl(x, 5 + 2 * h) & 0x10101010u;
+  }
+  if (DT == 2) {
+    w0 = sub_bytes(w0, 8); w1 = sub_bytes(w1, 8); w2 = sub_bytes(w2, 8); w3 = sub_bytes(w3, 8);
+  }
+  if (DT == 6) {
+    w0 = sub_bytes(w0, 16); w1 = sub_bytes(w1, 16); w2 = sub_bytes(w2, 16); w3 = sub_bytes(w3, 16);
+  }
+  v4i b;
+  b.x = (int)w0; b.y = (int)w1; b.z = (int)w2; b.w = (int)w3;
+  return b;
+}
+
+// --------------------------------------------------------- k_block_dots
+
+// S[i, j, bl] for every (i < m, j < n); one 32x32 tile per wavefront.
+template <int DT>
+__global__ __launch_bounds__(64) void k_block_dots(WeightView w, ActView a, int m, int n, int32_t *__restrict__ S) {
+  const int l = threadIdx.x, h = l >> 5, r = l & 31;
+  const int gn = blockIdx.x, gm = blockIdx.y, bl = blockIdx.z;
+  float db, mb;
+  v4i bop = weight_operand<DT>(w, gn, bl, r, h, db, mb);
+  v4i aop = *reinterpret_cast<const v4i *>(a.qa + act_slot(a.nb, gm, bl, r) * QK + 16 * h);
+  v16i zero = {};
+  v16i s = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, zero, 0, 0, 0);
+  int j = gn * RG + r;
+  for (int v = 0; v < 16; ++v) {
+    int i = gm * RG + 8 * (v >> 2) + 4 * h + (v & 3);
+    if (i < m && j < n) S[((size_t)i * n + j) * a.nb + bl] = s[v];
+  }
+}
+
+// ---------------------------------------------------------------- k_gemm
+
+// Workgroup: 4 wavefronts in a 2x2 grid; each wavefront owns TM x TN tiles of
+// 32x32 outputs (activation rows x weight rows).  Per block: one int8 MFMA
+// per tile gives the exact S, then the f32 combine.
+template <int DT, int TM, int TN>
+__global__ __launch_bounds__(256) void k_gemm(WeightView w, ActView a, int m, int n, const float *__restrict__ bias,
+                                              float *__restrict__ out) {
+  const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int h = l >> 5, r = l & 31;
+  const int wm = wv & 1, wn = wv >> 1;
+  int rt[TM], ct[TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) rt[i] = (blockIdx.y * 2 + wm) * TM + i;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) ct[j] = (blockIdx.x * 2 + wn) * TN + j;
+  int rtc[TM], ctc[TN];  // clamped for loads; results of clamped tiles are dropped
+#pragma unroll
+  for (int i = 0; i < TM; ++i) rtc[i] = rt[i] < a.mgroups ? rt[i] : a.mgroups - 1;
+#pragma unroll
+  for (int j = 0; j < TN; ++j) ctc[j] = ct[j] < w.ngroups ? ct[j] : w.ngroups - 1;
+
+  float acc[TM][TN][16];
+  float accm[TM][TN][16];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        acc[i][j][v] = 0.0f;
+        accm[i][j][v] = 0.0f;
+      }
+
+  const v16i zero = {};
+  for (int bl = 0; bl < w.nb; ++bl) {
+    v4i aop[TM];
+    float4 dav[TM][4], pav[TM][4];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      size_t base = act_slot(a.nb, rtc[i], bl, 0);
+      aop[i] = *reinterpret_cast<const v4i *>(a.qa + (base + r) * QK + 16 * h);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        dav[i][q] = *reinterpret_cast<const float4 *>(a.da + base + 8 * q + 4 * h);
+        if (has_min(DT)) pav[i][q] = *reinterpret_cast<const float4 *>(a.pa + base + 8 * q + 4 * h);
+      }
+    }
+    v4i bop[TN];
+    float db[TN], mb[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) bop[j] = weight_operand<DT>(w, ctc[j], bl, r, h, db[j], mb[j]);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        v16i s = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[i], bop[j], zero, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float dq[4] = {dav[i][q].x, dav[i][q].y, dav[i][q].z, dav[i][q].w};
+          const float pq[4] = {pav[i][q].x, pav[i][q].y, pav[i][q].z, pav[i][q].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int v = 4 * q + e;
+            acc[i][j][v] = __builtin_fmaf(dq[e] * db[j], (float)s[v], acc[i][j][v]);
+            if (has_min(DT)) accm[i][j][v] = __builtin_fmaf(mb[j], pq[e], accm[i][j][v]);
+          }
+        }
+      }
+  }
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      if (rt[i] >= a.mgroups || ct[j] >= w.ngroups) continue;
+      const int col = ct[j] * RG + r;
+      if (col >= n) continue;
+      const float b = bias ? bias[col] : 0.0f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = rt[i] * RG + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (row >= m) continue;
+        float y = acc[i][j][v];
+        if (has_min(DT)) y = y + accm[i][j][v];
+        if (bias) y = y + b;
+        out[(size_t)row * n + col] = y;
+      }
+    }
+}
+
+// ---------------------------------------------------------------- k_gemv
+
+// m = MR <= 8 activation rows (all in row group 0 of the activation layout).
+// A workgroup is 4 wavefronts; KS of them share one set of 64 weight rows
+// (two row groups, one row per lane) and split its blocks KS ways by whole
+// octets.  Partial results meet in LDS and are added in wavefront order.
+template <int DT, int MR, int KS>
+__global__ __launch_bounds__(256) void k_gemv(WeightView w, ActView a, int n, const float *__restrict__ bias,
+                                              float *__restrict__ out) {
+  constexpr int SETS = 4 / KS;
+  const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int set = wv / KS, part = wv % KS;
+  const int g_raw = (blockIdx.x * SETS + set) * 2 + (l >> 5);
+  const int g = g_raw < w.ngroups ? g_raw : w.ngroups - 1;
+  const int r = l & 31;
+  const int o0 = (w.noct * part) / KS, o1 = (w.noct * (part + 1)) / KS;
+
+  float acc[MR], accm[MR];
+#pragma unroll
+  for (int i = 0; i < MR; ++i) {
+    acc[i] = 0.0f;
+    accm[i] = 0.0f;
+  }
+
+  for (int o = o0; o < o1; ++o) {
+    const size_t sbase = (((size_t)g * w.noct + o) * RG + r) * OCT;
+    uint4 dv = *reinterpret_cast<const uint4 *>(w.d + sbase);
+    uint4 mv = make_uint4(0, 0, 0, 0);
+    if (has_min(DT)) mv = *reinterpret_cast<const uint4 *>(w.m + sbase);
+    uint4 hv0 = make_uint4(0, 0, 0, 0), hv1 = make_uint4(0, 0, 0, 0);
+    if (has_high(DT)) {
+      hv0 = *reinterpret_cast<const uint4 *>(w.qh + sbase);
+      hv1 = *reinterpret_cast<const uint4 *>(w.qh + sbase + 4);
+    }
+    const uint32_t dw[4] = {dv.x, dv.y, dv.z, dv.w};
+    const uint32_t mw[4] = {mv.x, mv.y, mv.z, mv.w};
+    const uint32_t hw[8] = {hv0.x, hv0.y, hv0.z, hv0.w, hv1.x, hv1.y, hv1.z, hv1.w};
+#pragma unroll
+    for (int b8 = 0; b8 < OCT; ++b8) {
+      const int bl = o * OCT + b8;
+      if (bl >= w.nb) break;
+      const float db = h2f((uint16_t)(dw[b8 >> 1] >> (16 * (b8 & 1))));
+      const float mb = has_min(DT) ? h2f((uint16_t)(mw[b8 >> 1] >> (16 * (b8 & 1)))) : 0.0f;
+      // the block's 32 quants as 8 "natural" dwords: dword t = elements 4t..4t+3
+      uint32_t wd[8];
+      const size_t slot = qs_slot(w, g, bl, r);
+      if (DT == 8) {
+        // stored in MFMA order: dword p holds natural dword nat[p]
+        const uint4 q0 = *reinterpret_cast<const uint4 *>(w.qs + slot * 32);
+        const uint4 q1 = *reinterpret_cast<const uint4 *>(w.qs + slot * 32 + 16);
+        wd[0] = q0.x; wd[1] = q0.y; wd[4] = q0.z; wd[5] = q0.w;
+        wd[2] = q1.x; wd[3] = q1.y; wd[6] = q1.z; wd[7] = q1.w;
+      } else {
+        const uint4 q = *reinterpret_cast<const uint4 *>(w.qs + slot * 16);
+        const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          wd[t] = qq[t] & 0x0f0f0f0fu;
+          wd[t + 4] = (qq[t] >> 4) & 0x0f0f0f0fu;
+        }
+        if (has_high(DT)) {
+          const uint32_t x = hw[b8];
+#pragma unroll
+          for (int t = 0; t < 8; ++t) wd[t] |= rotl(x, t) & 0x10101010u;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < MR; ++i) {
+        const size_t as = act_slot(a.nb, 0, bl, i);
+        const int *ap = reinterpret_cast<const int *>(a.qa + as * QK);
+        // activation dwords are in MFMA order: natural dword t sits at ap[pos]
+        int s = 0;
+        s = __builtin_amdgcn_sdot4((int)wd[0], ap[0], s, false);
+        s = __builtin_amdgcn_sdot4((int)wd[1], ap[1], s, false);
+        s = __builtin_amdgcn_sdot4((int)wd[2], ap[4], s, false);
+        s = __builtin_amdgcn_sdot4((int)wd[3], ap[5], s, false);
+        s = __builtin_amdgcn_sdot4((int)wd[4], ap[2], s, false);
+        s = __builtin_amdgcn_sdot4((int)wd[5], ap[3], s, false);
+        s = __builtin_amdgcn_sdot4((int)wd[6], ap[6], s, false);
+        s = __builtin_amdgcn_sdot4((int)wd[7], ap[7], s, false);
+        // centered formats: sum(q_a*(q-c)) = sum(q_a*q) - c*sum(q_a)
+        if (DT == 2) s -= 8 * a.sa[as];
+        if (DT == 6) s -= 16 * a.sa[as];
+        acc[i] = __builtin_fmaf(a.da[as] * db, (float)s, acc[i]);
+        if (has_min(DT)) accm[i] = __builtin_fmaf(mb, a.pa[as], accm[i]);
+      }
+    }
+  }
+
+  float y[MR];
+#pragma unroll
+  for (int i = 0; i < MR; ++i) y[i] = has_min(DT) ? acc[i] + accm[i] : acc[i];
+
+  const int col = g_raw * RG + r;
+  if (KS == 1) {
+    if (g_raw < w.ngroups && col < n)
+#pragma unroll
+      for (int i = 0; i < MR; ++i) out[(size_t)i * n + col] = bias ? y[i] + bias[col] : y[i];
+    return;
+  }
+  __shared__ float red[4][MR][64];
+#pragma unroll
+  for (int i = 0; i < MR; ++i) red[wv][i][l] = y[i];
+  __syncthreads();
+  if (part == 0 && g_raw < w.ngroups && col < n) {
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+      float t = red[wv][i][l];
+      for (int p = 1; p < KS; ++p) t = t + red[wv + p][i][l];
+      out[(size_t)i * n + col] = bias ? t + bias[col] : t;
+    }
+  }
+}
+
+}  // namespace rw

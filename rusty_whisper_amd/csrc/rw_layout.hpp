@@ -1,0 +1,93 @@
+// rw_layout.hpp -- how quantized weights and quantized activations sit in HBM.
+//
+// Weights ([n, k] ggml matrix, nb = k/32 blocks per row) are repacked once at
+// upload into four planes.  Rows are interleaved in groups of 32 ("row
+// groups"), so the 32 rows of one group are contiguous for a given block:
+// a wavefront reading one block of 32 consecutive rows touches one
+// contiguous span.  Blocks are padded to a multiple of 8 ("octets") so the
+// per-block scalars of 8 blocks are 16/32 contiguous bytes per row.
+//
+//   qs  [ngroups][nb_pad][32 rows][QSB]   QSB = 16 (Q4/Q5: packed nibbles,
+//        byte t = element t | element t+16 << 4, as in ggml) or 32 (Q8_0:
+//        int8 in MFMA order, see below)
+//   qh  [ngroups][noct][32 rows][8 blocks] u32, Q5 only, bit-permuted (below)
+//   d   [ngroups][noct][32 rows][8 blocks] f16 bits (block scale)
+//   m   [ngroups][noct][32 rows][8 blocks] f16 bits (block min, _1 formats)
+//
+// Rows past n and blocks past nb are zero (d = m = 0), so they contribute
+// nothing.
+//
+// MFMA order.  One v_mfma_i32_32x32x32_i8 consumes one 32-element block per
+// operand row: lane l supplies row l%32, and lane half h = l/32 supplies 16
+// of the 32 elements.  Any assignment of elements to (h, byte) works as long
+// as activations and weights use the same one; we use
+//     h = 0: elements 0-7 then 16-23,   h = 1: elements 8-15 then 24-31
+// because that is what 8 packed nibble bytes qs[8h..8h+8) give directly
+// (low nibbles = elements 8h.., high nibbles = elements 16+8h..).  Stored
+// 32-byte blocks (Q8_0 weights, quantized activations) are kept in that order:
+//     position p holds element  p (p<8), p+8 (8<=p<16), p-8 (16<=p<24), p (p>=24)
+// (the map is its own inverse).
+//
+// High bits.  A Q5 block's 32 high bits are stored permuted so that the
+// flag word of "natural dword" t (elements 4t..4t+3, one per byte) is
+// rotl(X, t) & 0x10101010: element 4t+u's bit sits at bit (8u + 4 - t) mod 32
+// of X.  Two VALU ops per 4 elements instead of four.
+//
+// Quantized activations ([m, k] f32 in, quantize_acts_i8 semantics) are
+// written by the quantize kernel in the same row-group form:
+//   qa  [mgroups][nb][32 rows][32 B]  int8, MFMA order
+//   da  [mgroups][nb][32 rows]        f32 block scale d_a
+//   pa  [mgroups][nb][32 rows]        f32 d_a * (float)sum(q_a)  (min term)
+//   sa  [mgroups][nb][32 rows]        i32 sum(q_a)
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+namespace rw {
+
+constexpr int QK = 32;        // elements per block
+constexpr int RG = 32;        // rows per row group
+constexpr int OCT = 8;        // blocks per octet
+
+#if defined(__HIPCC__)
+#define RW_HD __host__ __device__
+#else
+#define RW_HD
+#endif
+
+RW_HD inline int qs_bytes(int dtype) { return dtype == 8 ? 32 : 16; }
+RW_HD inline bool has_min(int dtype) { return dtype == 3 || dtype == 7; }
+RW_HD inline bool has_high(int dtype) { return dtype == 6 || dtype == 7; }
+
+// stored position <-> element of a 32-byte MFMA-order block (an involution)
+RW_HD inline int mfma_pos(int e) { return (e >= 8 && e < 16) ? e + 8 : (e >= 16 && e < 24) ? e - 8 : e; }
+
+// bit of the permuted high-bit word that holds element e = 4t + u
+RW_HD inline int qh_bit(int e) { return (8 * (e & 3) + 4 - (e >> 2)) & 31; }
+
+struct WeightView {
+  const uint8_t *qs;
+  const uint32_t *qh;
+  const uint16_t *d;
+  const uint16_t *m;
+  int nb, nb_pad, noct, ngroups;
+};
+
+struct ActView {
+  const int8_t *qa;
+  const float *da;
+  const float *pa;
+  const int32_t *sa;
+  int nb, mgroups;
+};
+
+// element offsets
+RW_HD inline size_t qs_slot(const WeightView &w, int g, int bl, int r) {
+  return ((size_t)g * w.nb_pad + bl) * RG + r;
+}
+RW_HD inline size_t sc_index(const WeightView &w, int g, int bl, int r) {
+  return (((size_t)g * w.noct + (bl >> 3)) * RG + r) * OCT + (bl & 7);
+}
+RW_HD inline size_t act_slot(int nb, int g, int bl, int r) { return ((size_t)g * nb + bl) * RG + r; }
+
+}  // namespace rw

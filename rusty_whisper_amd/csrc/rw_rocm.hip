@@ -1,0 +1,672 @@
+// rw_rocm.hip -- librw_rocm.so: the C ABI of include/rw_rocm.h over the
+// gfx950 kernels of rw_kernels.hpp.
+//
+// Host-side responsibilities (the parts of src/quant.rs that are not
+// arithmetic):
+//   - argument checks with the reference's failure conditions
+//     (k % 32, inner-dimension mismatch, unknown dtype: src/quant.rs:757-758,
+//     129) reported as status codes + per-thread error text;
+//   - one-time upload + repack of a weight (QTensor::new plus the packed int8
+//     cache, src/quant.rs:553-563, 589-639);
+//   - regime dispatch (src/quant.rs:754-1051 picks tiers by CPU; here m
+//     picks the kernel: m <= 8 -> k_gemv, else k_gemm);
+//   - thread safety: host-pointer calls borrow a (stream, buffers) context
+//     from a per-device pool, so concurrent callers never share buffers.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "rw_kernels.hpp"
+#include "rw_rocm.h"
+
+using namespace rw;
+
+// ------------------------------------------------------------- errors
+
+static thread_local std::string g_err;
+
+static int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                       \
+  do {                                                                                      \
+    hipError_t e_ = (expr);                                                                 \
+    if (e_ != hipSuccess) return fail(RW_EHIP, "%s: %s", #expr, hipGetErrorString(e_));     \
+  } while (0)
+
+#define LAUNCH_TRY(what)                                                                    \
+  do {                                                                                      \
+    hipError_t e_ = hipGetLastError();                                                      \
+    if (e_ != hipSuccess) return fail(RW_EHIP, "launch of %s: %s", what, hipGetErrorString(e_)); \
+  } while (0)
+
+static int bb_of(int dtype) {
+  switch (dtype) {
+    case RW_Q4_0: return 18;
+    case RW_Q4_1: return 20;
+    case RW_Q5_0: return 22;
+    case RW_Q5_1: return 24;
+    case RW_Q8_0: return 34;
+    default: return -1;
+  }
+}
+
+static size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+static size_t cdiv(size_t a, size_t b) { return (a + b - 1) / b; }
+
+// ------------------------------------------------------------ devices
+
+static std::mutex g_dev_mu;
+static std::map<int, bool> g_dev_ok;  // device -> is gfx950
+
+static int check_device(int dev) {
+  std::lock_guard<std::mutex> lk(g_dev_mu);
+  auto it = g_dev_ok.find(dev);
+  if (it == g_dev_ok.end()) {
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, dev) != hipSuccess) return fail(RW_ENODEV, "no HIP device %d", dev);
+    bool ok = strncmp(p.gcnArchName, "gfx950", 6) == 0;
+    it = g_dev_ok.emplace(dev, ok).first;
+    if (!ok) return fail(RW_ENODEV, "device %d is %s, this library is built for gfx950 only", dev, p.gcnArchName);
+  }
+  if (!it->second) return fail(RW_ENODEV, "device %d is not gfx950", dev);
+  return RW_OK;
+}
+
+static int current_device(int *dev) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return fail(RW_ENODEV, "no HIP device visible");
+  HIP_TRY(hipGetDevice(dev));
+  return check_device(*dev);
+}
+
+// ------------------------------------------------------------ weights
+
+struct rw_weight {
+  int dtype, device;
+  size_t n, k;
+  int nb, nb_pad, noct, ngroups;
+  void *base;
+  size_t bytes;
+  WeightView view;
+};
+
+// ------------------------------------------------------ context pool
+
+struct Ctx {
+  int device;
+  hipStream_t stream;
+  void *buf;
+  size_t cap;
+};
+
+static std::mutex g_pool_mu;
+static std::vector<Ctx *> g_pool;
+
+static int ctx_acquire(int device, Ctx **out) {
+  {
+    std::lock_guard<std::mutex> lk(g_pool_mu);
+    for (size_t i = 0; i < g_pool.size(); ++i)
+      if (g_pool[i]->device == device) {
+        *out = g_pool[i];
+        g_pool.erase(g_pool.begin() + i);
+        return RW_OK;
+      }
+  }
+  Ctx *c = new Ctx{device, nullptr, nullptr, 0};
+  hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete c;
+    return fail(RW_EHIP, "hipStreamCreateWithFlags: %s", hipGetErrorString(e));
+  }
+  *out = c;
+  return RW_OK;
+}
+
+static void ctx_release(Ctx *c) {
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  g_pool.push_back(c);
+}
+
+static int ctx_reserve(Ctx *c, size_t bytes) {
+  if (c->cap >= bytes) return RW_OK;
+  if (c->buf) HIP_TRY(hipFree(c->buf));
+  c->buf = nullptr;
+  c->cap = 0;
+  size_t want = align_up(bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes, (size_t)1 << 20);
+  if (hipMalloc(&c->buf, want) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(RW_ENOMEM, "hipMalloc(%zu) for a call workspace failed", want);
+  }
+  c->cap = want;
+  return RW_OK;
+}
+
+struct CtxGuard {
+  Ctx *c = nullptr;
+  ~CtxGuard() {
+    if (c) ctx_release(c);
+  }
+};
+
+// per-(device, stream) workspaces for rw_rocm_matmul_t_q_dev(workspace=NULL)
+static std::mutex g_sws_mu;
+static std::map<std::pair<int, void *>, std::pair<void *, size_t>> g_stream_ws;
+
+static int stream_workspace(int device, void *stream, size_t bytes, void **out) {
+  std::lock_guard<std::mutex> lk(g_sws_mu);
+  auto &slot = g_stream_ws[std::make_pair(device, stream)];
+  if (slot.second < bytes) {
+    if (slot.first) HIP_TRY(hipFree(slot.first));
+    slot.first = nullptr;
+    slot.second = 0;
+    size_t want = align_up(bytes, (size_t)1 << 20);
+    if (hipMalloc(&slot.first, want) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(RW_ENOMEM, "hipMalloc(%zu) for a stream workspace failed", want);
+    }
+    slot.second = want;
+  }
+  *out = slot.first;
+  return RW_OK;
+}
+
+// ----------------------------------------------- activation workspace
+
+struct ActLayout {
+  int nb, mgroups;
+  size_t off_qa, off_da, off_pa, off_sa, bytes;
+};
+
+static ActLayout act_layout(size_t m, size_t k) {
+  ActLayout L;
+  L.nb = (int)(k / QK);
+  L.mgroups = (int)cdiv(m, RG);
+  size_t rows = (size_t)L.mgroups * RG;
+  size_t nsc = rows * L.nb;
+  L.off_qa = 0;
+  L.off_da = align_up(rows * k, 256);
+  L.off_pa = align_up(L.off_da + nsc * 4, 256);
+  L.off_sa = align_up(L.off_pa + nsc * 4, 256);
+  L.bytes = align_up(L.off_sa + nsc * 4, 256);
+  return L;
+}
+
+static ActView act_view(const ActLayout &L, void *ws) {
+  char *b = (char *)ws;
+  return ActView{(const int8_t *)(b + L.off_qa), (const float *)(b + L.off_da), (const float *)(b + L.off_pa),
+                 (const int32_t *)(b + L.off_sa), L.nb, L.mgroups};
+}
+
+// --------------------------------------------------------- launches
+
+static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &L, void *ws, hipStream_t s) {
+  char *b = (char *)ws;
+  size_t threads = (size_t)L.mgroups * RG * L.nb * 8;
+  hipLaunchKernelGGL(k_quantize, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0, s, a, (int)m, (int)k, L.nb,
+                     L.mgroups, (int8_t *)(b + L.off_qa), (float *)(b + L.off_da), (float *)(b + L.off_pa),
+                     (int32_t *)(b + L.off_sa));
+  LAUNCH_TRY("k_quantize");
+  return RW_OK;
+}
+
+// GEMM tiling: each wavefront 1 x 2 tiles of 32x32, workgroup 2x2 wavefronts
+constexpr int GEMM_TM = 1, GEMM_TN = 2;
+
+template <int DT>
+static void launch_gemm_dt(const rw_weight *w, const ActView &av, int m, const float *bias, float *out,
+                           hipStream_t s) {
+  dim3 grid((unsigned)cdiv(w->ngroups, 2 * GEMM_TN), (unsigned)cdiv(av.mgroups, 2 * GEMM_TM));
+  hipLaunchKernelGGL((k_gemm<DT, GEMM_TM, GEMM_TN>), grid, dim3(256), 0, s, w->view, av, m, (int)w->n, bias, out);
+}
+
+// the split of a row's blocks over wavefronts depends on the weight only
+static int gemv_ks(const rw_weight *w) { return w->noct >= 4 ? 4 : w->noct >= 2 ? 2 : 1; }
+
+template <int DT, int MR, int KS>
+static void launch_gemv_ks(const rw_weight *w, const ActView &av, const float *bias, float *out, hipStream_t s) {
+  constexpr int SETS = 4 / KS;
+  dim3 grid((unsigned)cdiv(w->ngroups, 2 * SETS));
+  hipLaunchKernelGGL((k_gemv<DT, MR, KS>), grid, dim3(256), 0, s, w->view, av, (int)w->n, bias, out);
+}
+
+template <int DT, int MR>
+static void launch_gemv_mr(const rw_weight *w, const ActView &av, const float *bias, float *out, hipStream_t s) {
+  switch (gemv_ks(w)) {
+    case 4: launch_gemv_ks<DT, MR, 4>(w, av, bias, out, s); break;
+    case 2: launch_gemv_ks<DT, MR, 2>(w, av, bias, out, s); break;
+    default: launch_gemv_ks<DT, MR, 1>(w, av, bias, out, s); break;
+  }
+}
+
+template <int DT>
+static void launch_gemv_dt(const rw_weight *w, const ActView &av, int m, const float *bias, float *out,
+                           hipStream_t s) {
+  switch (m) {
+    case 1: launch_gemv_mr<DT, 1>(w, av, bias, out, s); break;
+    case 2: launch_gemv_mr<DT, 2>(w, av, bias, out, s); break;
+    case 3: launch_gemv_mr<DT, 3>(w, av, bias, out, s); break;
+    case 4: launch_gemv_mr<DT, 4>(w, av, bias, out, s); break;
+    case 5: launch_gemv_mr<DT, 5>(w, av, bias, out, s); break;
+    case 6: launch_gemv_mr<DT, 6>(w, av, bias, out, s); break;
+    case 7: launch_gemv_mr<DT, 7>(w, av, bias, out, s); break;
+    default: launch_gemv_mr<DT, 8>(w, av, bias, out, s); break;
+  }
+}
+
+#define RW_DISPATCH_DT(dt, FN, ...)                  \
+  switch (dt) {                                      \
+    case RW_Q4_0: FN<RW_Q4_0>(__VA_ARGS__); break;   \
+    case RW_Q4_1: FN<RW_Q4_1>(__VA_ARGS__); break;   \
+    case RW_Q5_0: FN<RW_Q5_0>(__VA_ARGS__); break;   \
+    case RW_Q5_1: FN<RW_Q5_1>(__VA_ARGS__); break;   \
+    default: FN<RW_Q8_0>(__VA_ARGS__); break;        \
+  }
+
+constexpr size_t GEMV_MAX_M = 8;
+
+// the product from an already quantized workspace, on `s`
+static int run_product(const rw_weight *w, size_t m, const float *bias, float *out, const void *ws,
+                       hipStream_t s) {
+  ActLayout L = act_layout(m, w->k);
+  ActView av = act_view(L, (void *)ws);
+  if (m <= GEMV_MAX_M) {
+    RW_DISPATCH_DT(w->dtype, launch_gemv_dt, w, av, (int)m, bias, out, s);
+    LAUNCH_TRY("k_gemv");
+  } else {
+    RW_DISPATCH_DT(w->dtype, launch_gemm_dt, w, av, (int)m, bias, out, s);
+    LAUNCH_TRY("k_gemm");
+  }
+  return RW_OK;
+}
+
+// quantize + product on `s`, all pointers on the device
+static int run_matmul(const rw_weight *w, const float *a, size_t m, const float *bias, float *out, void *ws,
+                      hipStream_t s) {
+  if (m == 0) return RW_OK;
+  ActLayout L = act_layout(m, w->k);
+  int rc = launch_quantize(a, m, w->k, L, ws, s);
+  if (rc) return rc;
+  return run_product(w, m, bias, out, ws, s);
+}
+
+static int check_matmul_args(const rw_weight *w, const void *a, size_t m, size_t k, const void *out) {
+  if (!w) return fail(RW_EINVAL, "weight is NULL");
+  if (k != w->k) return fail(RW_EINVAL, "matmul_t_q inner dims: %zu vs %zu", k, w->k);
+  if (m > 0 && (!a || !out)) return fail(RW_EINVAL, "activation or output pointer is NULL");
+  if (m > (size_t)INT32_MAX / 2) return fail(RW_EINVAL, "m = %zu is too large", m);
+  return RW_OK;
+}
+
+// --------------------------------------------------------------- ABI
+
+extern "C" {
+
+int rw_rocm_version(void) { return 0x000100; }
+
+int rw_rocm_last_error(char *buf, size_t len) {
+  if (buf && len) {
+    size_t c = g_err.size() < len - 1 ? g_err.size() : len - 1;
+    memcpy(buf, g_err.data(), c);
+    buf[c] = 0;
+  }
+  return (int)g_err.size();
+}
+
+int rw_rocm_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  int ok = 0;
+  for (int d = 0; d < n; ++d)
+    if (check_device(d) == RW_OK) ++ok;
+  return ok;
+}
+
+int rw_rocm_init(int device) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    return fail(RW_ENODEV, "no HIP device visible");
+  }
+  if (device < 0 || device >= n) return fail(RW_ENODEV, "device %d out of range (%d visible)", device, n);
+  int rc = check_device(device);
+  if (rc) return rc;
+  HIP_TRY(hipSetDevice(device));
+  return RW_OK;
+}
+
+int rw_rocm_block_bytes(int dtype) {
+  int bb = bb_of(dtype);
+  return bb < 0 ? fail(RW_EINVAL, "unsupported dtype %d", dtype) : bb;
+}
+
+int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, size_t raw_len, rw_weight **out) {
+  if (!out) return fail(RW_EINVAL, "out is NULL");
+  *out = nullptr;
+  int bb = bb_of(dtype);
+  if (bb < 0) return fail(RW_EINVAL, "unsupported dtype %d", dtype);
+  if (k == 0 || k % QK) return fail(RW_EINVAL, "k must be a positive multiple of %d (got %zu)", QK, k);
+  if (n == 0) return fail(RW_EINVAL, "n must be positive");
+  if (k / QK > (size_t)1 << 24 || n > (size_t)1 << 28) return fail(RW_EINVAL, "shape [%zu, %zu] too large", n, k);
+  size_t nb = k / QK;
+  if (raw_len != n * nb * (size_t)bb)
+    return fail(RW_EINVAL, "raw length %zu != n*(k/32)*block_bytes = %zu", raw_len, n * nb * (size_t)bb);
+  if (!raw) return fail(RW_EINVAL, "raw is NULL");
+  int dev;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+
+  rw_weight *w = new rw_weight();
+  w->dtype = dtype;
+  w->device = dev;
+  w->n = n;
+  w->k = k;
+  w->nb = (int)nb;
+  w->nb_pad = (int)align_up(nb, OCT);
+  w->noct = w->nb_pad / OCT;
+  w->ngroups = (int)cdiv(n, RG);
+  size_t rows = (size_t)w->ngroups * RG;
+  size_t nsc = rows * w->nb_pad;
+  size_t qsz = nsc * qs_bytes(dtype);
+  size_t off_qh = align_up(qsz, 256);
+  size_t off_d = align_up(off_qh + (has_high(dtype) ? nsc * 4 : 0), 256);
+  size_t off_m = align_up(off_d + nsc * 2, 256);
+  w->bytes = align_up(off_m + (has_min(dtype) ? nsc * 2 : 0), 256);
+  if (hipMalloc(&w->base, w->bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    delete w;
+    return fail(RW_ENOMEM, "hipMalloc(%zu) for a [%zu, %zu] weight failed", w->bytes, n, k);
+  }
+  char *b = (char *)w->base;
+  w->view = WeightView{(const uint8_t *)b, (const uint32_t *)(b + off_qh), (const uint16_t *)(b + off_d),
+                       (const uint16_t *)(b + off_m), w->nb, w->nb_pad, w->noct, w->ngroups};
+
+  void *tmp = nullptr;
+  hipError_t e = hipMalloc(&tmp, raw_len);
+  if (e == hipSuccess) e = hipMemcpy(tmp, raw, raw_len, hipMemcpyHostToDevice);
+  if (e == hipSuccess) {
+    size_t threads = nsc;
+    dim3 grid((unsigned)cdiv(threads, 256));
+#define RW_REPACK(DT)                                                                                      \
+  hipLaunchKernelGGL(k_repack<DT>, grid, dim3(256), 0, 0, (const uint8_t *)tmp, (int)n, (int)nb, (uint8_t *)b, \
+                     (uint32_t *)(b + off_qh), (uint16_t *)(b + off_d), (uint16_t *)(b + off_m), w->nb_pad,      \
+                     w->noct, w->ngroups)
+    switch (dtype) {
+      case RW_Q4_0: RW_REPACK(RW_Q4_0); break;
+      case RW_Q4_1: RW_REPACK(RW_Q4_1); break;
+      case RW_Q5_0: RW_REPACK(RW_Q5_0); break;
+      case RW_Q5_1: RW_REPACK(RW_Q5_1); break;
+      default: RW_REPACK(RW_Q8_0); break;
+    }
+#undef RW_REPACK
+    e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+  }
+  if (tmp) (void)hipFree(tmp);
+  if (e != hipSuccess) {
+    (void)hipFree(w->base);
+    delete w;
+    return fail(RW_EHIP, "weight upload: %s", hipGetErrorString(e));
+  }
+  *out = w;
+  return RW_OK;
+}
+
+int rw_rocm_weight_free(rw_weight *w) {
+  if (!w) return RW_OK;
+  int prev = -1;
+  (void)hipGetDevice(&prev);
+  (void)hipSetDevice(w->device);
+  hipError_t e = hipFree(w->base);
+  if (prev >= 0) (void)hipSetDevice(prev);
+  delete w;
+  if (e != hipSuccess) return fail(RW_EHIP, "hipFree: %s", hipGetErrorString(e));
+  return RW_OK;
+}
+
+int rw_rocm_weight_info(const rw_weight *w, int *dtype, size_t *n, size_t *k, size_t *device_bytes) {
+  if (!w) return fail(RW_EINVAL, "weight is NULL");
+  if (dtype) *dtype = w->dtype;
+  if (n) *n = w->n;
+  if (k) *k = w->k;
+  if (device_bytes) *device_bytes = w->bytes;
+  return RW_OK;
+}
+
+size_t rw_rocm_matmul_workspace_size(size_t m, size_t k) {
+  if (k == 0 || k % QK || m == 0) return 0;
+  return act_layout(m, k).bytes;
+}
+
+int rw_rocm_matmul_t_q_dev(const rw_weight *w, const float *a, size_t m, size_t k, const float *bias, float *out,
+                           void *workspace, size_t workspace_len, void *stream) {
+  int rc = check_matmul_args(w, a, m, k, out);
+  if (rc) return rc;
+  if (m == 0) return RW_OK;
+  HIP_TRY(hipSetDevice(w->device));
+  size_t need = act_layout(m, k).bytes;
+  void *ws = workspace;
+  if (ws) {
+    if (workspace_len < need) return fail(RW_EINVAL, "workspace of %zu bytes < %zu needed", workspace_len, need);
+  } else {
+    rc = stream_workspace(w->device, stream, need, &ws);
+    if (rc) return rc;
+  }
+  return run_matmul(w, a, m, bias, out, ws, (hipStream_t)stream);
+}
+
+int rw_rocm_quantize_dev(const float *a, size_t m, size_t k, void *workspace, size_t workspace_len,
+                         void *stream) {
+  if (k == 0 || k % QK) return fail(RW_EINVAL, "k must be a positive multiple of %d (got %zu)", QK, k);
+  if (m == 0) return RW_OK;
+  if (!a || !workspace) return fail(RW_EINVAL, "activation or workspace pointer is NULL");
+  if (m > (size_t)INT32_MAX / 2) return fail(RW_EINVAL, "m = %zu is too large", m);
+  ActLayout L = act_layout(m, k);
+  if (workspace_len < L.bytes) return fail(RW_EINVAL, "workspace of %zu bytes < %zu needed", workspace_len, L.bytes);
+  return launch_quantize(a, m, k, L, workspace, (hipStream_t)stream);
+}
+
+int rw_rocm_matmul_prequant_dev(const rw_weight *w, const void *workspace, size_t m, const float *bias,
+                                float *out, void *stream) {
+  if (!w) return fail(RW_EINVAL, "weight is NULL");
+  if (m == 0) return RW_OK;
+  if (!workspace || !out) return fail(RW_EINVAL, "workspace or output pointer is NULL");
+  if (m > (size_t)INT32_MAX / 2) return fail(RW_EINVAL, "m = %zu is too large", m);
+  HIP_TRY(hipSetDevice(w->device));
+  return run_product(w, m, bias, out, workspace, (hipStream_t)stream);
+}
+
+int rw_rocm_matmul_t_q(const rw_weight *w, const float *a, size_t m, size_t k, const float *bias, float *out) {
+  int rc = check_matmul_args(w, a, m, k, out);
+  if (rc) return rc;
+  if (m == 0) return RW_OK;
+  HIP_TRY(hipSetDevice(w->device));
+  CtxGuard g;
+  rc = ctx_acquire(w->device, &g.c);
+  if (rc) return rc;
+  Ctx *c = g.c;
+  ActLayout L = act_layout(m, k);
+  size_t off_a = align_up(L.bytes, 256);
+  size_t off_o = align_up(off_a + m * k * 4, 256);
+  size_t off_b = align_up(off_o + m * w->n * 4, 256);
+  size_t total = align_up(off_b + w->n * 4, 256);
+  rc = ctx_reserve(c, total);
+  if (rc) return rc;
+  char *b = (char *)c->buf;
+  float *da = (float *)(b + off_a), *dout = (float *)(b + off_o), *dbias = bias ? (float *)(b + off_b) : nullptr;
+  HIP_TRY(hipMemcpyAsync(da, a, m * k * 4, hipMemcpyHostToDevice, c->stream));
+  if (bias) HIP_TRY(hipMemcpyAsync(dbias, bias, w->n * 4, hipMemcpyHostToDevice, c->stream));
+  rc = run_matmul(w, da, m, dbias, dout, b, c->stream);
+  if (rc) {
+    (void)hipStreamSynchronize(c->stream);
+    return rc;
+  }
+  HIP_TRY(hipMemcpyAsync(out, dout, m * w->n * 4, hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return RW_OK;
+}
+
+size_t rw_rocm_grouped_workspace_size(const rw_linear *items, size_t count) {
+  size_t best = 0;
+  for (size_t i = 0; items && i < count; ++i)
+    if (items[i].w && items[i].m > 0) {
+      size_t b = act_layout(items[i].m, items[i].w->k).bytes;
+      best += align_up(b, 256);
+    }
+  return best;
+}
+
+int rw_rocm_matmul_grouped_dev(const rw_linear *items, size_t count, void *workspace, size_t workspace_len,
+                               void *stream) {
+  if (count == 0) return RW_OK;
+  if (!items) return fail(RW_EINVAL, "items is NULL");
+  size_t need = rw_rocm_grouped_workspace_size(items, count);
+  for (size_t i = 0; i < count; ++i) {
+    const rw_linear &it = items[i];
+    int rc = check_matmul_args(it.w, it.a, it.m, it.w ? it.w->k : 0, it.out);
+    if (rc) return fail(rc, "item %zu: %s", i, g_err.c_str());
+    if (it.m > GEMV_MAX_M) return fail(RW_EINVAL, "item %zu: m = %zu > %zu", i, it.m, GEMV_MAX_M);
+    if (it.w->device != items[0].w->device) return fail(RW_EINVAL, "item %zu is on another device", i);
+  }
+  HIP_TRY(hipSetDevice(items[0].w->device));
+  void *ws = workspace;
+  if (ws) {
+    if (workspace_len < need) return fail(RW_EINVAL, "workspace of %zu bytes < %zu needed", workspace_len, need);
+  } else {
+    int rc = stream_workspace(items[0].w->device, stream, need, &ws);
+    if (rc) return rc;
+  }
+  char *p = (char *)ws;
+  for (size_t i = 0; i < count; ++i) {
+    const rw_linear &it = items[i];
+    if (it.m == 0) continue;
+    int rc = run_matmul(it.w, it.a, it.m, it.bias, it.out, p, (hipStream_t)stream);
+    if (rc) return fail(rc, "item %zu: %s", i, g_err.c_str());
+    p += align_up(act_layout(it.m, it.w->k).bytes, 256);
+  }
+  return RW_OK;
+}
+
+int rw_rocm_dequant_rows(const rw_weight *w, size_t row0, size_t nrows, float *out) {
+  if (!w) return fail(RW_EINVAL, "weight is NULL");
+  if (row0 > w->n || nrows > w->n - row0)
+    return fail(RW_EINVAL, "rows [%zu, %zu) out of range for %zu rows", row0, row0 + nrows, w->n);
+  if (nrows == 0) return RW_OK;
+  if (!out) return fail(RW_EINVAL, "out is NULL");
+  HIP_TRY(hipSetDevice(w->device));
+  CtxGuard g;
+  int rc = ctx_acquire(w->device, &g.c);
+  if (rc) return rc;
+  size_t bytes = nrows * w->k * 4;
+  rc = ctx_reserve(g.c, bytes);
+  if (rc) return rc;
+  size_t threads = nrows * (size_t)w->nb;
+  dim3 grid((unsigned)cdiv(threads, 256));
+#define RW_DEQ(DT) \
+  hipLaunchKernelGGL(k_dequant<DT>, grid, dim3(256), 0, g.c->stream, w->view, (int)row0, (int)nrows, (float *)g.c->buf)
+  switch (w->dtype) {
+    case RW_Q4_0: RW_DEQ(RW_Q4_0); break;
+    case RW_Q4_1: RW_DEQ(RW_Q4_1); break;
+    case RW_Q5_0: RW_DEQ(RW_Q5_0); break;
+    case RW_Q5_1: RW_DEQ(RW_Q5_1); break;
+    default: RW_DEQ(RW_Q8_0); break;
+  }
+#undef RW_DEQ
+  LAUNCH_TRY("k_dequant");
+  HIP_TRY(hipMemcpyAsync(out, g.c->buf, bytes, hipMemcpyDeviceToHost, g.c->stream));
+  HIP_TRY(hipStreamSynchronize(g.c->stream));
+  return RW_OK;
+}
+
+int rw_rocm_quantize_acts(const float *a, size_t m, size_t k, int8_t *q, float *d, int32_t *sum) {
+  if (k == 0 || k % QK) return fail(RW_EINVAL, "k must be a positive multiple of %d (got %zu)", QK, k);
+  if (m == 0) return RW_OK;
+  if (!a || !q || !d || !sum) return fail(RW_EINVAL, "NULL argument");
+  int dev;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  CtxGuard g;
+  rc = ctx_acquire(dev, &g.c);
+  if (rc) return rc;
+  ActLayout L = act_layout(m, k);
+  size_t off_a = align_up(L.bytes, 256);
+  rc = ctx_reserve(g.c, off_a + m * k * 4);
+  if (rc) return rc;
+  char *b = (char *)g.c->buf;
+  HIP_TRY(hipMemcpyAsync(b + off_a, a, m * k * 4, hipMemcpyHostToDevice, g.c->stream));
+  rc = launch_quantize((const float *)(b + off_a), m, k, L, b, g.c->stream);
+  if (rc) return rc;
+  std::vector<uint8_t> host(L.bytes);
+  HIP_TRY(hipMemcpyAsync(host.data(), b, L.bytes, hipMemcpyDeviceToHost, g.c->stream));
+  HIP_TRY(hipStreamSynchronize(g.c->stream));
+  const int8_t *hq = (const int8_t *)(host.data() + L.off_qa);
+  const float *hd = (const float *)(host.data() + L.off_da);
+  const int32_t *hs = (const int32_t *)(host.data() + L.off_sa);
+  for (size_t i = 0; i < m; ++i)
+    for (int bl = 0; bl < L.nb; ++bl) {
+      size_t slot = act_slot(L.nb, (int)(i / RG), bl, (int)(i % RG));
+      for (int e = 0; e < QK; ++e) q[i * k + (size_t)bl * QK + e] = hq[slot * QK + mfma_pos(e)];
+      d[i * L.nb + bl] = hd[slot];
+      sum[i * L.nb + bl] = hs[slot];
+    }
+  return RW_OK;
+}
+
+int rw_rocm_block_dots(const rw_weight *w, const int8_t *qa, size_t m, int32_t *S) {
+  if (!w) return fail(RW_EINVAL, "weight is NULL");
+  if (m == 0) return RW_OK;
+  if (!qa || !S) return fail(RW_EINVAL, "NULL argument");
+  HIP_TRY(hipSetDevice(w->device));
+  CtxGuard g;
+  int rc = ctx_acquire(w->device, &g.c);
+  if (rc) return rc;
+  ActLayout L = act_layout(m, w->k);
+  size_t sbytes = m * w->n * (size_t)w->nb * 4;
+  size_t off_s = align_up(L.bytes, 256);
+  rc = ctx_reserve(g.c, off_s + sbytes);
+  if (rc) return rc;
+  std::vector<int8_t> host(L.bytes, 0);
+  for (size_t i = 0; i < m; ++i)
+    for (int bl = 0; bl < L.nb; ++bl) {
+      size_t slot = act_slot(L.nb, (int)(i / RG), bl, (int)(i % RG));
+      for (int e = 0; e < QK; ++e) host[slot * QK + mfma_pos(e)] = qa[i * w->k + (size_t)bl * QK + e];
+    }
+  char *b = (char *)g.c->buf;
+  HIP_TRY(hipMemcpyAsync(b, host.data(), L.bytes, hipMemcpyHostToDevice, g.c->stream));
+  ActView av = act_view(L, b);
+  dim3 grid((unsigned)w->ngroups, (unsigned)L.mgroups, (unsigned)w->nb);
+#define RW_BD(DT) \
+  hipLaunchKernelGGL(k_block_dots<DT>, grid, dim3(64), 0, g.c->stream, w->view, av, (int)m, (int)w->n, (int32_t *)(b + off_s))
+  switch (w->dtype) {
+    case RW_Q4_0: RW_BD(RW_Q4_0); break;
+    case RW_Q4_1: RW_BD(RW_Q4_1); break;
+    case RW_Q5_0: RW_BD(RW_Q5_0); break;
+    case RW_Q5_1: RW_BD(RW_Q5_1); break;
+    default: RW_BD(RW_Q8_0); break;
+  }
+#undef RW_BD
+  LAUNCH_TRY("k_block_dots");
+  HIP_TRY(hipMemcpyAsync(S, b + off_s, sbytes, hipMemcpyDeviceToHost, g.c->stream));
+  HIP_TRY(hipStreamSynchronize(g.c->stream));
+  return RW_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,317 @@
+"""GPU parity: librw_rocm.so (through its C ABI) against the oracle.
+
+Bars (written in each test):
+  * dequantized weights: bit-exact with dequant_row_scalar (quant.rs:528-537)
+  * activation quantization q/d/sum: bit-exact with quantize_acts_i8
+    (quant.rs:691-716)
+  * per-block integer sums: bit-exact
+  * f32 outputs: within 1e-3 of the reference CPU path, max error scaled by
+    the reference row's L2 norm; and within a few f32 roundings per block of
+    the exact (float64) combination of the exact integer sums.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from rusty_whisper_amd import _abi as A
+
+from _data import DTYPES, NAMES, activations, random_blocks, rel_row_l2, weights
+
+pytestmark = pytest.mark.gpu
+
+NORTH_STAR_TOL = 1e-3
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    A.init(0)
+
+
+def _abs_terms(a, dtype, raw, n):
+    """sum_bl |d_a d_b S| + |m_b d_a sum_a| in float64: the scale of the f32
+    combine's rounding error for each output."""
+    k = a.shape[1]
+    qa, da, sa = O.quantize_acts(a)
+    S = O.block_dots(dtype, raw, n, k, qa).astype(np.float64)  # [m, n, nb]
+    _, db, mb, _ = O.unpack_rows(dtype, raw, n, k)
+    t = np.abs(da[:, None, :].astype(np.float64) * db[None, :, :] * S)
+    t += np.abs(mb[None, :, :].astype(np.float64) * (da * sa)[:, None, :])
+    return t.sum(axis=2)
+
+
+def _check_exact_combine(got, a, dtype, raw, n, bias=None):
+    exact = O.matmul_exact(a, dtype, raw, n, bias=bias)
+    nb = a.shape[1] // 32
+    scale = _abs_terms(a, dtype, raw, n)
+    if bias is not None:
+        scale = scale + np.abs(bias)[None, :]
+    # one rounding per fma / product / add on the path: (2*nb + 3) half-ulps
+    bound = (2 * nb + 3) * 2.0 ** -24 * scale + 1e-30
+    err = np.abs(got.astype(np.float64) - exact)
+    assert np.all(err <= bound), f"max err/bound {np.max(err / bound):.3g}"
+
+
+# ------------------------------------------------------------ dequant
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: NAMES[d])
+@pytest.mark.parametrize("n,k", [(64, 256), (33, 96), (7, 32), (100, 416)])
+def test_dequant_bit_exact_random_blocks(dtype, n, k):
+    raw = random_blocks(dtype, n * k // 32, seed=1000 + dtype + n)
+    w = A.DeviceWeight(dtype, n, k, raw)
+    got = w.dequant_rows()
+    ref = O.dequant(dtype, raw, n, k)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: NAMES[d])
+def test_dequant_pinned_scales_like_avx2_test(dtype):
+    # quant.rs:1125-1160: 7 random blocks, d = 0x3555, m = 0xb555, bitwise
+    raw = random_blocks(dtype, 7, seed=0x12345678 & 0xFFFF, scale_codes=(0x3555, 0xB555))
+    w = A.DeviceWeight(dtype, 1, 7 * 32, raw)
+    got = w.dequant_rows()
+    ref = O.dequant(dtype, raw, 1, 7 * 32)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: NAMES[d])
+def test_dequant_row_slices(dtype):
+    n, k = 70, 128
+    raw = weights(dtype, n, k, seed=5)
+    w = A.DeviceWeight(dtype, n, k, raw)
+    ref = O.dequant(dtype, raw, n, k)
+    for row0, nrows in [(0, 1), (31, 2), (32, 32), (69, 1), (5, 60)]:
+        got = w.dequant_rows(row0, nrows)
+        assert np.array_equal(got.view(np.uint32), ref[row0:row0 + nrows].view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: NAMES[d])
+def test_dequant_nonfinite_scales(dtype):
+    # inf / NaN scale codes: the reference keeps the NaN payload (model.rs:82);
+    # after d*q+m only NaN-ness and inf values are comparable.
+    codes = np.array([[0x7C00, 0x3C00], [0xFC00, 0x3C00], [0x7E01, 0x3C00], [0x3C00, 0x7C00]], np.uint16)
+    raws = [random_blocks(dtype, 1, seed=7 + i, scale_codes=tuple(c)) for i, c in enumerate(codes)]
+    raw = np.concatenate(raws)
+    w = A.DeviceWeight(dtype, 4, 32, raw)
+    got = w.dequant_rows()
+    ref = O.dequant(dtype, raw, 4, 32)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    fin = ~np.isnan(ref)
+    assert np.array_equal(got[fin].view(np.uint32), ref[fin].view(np.uint32))
+
+
+# ----------------------------------------------------- quantize_acts
+
+
+def _edge_activation_rows(k):
+    rows = []
+    z = np.zeros(k, np.float32)
+    rows.append(z)  # d = 0 -> inv = 0 -> q = 0
+    h = np.zeros(k, np.float32)
+    h[:4] = [127.0, 0.5, -0.5, 1.5]  # amax 127 -> d = 1: exact halves round away from 0
+    rows.append(h)
+    e = np.zeros(k, np.float32)
+    e[0], e[1] = 3.0, -3.0  # +-amax -> +-127
+    rows.append(e)
+    t = np.full(k, 1e-38, np.float32)  # d subnormal, 1/d overflows to inf
+    t[1] = -2e-39
+    rows.append(t)
+    s = np.full(k, 3e-45, np.float32)  # subnormal inputs
+    rows.append(s)
+    n = np.ones(k, np.float32)
+    n[3] = np.nan  # NaN ignored by the amax fold, quantizes to 0
+    rows.append(n)
+    i = np.ones(k, np.float32)
+    i[5] = np.inf  # amax = inf -> inv = 0 -> q = 0 (inf*0 = NaN -> 0)
+    rows.append(i)
+    b = np.full(k, 3.4e38, np.float32)
+    b[2] = -3.4e38
+    rows.append(b)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("m,k", [(37, 96), (1, 32), (64, 384), (70, 1280)])
+def test_quantize_acts_bit_exact(m, k):
+    a = activations(m, k, seed=m * 7 + k, outliers=0.01)
+    edge = _edge_activation_rows(k)
+    a = np.concatenate([a, edge])
+    with np.errstate(all="ignore"):
+        q0, d0, s0 = O.quantize_acts(a)
+    q1, d1, s1 = A.quantize_acts(a)
+    assert np.array_equal(q0, q1)
+    assert np.array_equal(d0.view(np.uint32), d1.view(np.uint32))
+    assert np.array_equal(s0, s1)
+
+
+def test_quantize_acts_reference_seed():
+    # the activations of quant.rs:1214-1231 (LCG seed 41, [1500, 384])
+    a = O.test_matrix(1, 1500 * 384, 41).reshape(1500, 384)
+    q0, d0, s0 = O.quantize_acts(a)
+    q1, d1, s1 = A.quantize_acts(a)
+    assert np.array_equal(q0, q1) and np.array_equal(s0, s1)
+    assert np.array_equal(d0.view(np.uint32), d1.view(np.uint32))
+
+
+# --------------------------------------------------------- block dots
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: NAMES[d])
+@pytest.mark.parametrize("m,n,k", [(37, 41, 96), (64, 64, 256), (5, 70, 160), (33, 1, 32)])
+def test_block_dots_exact(dtype, m, n, k):
+    raw = random_blocks(dtype, n * k // 32, seed=17 + dtype * 3 + m)
+    rng = np.random.default_rng(m + n + k)
+    qa = rng.integers(-128, 128, size=(m, k), dtype=np.int8)  # full int8 range
+    got = A.DeviceWeight(dtype, n, k, raw).block_dots(qa)
+    ref = O.block_dots(dtype, raw, n, k, qa)
+    assert np.array_equal(got, ref)
+
+
+# ------------------------------------------------------------- matmul
+
+SHAPES = [
+    (7, 96, 33),      # quant.rs:1189
+    (37, 96, 41),     # quant.rs:1238
+    (1, 384, 1536),   # decode, one row
+    (5, 1280, 1280),  # decode, beam 5
+    (8, 96, 64),      # largest GEMV m
+    (9, 96, 64),      # smallest GEMM m
+    (64, 128, 96),
+    (65, 160, 70),
+    (200, 416, 130),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: NAMES[d])
+@pytest.mark.parametrize("m,k,n", SHAPES, ids=lambda s: str(s))
+def test_matmul_parity(dtype, m, k, n):
+    a = activations(m, k, seed=m * 131 + k)
+    raw = weights(dtype, n, k, seed=n * 17 + k)
+    bias = np.random.default_rng(3).standard_normal(n).astype(np.float32)
+    w = A.DeviceWeight(dtype, n, k, raw)
+    got = w.matmul(a)
+    ref = O.matmul_emul(a, dtype, raw, n, tier=O.TIER_VNNI)
+    assert rel_row_l2(got, ref) <= NORTH_STAR_TOL
+    _check_exact_combine(got, a, dtype, raw, n)
+    got_b = w.matmul(a, bias)
+    assert np.array_equal(got_b.view(np.uint32), (got + bias[None, :]).view(np.uint32))
+    ref_b = O.matmul_emul(a, dtype, raw, n, bias=bias, tier=O.TIER_AVX2)
+    assert rel_row_l2(got_b, ref_b) <= NORTH_STAR_TOL
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: NAMES[d])
+def test_rows_independent_of_m(dtype):
+    k, n = 160, 100
+    raw = weights(dtype, n, k, seed=11)
+    w = A.DeviceWeight(dtype, n, k, raw)
+    a = activations(150, k, seed=12)
+    big = w.matmul(a)
+    for m in (9, 33, 64, 100):  # GEMM family: bitwise
+        assert np.array_equal(w.matmul(a[:m]).view(np.uint32), big[:m].view(np.uint32))
+    small = w.matmul(a[:8])
+    for m in range(1, 8):  # GEMV family: bitwise
+        assert np.array_equal(w.matmul(a[:m]).view(np.uint32), small[:m].view(np.uint32))
+    # across the two families: same exact sums, f32 order differs
+    assert rel_row_l2(small, big[:8]) <= 1e-6
+
+
+def test_m_zero_is_a_noop():
+    w = A.DeviceWeight(8, 4, 32, weights(8, 4, 32, seed=1))
+    out = w.matmul(np.zeros((0, 32), np.float32))
+    assert out.shape == (0, 4)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: NAMES[d])
+def test_scale_spread_and_outliers(dtype):
+    # per-block weight scales spread over 2 decades, 1% x20 activation channels
+    m, k, n = 96, 1280, 160
+    raw = weights(dtype, n, k, seed=21, spread=True)
+    a = activations(m, k, seed=22, outliers=0.01)
+    got = A.DeviceWeight(dtype, n, k, raw).matmul(a)
+    ref = O.matmul_emul(a, dtype, raw, n)
+    assert rel_row_l2(got, ref) <= NORTH_STAR_TOL
+    _check_exact_combine(got, a, dtype, raw, n)
+
+
+# -------------------------------- the reference's own tests, on the GPU
+
+
+def _dense_check(fast, a, qt_raw, dtype, n, k):
+    reference = O.matmul_t_dense(a, O.dequant(dtype, qt_raw, n, k))
+    rms_ref = float(np.sqrt(np.mean(reference.astype(np.float32) ** 2, dtype=np.float32)))
+    assert np.all(np.abs(fast - reference) < 0.05 * max(rms_ref, 1.0))
+
+
+def test_matmul_t_q_matches_dense_within_quant_error():
+    # quant.rs:1187-1206
+    m, k, n = 7, 96, 33
+    a = O.test_matrix(1, m * k, 11).reshape(m, k)
+    raw = O.quantize(8, O.test_matrix(n, k, 13))
+    _dense_check(A.DeviceWeight(8, n, k, raw).matmul(a), a, raw, 8, n, k)
+
+
+def test_matmul_t_q_real_encoder_shape_q5_1():
+    # quant.rs:1213-1232: the tiny-encoder fc1 shape, LCG seeds 41 / 43
+    m, k, n = 1500, 384, 1536
+    a = O.test_matrix(1, m * k, 41).reshape(m, k)
+    raw = O.quantize(7, O.test_matrix(n, k, 43))
+    got = A.DeviceWeight(7, n, k, raw).matmul(a)
+    _dense_check(got, a, raw, 7, n, k)
+    ref = O.matmul_emul(a, 7, raw, n)
+    assert rel_row_l2(got, ref) <= NORTH_STAR_TOL
+
+
+@pytest.mark.parametrize("dtype,sa,sb", [(8, 17, 19), (7, 23, 29)], ids=["Q8_0", "Q5_1"])
+def test_matmul_t_q_odd_shape_matches_dense(dtype, sa, sb):
+    # quant.rs:1236-1278
+    m, k, n = 37, 96, 41
+    a = O.test_matrix(1, m * k, sa).reshape(m, k)
+    raw = O.quantize(dtype, O.test_matrix(n, k, sb))
+    _dense_check(A.DeviceWeight(dtype, n, k, raw).matmul(a), a, raw, dtype, n, k)
+
+
+def test_matmul_t_q_parallel_q5_1():
+    # quant.rs:1282-1301
+    m, k, n = 600, 128, 600
+    a = O.test_matrix(1, m * k, 31).reshape(m, k)
+    raw = O.quantize(7, O.test_matrix(n, k, 37))
+    _dense_check(A.DeviceWeight(7, n, k, raw).matmul(a), a, raw, 7, n, k)
+
+
+def test_matmul_t_q_repeated_calls_same_tensor_stay_correct():
+    # quant.rs:1311-1331: one resident weight, m = 1..5, fresh activations
+    k, n = 96, 41
+    raw = O.quantize(7, O.test_matrix(n, k, 29))
+    w = A.DeviceWeight(7, n, k, raw)
+    for call in range(5):
+        m = 1 + call
+        a = O.test_matrix(1, m * k, 100 + call).reshape(m, k)
+        _dense_check(w.matmul(a), a, raw, 7, n, k)
+
+
+def test_int8_gemm_matches_scalar_reference():
+    # quant.rs:1336-1370: against an independent scalar int8 computation,
+    # 1e-3 * max(|acc|, 1)
+    m, k, n = 5, 128, 20
+    a = O.test_matrix(1, m * k, 41).reshape(m, k)
+    raw = O.quantize(8, O.test_matrix(n, k, 43))
+    fast = A.DeviceWeight(8, n, k, raw).matmul(a)
+    qa, da, _ = O.quantize_acts(a)
+    S = O.block_dots(8, raw, n, k, qa)
+    _, db, _, _ = O.unpack_rows(8, raw, n, k)
+    for i in range(m):
+        for j in range(n):
+            acc = np.float32(0.0)
+            for bl in range(k // 32):
+                acc = np.float32(acc + np.float32(da[i, bl] * db[j, bl]) * np.float32(S[i, j, bl]))
+            assert abs(fast[i, j] - acc) < 1e-3 * max(abs(acc), 1.0)
+
+
+def test_matmul_t_q_parallel_matches_serial():
+    # quant.rs:1372-1384: row 0 of an m = 8 call is bitwise the m = 1 result
+    m, k, n = 8, 128, 1200
+    a = O.test_matrix(1, m * k, 21).reshape(m, k)
+    raw = O.quantize(8, O.test_matrix(n, k, 23))
+    w = A.DeviceWeight(8, n, k, raw)
+    par = w.matmul(a)
+    one = w.matmul(a[:1])
+    assert np.array_equal(par[0].view(np.uint32), one[0].view(np.uint32))
