@@ -26,6 +26,10 @@ namespace rw {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 // ------------------------------------------------------------ scalar helpers
 
@@ -65,6 +69,28 @@ __device__ inline uint32_t sub_bytes(uint32_t x, uint32_t c) {
 
 __device__ inline uint32_t rotl(uint32_t x, int t) { return t == 0 ? x : (x << t) | (x >> (32 - t)); }
 
+// Exact split of an f32 into bf16 parts by truncation: x = hi + r1,
+// r1 = mid + lo, each difference exact.  Returns the bf16 bit patterns.
+__device__ inline void split3_bf16(float x, uint32_t &hi, uint32_t &mid, uint32_t &lo) {
+  const uint32_t hb = __float_as_uint(x) & 0xffff0000u;
+  const float r1 = __fsub_rn(x, __uint_as_float(hb));
+  const uint32_t mb = __float_as_uint(r1) & 0xffff0000u;
+  const float r2 = __fsub_rn(r1, __uint_as_float(mb));
+  hi = hb >> 16;
+  mid = mb >> 16;
+  lo = __float_as_uint(r2) >> 16;
+}
+
+// f16-exact value (an f16 scale or min widened to f32) as two bf16 parts,
+// packed low half = high part: 8 + 3 significant bits, exact.
+__device__ inline uint32_t split2_bf16_packed(float x) {
+  const uint32_t hb = __float_as_uint(x) & 0xffff0000u;
+  const float r = __fsub_rn(x, __uint_as_float(hb));
+  return (hb >> 16) | (__float_as_uint(r) & 0xffff0000u);
+}
+
+__device__ inline uint32_t pair16(uint32_t v) { return v | (v << 16); }
+
 // --------------------------------------------------------------- k_repack
 
 template <int DT>
@@ -99,8 +125,8 @@ __device__ inline void read_block(const uint8_t *p, uint16_t &d, uint16_t &m, ui
 // one thread per (row, block) of the padded matrix
 template <int DT>
 __global__ __launch_bounds__(256) void k_repack(const uint8_t *__restrict__ raw, int n, int nb, uint8_t *qs,
-                                                uint32_t *qh, uint16_t *dd, uint16_t *mm, int nb_pad, int noct,
-                                                int ngroups) {
+                                                uint32_t *qh, uint16_t *dd, uint16_t *mm, uint32_t *dsp, uint32_t *msp,
+                                                int nb_pad, int noct, int ngroups) {
   constexpr int BB = DT == 2 ? 18 : DT == 3 ? 20 : DT == 6 ? 22 : DT == 7 ? 24 : 34;
   constexpr int QSB = DT == 8 ? 32 : 16;
   size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -124,6 +150,9 @@ __global__ __launch_bounds__(256) void k_repack(const uint8_t *__restrict__ raw,
   size_t si = sc_index(w, g, bl, r);
   dd[si] = d;
   if (has_min(DT)) mm[si] = m;
+  const size_t slot = qs_slot(w, g, bl, r);
+  dsp[slot] = split2_bf16_packed(h2f_exact(d));
+  if (has_min(DT)) msp[slot] = split2_bf16_packed(h2f_exact(m));
   if (has_high(DT)) {
     uint32_t x = 0;
     for (int e = 0; e < 32; ++e) x |= ((h >> e) & 1u) << qh_bit(e);
@@ -168,7 +197,9 @@ __global__ __launch_bounds__(256) void k_dequant(WeightView w, int row0, int nro
 // are written as zeros.
 __global__ __launch_bounds__(256) void k_quantize(const float *__restrict__ a, int m, int k, int nb, int mgroups,
                                                   int8_t *__restrict__ qa, float *__restrict__ da,
-                                                  float *__restrict__ pa, int32_t *__restrict__ sa) {
+                                                  float *__restrict__ pa, int32_t *__restrict__ sa,
+                                                  uint16_t *__restrict__ qh16, uint32_t *__restrict__ ds16,
+                                                  uint32_t *__restrict__ pm16) {
   size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   size_t rb = t >> 3;
   int lt = (int)(t & 7);
@@ -198,10 +229,23 @@ __global__ __launch_bounds__(256) void k_quantize(const float *__restrict__ a, i
                     ((uint32_t)(q3 & 0xff) << 24);
   size_t slot = act_slot(nb, g, bl, r);
   *reinterpret_cast<uint32_t *>(qa + slot * QK + mfma_pos(4 * lt)) = packed;
+  if (qh16) {
+    h2v lo2 = {(_Float16)q0, (_Float16)q1}, hi2 = {(_Float16)q2, (_Float16)q3};
+    uint2 hv = make_uint2(__builtin_bit_cast(uint32_t, lo2), __builtin_bit_cast(uint32_t, hi2));
+    *reinterpret_cast<uint2 *>(qh16 + slot * QK + mfma_pos(4 * lt)) = hv;
+  }
   if (lt == 0) {
+    const float p = __fmul_rn(d, (float)s);
     da[slot] = d;
-    pa[slot] = __fmul_rn(d, (float)s);
+    pa[slot] = p;
     sa[slot] = s;
+    if (ds16) {
+      uint32_t hi, mid, lo;
+      split3_bf16(d, hi, mid, lo);
+      *reinterpret_cast<uint4 *>(ds16 + slot * 4) = make_uint4(pair16(hi), pair16(mid), pair16(lo), 0u);
+      split3_bf16(p, hi, mid, lo);
+      *reinterpret_cast<uint4 *>(pm16 + slot * 4) = make_uint4(pair16(hi), pair16(mid), pair16(lo), 0u);
+    }
   }
 }
 
@@ -458,6 +502,166 @@ __global__ __launch_bounds__(256) void k_gemv(WeightView w, ActView a, int n, co
       float t = red[wv][i][l];
       for (int p = 1; p < KS; ++p) t = t + red[wv + p][i][l];
       out[(size_t)i * n + col] = bias ? t + bias[col] : t;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- k_gemm2
+
+// The B operand of the two f16 MFMAs of one block: lane half h, row slot r of
+// row group g.  Items 0-7 (first MFMA) are elements 8h..8h+7, items 8-15
+// (second MFMA) elements 16+8h..16+8h+7 -- the order the activation f16
+// plane uses.  Each byte b becomes the f16 1024 + b (bits 0x6400 | b, one
+// v_perm for two of them) and one packed subtract of 1024 + offset leaves the
+// exact centered quant.
+template <int DT>
+__device__ inline void weight_operand_f16(const WeightView &w, int g, int bl, int r, int h, v8h &b0, v8h &b1) {
+  const size_t slot = qs_slot(w, g, bl, r);
+  uint32_t q[4];
+  if (DT == 8) {
+    const uint4 v = *reinterpret_cast<const uint4 *>(w.qs + slot * 32 + 16 * h);
+    q[0] = v.x ^ 0x80808080u; q[1] = v.y ^ 0x80808080u; q[2] = v.z ^ 0x80808080u; q[3] = v.w ^ 0x80808080u;
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2 *>(w.qs + slot * 16 + 8 * h);
+    q[0] = v.x & 0x0f0f0f0fu;
+    q[1] = v.y & 0x0f0f0f0fu;
+    q[2] = (v.x >> 4) & 0x0f0f0f0fu;
+    q[3] = (v.y >> 4) & 0x0f0f0f0fu;
+    if (has_high(DT)) {
+      const uint32_t x = w.qh[sc_index(w, g, bl, r)];
+      q[0] |= rotl(x, 2 * h) & 0x10101010u;
+      q[1] |= rotl(x, 2 * h + 1) & 0x10101010u;
+      q[2] |= rotl(x, 4 + 2 * h) & 0x10101010u;
+      q[3] |= rotl(x, 5 + 2 * h) & 0x10101010u;
+    }
+  }
+  constexpr float off = DT == 8 ? 1152.0f : DT == 2 ? 1032.0f : DT == 6 ? 1040.0f : 1024.0f;
+  const h2v sub = {(_Float16)(-off), (_Float16)(-off)};
+  h2v e[8];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    e[2 * t] = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, q[t], 0x04010400u)) + sub;
+    e[2 * t + 1] = __builtin_bit_cast(h2v, __builtin_amdgcn_perm(0x64646464u, q[t], 0x04030402u)) + sub;
+  }
+  b0 = (v8h){e[0].x, e[0].y, e[1].x, e[1].y, e[2].x, e[2].y, e[3].x, e[3].y};
+  b1 = (v8h){e[4].x, e[4].y, e[5].x, e[5].y, e[6].x, e[6].y, e[7].x, e[7].y};
+}
+
+__device__ inline v8bf bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  return __builtin_bit_cast(v8bf, make_uint4(a, b, c, d));
+}
+
+// Encoder-shape GEMM (m > 8).  Per 32x32 output tile and block:
+//   S  = two v_mfma_f32_32x32x16_f16 on exact small integers (exact in f32)
+//   s  = one v_mfma_f32_32x32x16_bf16 outer product of the exact bf16
+//        splits of d_a (rows) and d_b (columns): d_a*d_b, rounded once
+//   acc = fma(s, S, acc)                         (the only VALU op)
+// and, for the _1 formats, every two blocks one more bf16 MFMA adds the
+// min term m_b * d_a * sum(q_a) of both blocks into accm.
+// A workgroup is 4 wavefronts: TILES = 4/SK wave tiles side by side along n,
+// each split over SK wavefronts along k (SK depends on k only, so a row's
+// result never depends on m).  A wave tile is TM row groups x 1 column group.
+// Partials meet in LDS and are added in k order; y = sum(acc + accm) + bias.
+template <int DT, int TM, int SK>
+__global__ __launch_bounds__(256) void k_gemm2(WeightView w, GemmPlanes gp, ActView a, int m, int n,
+                                               const float *__restrict__ bias, float *__restrict__ out) {
+  constexpr int TILES = 4 / SK;
+  const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int h = l >> 5, r = l & 31;
+  const int tile = wv / SK, part = wv % SK;
+  const int ct_raw = blockIdx.x * TILES + tile;
+  const int ct = ct_raw < w.ngroups ? ct_raw : w.ngroups - 1;
+  int rt[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int t = blockIdx.y * TM + i;
+    rt[i] = t < a.mgroups ? t : a.mgroups - 1;
+  }
+  const int nb = w.nb;
+  const int npairs = (nb + 1) >> 1;
+  const int p0 = (npairs * part) / SK, p1 = (npairs * (part + 1)) / SK;
+
+  v16f acc[TM], accm[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    acc[i] = (v16f){};
+    accm[i] = (v16f){};
+  }
+  const v16f zero = {};
+
+  for (int pr = p0; pr < p1; ++pr) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int bl = 2 * pr + half;
+      if (bl >= nb) break;
+      v8h b0, b1;
+      weight_operand_f16<DT>(w, ct, bl, r, h, b0, b1);
+      const uint32_t dsv = gp.dsp[qs_slot(w, ct, bl, r)];
+      const v8bf bs = bf16x8(dsv, dsv, dsv, 0u);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const size_t as = act_slot(a.nb, rt[i], bl, r);
+        const uint4 qv0 = *reinterpret_cast<const uint4 *>(a.qh16 + as * QK + 16 * h);
+        const uint4 qv1 = *reinterpret_cast<const uint4 *>(a.qh16 + as * QK + 16 * h + 8);
+        uint4 sv = *reinterpret_cast<const uint4 *>(a.ds16 + as * 4);
+        if (h) sv = make_uint4(0u, 0u, 0u, 0u);
+        v16f S = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, qv0), b0, zero, 0, 0, 0);
+        S = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, qv1), b1, S, 0, 0, 0);
+        const v16f sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, sv), bs, zero, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][v] = __builtin_fmaf(sc[v], S[v], acc[i][v]);
+      }
+    }
+    if (has_min(DT)) {
+      // lane half h carries block 2*pr + h of the pair
+      const int bl = 2 * pr + h;
+      const bool ok = bl < nb;
+      const uint32_t msv = ok ? gp.msp[qs_slot(w, ct, bl, r)] : 0u;
+      const v8bf bm = bf16x8(msv, msv, msv, 0u);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        uint4 pv = make_uint4(0u, 0u, 0u, 0u);
+        if (ok) pv = *reinterpret_cast<const uint4 *>(a.pm16 + act_slot(a.nb, rt[i], bl, r) * 4);
+        accm[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, pv), bm, accm[i], 0, 0, 0);
+      }
+    }
+  }
+
+  v16f y[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) y[i] = has_min(DT) ? acc[i] + accm[i] : acc[i];
+
+  if (SK > 1) {
+    __shared__ float red[SK > 1 ? SK - 1 : 1][TILES][TM * 16][64];
+    if (part > 0) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) red[part - 1][tile][i * 16 + v][l] = y[i][v];
+    }
+    __syncthreads();
+    if (part > 0) return;
+#pragma unroll
+    for (int p = 1; p < SK; ++p)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) y[i][v] = y[i][v] + red[p - 1][tile][i * 16 + v][l];
+  }
+
+  if (ct_raw >= w.ngroups) return;
+  const int col = ct_raw * RG + r;
+  if (col >= n) return;
+  const float b = bias ? bias[col] : 0.0f;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int t = blockIdx.y * TM + i;
+    if (t >= a.mgroups) break;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int row = t * RG + 8 * (v >> 2) + 4 * h + (v & 3);
+      if (row >= m) continue;
+      out[(size_t)row * n + col] = bias ? y[i][v] + b : y[i][v];
     }
   }
 }

@@ -33,12 +33,25 @@
 // rotl(X, t) & 0x10101010: element 4t+u's bit sits at bit (8u + 4 - t) mod 32
 // of X.  Two VALU ops per 4 elements instead of four.
 //
+// GEMM scale planes (weights): the f16 d_b and m_b of each block split
+// exactly into two bf16 (8 + 3 significant bits) and packed as one dword
+// (low half = high part), the B operand of the scale / min-term MFMAs:
+//   dsp [ngroups][nb_pad][32 rows]    u32  bf16 pair of d_b
+//   msp [ngroups][nb_pad][32 rows]    u32  bf16 pair of m_b (_1 formats)
+//
 // Quantized activations ([m, k] f32 in, quantize_acts_i8 semantics) are
 // written by the quantize kernel in the same row-group form:
 //   qa  [mgroups][nb][32 rows][32 B]  int8, MFMA order
 //   da  [mgroups][nb][32 rows]        f32 block scale d_a
 //   pa  [mgroups][nb][32 rows]        f32 d_a * (float)sum(q_a)  (min term)
 //   sa  [mgroups][nb][32 rows]        i32 sum(q_a)
+//   qh16 [mgroups][nb][32 rows][32 f16]  q_a as f16 (exact), MFMA order
+//   ds16 [mgroups][nb][32 rows][4 u32]   d_a split exactly into three bf16
+//        (hi, mid, lo: 8 + 8 + 8 bits), packed [hi hi][mid mid][lo lo][0 0]
+//   pm16 [mgroups][nb][32 rows][4 u32]   the same split of pa
+// The d_a and d_b splits meet in one bf16 MFMA whose six nonzero k-slots
+// pair (hi, mid, lo) x (hi, lo): the sum of the six exact products is
+// d_a * d_b before the single f32 rounding.
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
@@ -78,7 +91,15 @@ struct ActView {
   const float *da;
   const float *pa;
   const int32_t *sa;
+  const uint16_t *qh16;
+  const uint32_t *ds16;
+  const uint32_t *pm16;
   int nb, mgroups;
+};
+
+struct GemmPlanes {
+  const uint32_t *dsp;
+  const uint32_t *msp;
 };
 
 // element offsets

@@ -104,6 +104,7 @@ struct rw_weight {
   void *base;
   size_t bytes;
   WeightView view;
+  GemmPlanes gemm;
 };
 
 // ------------------------------------------------------ context pool
@@ -188,29 +189,50 @@ static int stream_workspace(int device, void *stream, size_t bytes, void **out) 
 
 // ----------------------------------------------- activation workspace
 
+// The GEMM-only planes (f16 quants, bf16 splits) are written only when m is
+// in the GEMM regime; the layout depends on (m, k) alone.
+constexpr size_t GEMV_MAX_M = 8;
+
 struct ActLayout {
   int nb, mgroups;
-  size_t off_qa, off_da, off_pa, off_sa, bytes;
+  bool gemm;
+  size_t off_qa, off_da, off_pa, off_sa, off_q16, off_ds16, off_pm16, bytes;
 };
 
 static ActLayout act_layout(size_t m, size_t k) {
   ActLayout L;
   L.nb = (int)(k / QK);
   L.mgroups = (int)cdiv(m, RG);
+  L.gemm = m > GEMV_MAX_M;
   size_t rows = (size_t)L.mgroups * RG;
   size_t nsc = rows * L.nb;
   L.off_qa = 0;
   L.off_da = align_up(rows * k, 256);
   L.off_pa = align_up(L.off_da + nsc * 4, 256);
   L.off_sa = align_up(L.off_pa + nsc * 4, 256);
-  L.bytes = align_up(L.off_sa + nsc * 4, 256);
+  size_t end = align_up(L.off_sa + nsc * 4, 256);
+  L.off_q16 = L.off_ds16 = L.off_pm16 = 0;
+  if (L.gemm) {
+    L.off_q16 = end;
+    L.off_ds16 = align_up(L.off_q16 + rows * k * 2, 256);
+    L.off_pm16 = align_up(L.off_ds16 + nsc * 16, 256);
+    end = align_up(L.off_pm16 + nsc * 16, 256);
+  }
+  L.bytes = end;
   return L;
 }
 
 static ActView act_view(const ActLayout &L, void *ws) {
   char *b = (char *)ws;
-  return ActView{(const int8_t *)(b + L.off_qa), (const float *)(b + L.off_da), (const float *)(b + L.off_pa),
-                 (const int32_t *)(b + L.off_sa), L.nb, L.mgroups};
+  return ActView{(const int8_t *)(b + L.off_qa),
+                 (const float *)(b + L.off_da),
+                 (const float *)(b + L.off_pa),
+                 (const int32_t *)(b + L.off_sa),
+                 L.gemm ? (const uint16_t *)(b + L.off_q16) : nullptr,
+                 L.gemm ? (const uint32_t *)(b + L.off_ds16) : nullptr,
+                 L.gemm ? (const uint32_t *)(b + L.off_pm16) : nullptr,
+                 L.nb,
+                 L.mgroups};
 }
 
 // --------------------------------------------------------- launches
@@ -220,19 +242,35 @@ static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &
   size_t threads = (size_t)L.mgroups * RG * L.nb * 8;
   hipLaunchKernelGGL(k_quantize, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0, s, a, (int)m, (int)k, L.nb,
                      L.mgroups, (int8_t *)(b + L.off_qa), (float *)(b + L.off_da), (float *)(b + L.off_pa),
-                     (int32_t *)(b + L.off_sa));
+                     (int32_t *)(b + L.off_sa), L.gemm ? (uint16_t *)(b + L.off_q16) : nullptr,
+                     L.gemm ? (uint32_t *)(b + L.off_ds16) : nullptr,
+                     L.gemm ? (uint32_t *)(b + L.off_pm16) : nullptr);
   LAUNCH_TRY("k_quantize");
   return RW_OK;
 }
 
-// GEMM tiling: each wavefront 1 x 2 tiles of 32x32, workgroup 2x2 wavefronts
-constexpr int GEMM_TM = 1, GEMM_TN = 2;
+// GEMM tiling: a wave tile is GEMM_TM row groups (32 rows each) of
+// activations against one row group of weights; the k split depends on k only.
+constexpr int GEMM_TM = 2;
+static int gemm_sk(const rw_weight *w) { return w->nb >= 32 ? 4 : w->nb >= 16 ? 2 : 1; }
+
+template <int DT, int SK>
+static void launch_gemm_sk(const rw_weight *w, const ActView &av, int m, const float *bias, float *out,
+                           hipStream_t s) {
+  constexpr int TILES = 4 / SK;
+  dim3 grid((unsigned)cdiv(w->ngroups, TILES), (unsigned)cdiv(av.mgroups, GEMM_TM));
+  hipLaunchKernelGGL((k_gemm2<DT, GEMM_TM, SK>), grid, dim3(256), 0, s, w->view, w->gemm, av, m, (int)w->n, bias,
+                     out);
+}
 
 template <int DT>
 static void launch_gemm_dt(const rw_weight *w, const ActView &av, int m, const float *bias, float *out,
                            hipStream_t s) {
-  dim3 grid((unsigned)cdiv(w->ngroups, 2 * GEMM_TN), (unsigned)cdiv(av.mgroups, 2 * GEMM_TM));
-  hipLaunchKernelGGL((k_gemm<DT, GEMM_TM, GEMM_TN>), grid, dim3(256), 0, s, w->view, av, m, (int)w->n, bias, out);
+  switch (gemm_sk(w)) {
+    case 4: launch_gemm_sk<DT, 4>(w, av, m, bias, out, s); break;
+    case 2: launch_gemm_sk<DT, 2>(w, av, m, bias, out, s); break;
+    default: launch_gemm_sk<DT, 1>(w, av, m, bias, out, s); break;
+  }
 }
 
 // the split of a row's blocks over wavefronts depends on the weight only
@@ -277,8 +315,6 @@ static void launch_gemv_dt(const rw_weight *w, const ActView &av, int m, const f
     case RW_Q5_1: FN<RW_Q5_1>(__VA_ARGS__); break;   \
     default: FN<RW_Q8_0>(__VA_ARGS__); break;        \
   }
-
-constexpr size_t GEMV_MAX_M = 8;
 
 // the product from an already quantized workspace, on `s`
 static int run_product(const rw_weight *w, size_t m, const float *bias, float *out, const void *ws,
@@ -389,7 +425,9 @@ int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, siz
   size_t off_qh = align_up(qsz, 256);
   size_t off_d = align_up(off_qh + (has_high(dtype) ? nsc * 4 : 0), 256);
   size_t off_m = align_up(off_d + nsc * 2, 256);
-  w->bytes = align_up(off_m + (has_min(dtype) ? nsc * 2 : 0), 256);
+  size_t off_dsp = align_up(off_m + (has_min(dtype) ? nsc * 2 : 0), 256);
+  size_t off_msp = align_up(off_dsp + nsc * 4, 256);
+  w->bytes = align_up(off_msp + (has_min(dtype) ? nsc * 4 : 0), 256);
   if (hipMalloc(&w->base, w->bytes) != hipSuccess) {
     (void)hipGetLastError();
     delete w;
@@ -398,6 +436,7 @@ int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, siz
   char *b = (char *)w->base;
   w->view = WeightView{(const uint8_t *)b, (const uint32_t *)(b + off_qh), (const uint16_t *)(b + off_d),
                        (const uint16_t *)(b + off_m), w->nb, w->nb_pad, w->noct, w->ngroups};
+  w->gemm = GemmPlanes{(const uint32_t *)(b + off_dsp), (const uint32_t *)(b + off_msp)};
 
   void *tmp = nullptr;
   hipError_t e = hipMalloc(&tmp, raw_len);
@@ -407,8 +446,8 @@ int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, siz
     dim3 grid((unsigned)cdiv(threads, 256));
 #define RW_REPACK(DT)                                                                                      \
   hipLaunchKernelGGL(k_repack<DT>, grid, dim3(256), 0, 0, (const uint8_t *)tmp, (int)n, (int)nb, (uint8_t *)b, \
-                     (uint32_t *)(b + off_qh), (uint16_t *)(b + off_d), (uint16_t *)(b + off_m), w->nb_pad,      \
-                     w->noct, w->ngroups)
+                     (uint32_t *)(b + off_qh), (uint16_t *)(b + off_d), (uint16_t *)(b + off_m),                \
+                     (uint32_t *)(b + off_dsp), (uint32_t *)(b + off_msp), w->nb_pad, w->noct, w->ngroups)
     switch (dtype) {
       case RW_Q4_0: RW_REPACK(RW_Q4_0); break;
       case RW_Q4_1: RW_REPACK(RW_Q4_1); break;
