@@ -508,33 +508,51 @@ __global__ __launch_bounds__(256) void k_gemv(WeightView w, ActView a, int n, co
 
 // ---------------------------------------------------------------- k_gemm2
 
-// The B operand of the two f16 MFMAs of one block: lane half h, row slot r of
-// row group g.  Items 0-7 (first MFMA) are elements 8h..8h+7, items 8-15
-// (second MFMA) elements 16+8h..16+8h+7 -- the order the activation f16
-// plane uses.  Each byte b becomes the f16 1024 + b (bits 0x6400 | b, one
-// v_perm for two of them) and one packed subtract of 1024 + offset leaves the
+__device__ inline v8bf bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  return __builtin_bit_cast(v8bf, make_uint4(a, b, c, d));
+}
+
+// Raw operands of one block for a wave tile, as loaded from HBM / L2: the
+// f16 activation quants and d_a splits of TM row groups, the packed weight
+// quants, high bits and d_b split of TN row groups.
+template <int TM, int TN>
+struct BlockOps {
+  uint4 qa0[TM], qa1[TM], sa[TM];
+  uint4 qw[TN];  // packed nibbles in .x/.y, or the 16 Q8_0 bytes
+  uint32_t qh[TN], ds[TN];
+};
+
+template <int DT, int TM, int TN>
+__device__ inline void load_block_ops(BlockOps<TM, TN> &o, const WeightView &w, const GemmPlanes &gp,
+                                      const ActView &a, const int (&rt)[TM], const int (&ct)[TN], int bl, int r,
+                                      int h) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const size_t as = act_slot(a.nb, rt[i], bl, r);
+    o.qa0[i] = *reinterpret_cast<const uint4 *>(a.qh16 + as * QK + 16 * h);
+    o.qa1[i] = *reinterpret_cast<const uint4 *>(a.qh16 + as * QK + 16 * h + 8);
+    o.sa[i] = *reinterpret_cast<const uint4 *>(a.ds16 + as * 4);
+  }
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const size_t slot = qs_slot(w, ct[j], bl, r);
+    if (DT == 8) {
+      o.qw[j] = *reinterpret_cast<const uint4 *>(w.qs + slot * 32 + 16 * h);
+    } else {
+      const uint2 v = *reinterpret_cast<const uint2 *>(w.qs + slot * 16 + 8 * h);
+      o.qw[j] = make_uint4(v.x, v.y, 0u, 0u);
+    }
+    o.qh[j] = has_high(DT) ? w.qh[sc_index(w, ct[j], bl, r)] : 0u;
+    o.ds[j] = gp.dsp[slot];
+  }
+}
+
+// Nibble bytes (plus high-bit flags) of one lane's 16 quants -> the two f16
+// B operands.  Each byte b becomes the f16 1024 + b (bits 0x6400 | b, one
+// v_perm per two of them) and one packed subtract of 1024 + offset leaves the
 // exact centered quant.
 template <int DT>
-__device__ inline void weight_operand_f16(const WeightView &w, int g, int bl, int r, int h, v8h &b0, v8h &b1) {
-  const size_t slot = qs_slot(w, g, bl, r);
-  uint32_t q[4];
-  if (DT == 8) {
-    const uint4 v = *reinterpret_cast<const uint4 *>(w.qs + slot * 32 + 16 * h);
-    q[0] = v.x ^ 0x80808080u; q[1] = v.y ^ 0x80808080u; q[2] = v.z ^ 0x80808080u; q[3] = v.w ^ 0x80808080u;
-  } else {
-    const uint2 v = *reinterpret_cast<const uint2 *>(w.qs + slot * 16 + 8 * h);
-    q[0] = v.x & 0x0f0f0f0fu;
-    q[1] = v.y & 0x0f0f0f0fu;
-    q[2] = (v.x >> 4) & 0x0f0f0f0fu;
-    q[3] = (v.y >> 4) & 0x0f0f0f0fu;
-    if (has_high(DT)) {
-      const uint32_t x = w.qh[sc_index(w, g, bl, r)];
-      q[0] |= rotl(x, 2 * h) & 0x10101010u;
-      q[1] |= rotl(x, 2 * h + 1) & 0x10101010u;
-      q[2] |= rotl(x, 4 + 2 * h) & 0x10101010u;
-      q[3] |= rotl(x, 5 + 2 * h) & 0x10101010u;
-    }
-  }
+__device__ inline void quants_to_f16(const uint32_t (&q)[4], v8h &b0, v8h &b1) {
   constexpr float off = DT == 8 ? 1152.0f : DT == 2 ? 1032.0f : DT == 6 ? 1040.0f : 1024.0f;
   const h2v sub = {(_Float16)(-off), (_Float16)(-off)};
   h2v e[8];
@@ -547,8 +565,51 @@ __device__ inline void weight_operand_f16(const WeightView &w, int g, int bl, in
   b1 = (v8h){e[4].x, e[4].y, e[5].x, e[5].y, e[6].x, e[6].y, e[7].x, e[7].y};
 }
 
-__device__ inline v8bf bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-  return __builtin_bit_cast(v8bf, make_uint4(a, b, c, d));
+// The B operand of the two f16 MFMAs of one block for lane half h: items
+// 0-7 (first MFMA) are elements 8h..8h+7, items 8-15 (second MFMA) elements
+// 16+8h..16+8h+7 -- the order of the activation f16 plane.
+template <int DT>
+__device__ inline void weight_f16_from(int h, uint4 qs, uint32_t qhw, v8h &b0, v8h &b1) {
+  uint32_t q[4];
+  if (DT == 8) {
+    q[0] = qs.x ^ 0x80808080u; q[1] = qs.y ^ 0x80808080u; q[2] = qs.z ^ 0x80808080u; q[3] = qs.w ^ 0x80808080u;
+  } else {
+    q[0] = qs.x & 0x0f0f0f0fu;
+    q[1] = qs.y & 0x0f0f0f0fu;
+    q[2] = (qs.x >> 4) & 0x0f0f0f0fu;
+    q[3] = (qs.y >> 4) & 0x0f0f0f0fu;
+    if (has_high(DT)) {
+      q[0] |= rotl(qhw, 2 * h) & 0x10101010u;
+      q[1] |= rotl(qhw, 2 * h + 1) & 0x10101010u;
+      q[2] |= rotl(qhw, 4 + 2 * h) & 0x10101010u;
+      q[3] |= rotl(qhw, 5 + 2 * h) & 0x10101010u;
+    }
+  }
+  quants_to_f16<DT>(q, b0, b1);
+}
+
+// One block of a wave tile: per tile two f16 MFMAs for the exact sums, one
+// bf16 MFMA for the scale outer product, then acc += s * S.  valid == false
+// (a clamped, missing block) zeroes d_b so the block adds nothing.
+template <int DT, int TM, int TN>
+__device__ inline void gemm_block(v16f (&acc)[TM][TN], const BlockOps<TM, TN> &o, int h, bool valid) {
+  const v16f zero = {};
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    v8h wb0, wb1;
+    weight_f16_from<DT>(h, o.qw[j], o.qh[j], wb0, wb1);
+    const uint32_t dsv = valid ? o.ds[j] : 0u;
+    const v8bf bs = bf16x8(dsv, dsv, dsv, 0u);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const uint4 sv = h ? make_uint4(0u, 0u, 0u, 0u) : o.sa[i];
+      v16f S = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, o.qa0[i]), wb0, zero, 0, 0, 0);
+      S = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, o.qa1[i]), wb1, S, 0, 0, 0);
+      const v16f sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, sv), bs, zero, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = __builtin_fmaf(sc[v], S[v], acc[i][j][v]);
+    }
+  }
 }
 
 // Encoder-shape GEMM (m > 8).  Per 32x32 output tile and block:
@@ -556,112 +617,137 @@ __device__ inline v8bf bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
 //   s  = one v_mfma_f32_32x32x16_bf16 outer product of the exact bf16
 //        splits of d_a (rows) and d_b (columns): d_a*d_b, rounded once
 //   acc = fma(s, S, acc)                         (the only VALU op)
-// and, for the _1 formats, every two blocks one more bf16 MFMA adds the
-// min term m_b * d_a * sum(q_a) of both blocks into accm.
-// A workgroup is 4 wavefronts: TILES = 4/SK wave tiles side by side along n,
-// each split over SK wavefronts along k (SK depends on k only, so a row's
-// result never depends on m).  A wave tile is TM row groups x 1 column group.
-// Partials meet in LDS and are added in k order; y = sum(acc + accm) + bias.
-template <int DT, int TM, int SK>
-__global__ __launch_bounds__(256) void k_gemm2(WeightView w, GemmPlanes gp, ActView a, int m, int n,
-                                               const float *__restrict__ bias, float *__restrict__ out) {
+// For the _1 formats one more bf16 MFMA per block pair adds the min term
+// m_b * d_a * sum(q_a) of both blocks (each lane half carries one block of
+// the pair) straight into acc.
+// A wavefront owns TM x TN tiles (TM activation row groups x TN weight row
+// groups), so each operand it loads feeds TN or TM tiles, and it loads block
+// b+1's raw operands while block b computes.  A workgroup is 4 wavefronts:
+// 4/SK wave tiles side by side along n, each split over SK wavefronts along k
+// (SK depends on the weight's shape only, so a row's result never depends on
+// m).  Partials meet in LDS and are added in k order; y = sum of acc + bias.
+template <int DT, int TM, int TN, int SK>
+__global__ __launch_bounds__(256, 2) void k_gemm2(WeightView w, GemmPlanes gp, ActView a, int m, int n,
+                                                  const float *__restrict__ bias, float *__restrict__ out) {
   constexpr int TILES = 4 / SK;
   const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int h = l >> 5, r = l & 31;
   const int tile = wv / SK, part = wv % SK;
-  const int ct_raw = blockIdx.x * TILES + tile;
-  const int ct = ct_raw < w.ngroups ? ct_raw : w.ngroups - 1;
-  int rt[TM];
+  // XCD-aware order: consecutive workgroup ids go to different XCDs (id % 8),
+  // so hand each XCD one contiguous band of the row-major tile order; its L2
+  // then holds one band of activation rows instead of all of them.
+  int bx, by;
+  {
+    const int nx = gridDim.x, total = nx * gridDim.y;
+    const int id = blockIdx.y * nx + blockIdx.x;
+    const int per = total / 8, rem = total % 8, xcd = id % 8, slot = id / 8;
+    const int lin = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+    bx = lin % nx;
+    by = lin / nx;
+  }
+  int ct_raw[TN], ct[TN], rt[TM];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    ct_raw[j] = (bx * TILES + tile) * TN + j;
+    ct[j] = ct_raw[j] < w.ngroups ? ct_raw[j] : w.ngroups - 1;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
-    const int t = blockIdx.y * TM + i;
+    const int t = by * TM + i;
     rt[i] = t < a.mgroups ? t : a.mgroups - 1;
   }
   const int nb = w.nb;
   const int npairs = (nb + 1) >> 1;
   const int p0 = (npairs * part) / SK, p1 = (npairs * (part + 1)) / SK;
+  const int b1 = 2 * p1 < nb ? 2 * p1 : nb;
 
-  v16f acc[TM], accm[TM];
+  v16f acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    acc[i] = (v16f){};
-    accm[i] = (v16f){};
-  }
-  const v16f zero = {};
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = (v16f){};
 
-  for (int pr = p0; pr < p1; ++pr) {
+  if (p0 < p1) {
+    BlockOps<TM, TN> cur;
+    load_block_ops<DT, TM, TN>(cur, w, gp, a, rt, ct, 2 * p0, r, h);
+    for (int pr = p0; pr < p1; ++pr) {
+      // min-term operands of this pair (lane half h carries block 2*pr + h),
+      // issued now and consumed after both blocks; the load is unconditional
+      // (an odd last block re-reads block nb-1 and is zeroed after)
+      const int mbl = 2 * pr + h;
+      const bool mok = mbl < nb;
+      const int mld = mok ? mbl : nb - 1;
+      uint32_t msv[TN];
+      uint4 pv[TM];
+      if (has_min(DT)) {
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const int bl = 2 * pr + half;
-      if (bl >= nb) break;
-      v8h b0, b1;
-      weight_operand_f16<DT>(w, ct, bl, r, h, b0, b1);
-      const uint32_t dsv = gp.dsp[qs_slot(w, ct, bl, r)];
-      const v8bf bs = bf16x8(dsv, dsv, dsv, 0u);
+        for (int j = 0; j < TN; ++j) msv[j] = gp.msp[qs_slot(w, ct[j], mld, r)];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const size_t as = act_slot(a.nb, rt[i], bl, r);
-        const uint4 qv0 = *reinterpret_cast<const uint4 *>(a.qh16 + as * QK + 16 * h);
-        const uint4 qv1 = *reinterpret_cast<const uint4 *>(a.qh16 + as * QK + 16 * h + 8);
-        uint4 sv = *reinterpret_cast<const uint4 *>(a.ds16 + as * 4);
-        if (h) sv = make_uint4(0u, 0u, 0u, 0u);
-        v16f S = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, qv0), b0, zero, 0, 0, 0);
-        S = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, qv1), b1, S, 0, 0, 0);
-        const v16f sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, sv), bs, zero, 0, 0, 0);
+        for (int i = 0; i < TM; ++i)
+          pv[i] = *reinterpret_cast<const uint4 *>(a.pm16 + act_slot(a.nb, rt[i], mld, r) * 4);
+      }
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][v] = __builtin_fmaf(sc[v], S[v], acc[i][v]);
+      for (int half = 0; half < 2; ++half) {
+        const int bl = 2 * pr + half;
+        if (bl >= b1) break;
+        // prefetch the next block (the last one re-loads its own block)
+        BlockOps<TM, TN> nxt;
+        load_block_ops<DT, TM, TN>(nxt, w, gp, a, rt, ct, bl + 1 < b1 ? bl + 1 : bl, r, h);
+        gemm_block<DT, TM, TN>(acc, cur, h, true);
+        cur = nxt;
+      }
+      if (has_min(DT)) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          const uint4 pz = mok ? pv[i] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, pz),
+                                                                bf16x8(msv[j], msv[j], msv[j], 0u), acc[i][j], 0,
+                                                                0, 0);
+        }
       }
     }
-    if (has_min(DT)) {
-      // lane half h carries block 2*pr + h of the pair
-      const int bl = 2 * pr + h;
-      const bool ok = bl < nb;
-      const uint32_t msv = ok ? gp.msp[qs_slot(w, ct, bl, r)] : 0u;
-      const v8bf bm = bf16x8(msv, msv, msv, 0u);
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        uint4 pv = make_uint4(0u, 0u, 0u, 0u);
-        if (ok) pv = *reinterpret_cast<const uint4 *>(a.pm16 + act_slot(a.nb, rt[i], bl, r) * 4);
-        accm[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, pv), bm, accm[i], 0, 0, 0);
-      }
-    }
   }
-
-  v16f y[TM];
-#pragma unroll
-  for (int i = 0; i < TM; ++i) y[i] = has_min(DT) ? acc[i] + accm[i] : acc[i];
 
   if (SK > 1) {
-    __shared__ float red[SK > 1 ? SK - 1 : 1][TILES][TM * 16][64];
+    __shared__ float red[SK > 1 ? SK - 1 : 1][TILES][TM * TN * 16][64];
     if (part > 0) {
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) red[part - 1][tile][i * 16 + v][l] = y[i][v];
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) red[part - 1][tile][(i * TN + j) * 16 + v][l] = acc[i][j][v];
     }
     __syncthreads();
     if (part > 0) return;
-#pragma unroll
+#pragma unroll 1
     for (int p = 1; p < SK; ++p)
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) y[i][v] = y[i][v] + red[p - 1][tile][i * 16 + v][l];
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) acc[i][j][v] = acc[i][j][v] + red[p - 1][tile][(i * TN + j) * 16 + v][l];
   }
 
-  if (ct_raw >= w.ngroups) return;
-  const int col = ct_raw * RG + r;
-  if (col >= n) return;
-  const float b = bias ? bias[col] : 0.0f;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int t = blockIdx.y * TM + i;
-    if (t >= a.mgroups) break;
+  for (int j = 0; j < TN; ++j) {
+    if (ct_raw[j] >= w.ngroups) continue;
+    const int col = ct_raw[j] * RG + r;
+    if (col >= n) continue;
+    const float b = bias ? bias[col] : 0.0f;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int row = t * RG + 8 * (v >> 2) + 4 * h + (v & 3);
-      if (row >= m) continue;
-      out[(size_t)row * n + col] = bias ? y[i][v] + b : y[i][v];
+    for (int i = 0; i < TM; ++i) {
+      const int t = by * TM + i;
+      if (t >= a.mgroups) break;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = t * RG + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (row >= m) continue;
+        out[(size_t)row * n + col] = bias ? acc[i][j][v] + b : acc[i][j][v];
+      }
     }
   }
 }

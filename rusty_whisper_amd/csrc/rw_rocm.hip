@@ -249,18 +249,24 @@ static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &
   return RW_OK;
 }
 
-// GEMM tiling: a wave tile is GEMM_TM row groups (32 rows each) of
-// activations against one row group of weights; the k split depends on k only.
-constexpr int GEMM_TM = 2;
-static int gemm_sk(const rw_weight *w) { return w->nb >= 32 ? 4 : w->nb >= 16 ? 2 : 1; }
+// GEMM tiling: a wave tile is GEMM_TM activation row groups x GEMM_TN weight
+// row groups (32 rows each).  The k split is chosen from the weight's shape
+// alone (never from m): split more when there are few weight rows to spread.
+constexpr int GEMM_TM = 2, GEMM_TN = 2;
+static int gemm_sk(const rw_weight *w) {
+  if (w->nb < 16) return 1;
+  if (w->n <= 2048 && w->nb >= 32) return 4;
+  if (w->n <= 4096) return 2;
+  return 1;
+}
 
 template <int DT, int SK>
 static void launch_gemm_sk(const rw_weight *w, const ActView &av, int m, const float *bias, float *out,
                            hipStream_t s) {
   constexpr int TILES = 4 / SK;
-  dim3 grid((unsigned)cdiv(w->ngroups, TILES), (unsigned)cdiv(av.mgroups, GEMM_TM));
-  hipLaunchKernelGGL((k_gemm2<DT, GEMM_TM, SK>), grid, dim3(256), 0, s, w->view, w->gemm, av, m, (int)w->n, bias,
-                     out);
+  dim3 grid((unsigned)cdiv(w->ngroups, TILES * GEMM_TN), (unsigned)cdiv(av.mgroups, GEMM_TM));
+  hipLaunchKernelGGL((k_gemm2<DT, GEMM_TM, GEMM_TN, SK>), grid, dim3(256), 0, s, w->view, w->gemm, av, m,
+                     (int)w->n, bias, out);
 }
 
 template <int DT>
