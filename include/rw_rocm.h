@@ -131,18 +131,34 @@ typedef struct rw_linear {
     size_t m;
 } rw_linear;
 
-/* Run `count` independent linears in as few launches as their shapes allow
- * (all entries must share m <= 8, the decode-GEMV regime).  Device pointers,
- * asynchronous on `stream`.  Each result is bitwise identical to the same
- * linear run alone through rw_rocm_matmul_t_q_dev.  Replaces a sequence of
- * independent linear_w calls with the same activation row count (the Q/K/V
- * projections of src/decoder.rs:148-158 share x; the cross K/V of every layer
- * at src/decoder.rs:44-53 are independent). */
+/* Run `count` independent linears, each with m <= 8 (the decode-GEMV
+ * regime), in one launch per distinct (dtype, m, k-split); entries with
+ * m == 0 are skipped.  Device pointers, asynchronous on `stream`.  Each
+ * result is bitwise identical to the same linear run alone through
+ * rw_rocm_matmul_t_q_dev.  The launch tables go to `workspace` (>=
+ * rw_rocm_grouped_workspace_size bytes; NULL = a buffer of the library's own
+ * for this stream) through pinned host memory on `stream`.  Replaces a
+ * sequence of independent linear_w calls (src/quant.rs:1054-1063): the
+ * Q/K/V projections of src/decoder.rs:148-158 share x, the cross K/V of
+ * every layer at src/decoder.rs:44-53 are independent. */
 int rw_rocm_matmul_grouped_dev(const rw_linear *items, size_t count, void *workspace,
                                size_t workspace_len, void *stream);
 
 /* Workspace bytes rw_rocm_matmul_grouped_dev needs for these items. */
 size_t rw_rocm_grouped_workspace_size(const rw_linear *items, size_t count);
+
+/* A prepared group: the same launches as rw_rocm_matmul_grouped_dev over
+ * the same items (so bitwise the same results), with the launch tables
+ * uploaded once by rw_rocm_group_create.  rw_rocm_group_run then only
+ * launches, queued on `stream`: no copy, no allocation, no host wait.  For
+ * decode loops whose activation and output buffers stay put from token to
+ * token (src/decoder.rs:148-196 runs the same linears every step); the
+ * pointers in `items` are captured at creation.  Has no reference
+ * counterpart. */
+typedef struct rw_group rw_group;
+int rw_rocm_group_create(const rw_linear *items, size_t count, rw_group **out);
+int rw_rocm_group_run(const rw_group *g, void *stream);
+void rw_rocm_group_free(rw_group *g);
 
 /* Dequantize rows [row0, row0+nrows) of W to f32 into host `out`
  * (nrows*k floats): x = d*q + m exactly as dequant_row_scalar

@@ -7,7 +7,23 @@ Layers:
   quant           the reference's QTensor / Weight / matmul_t_q / linear_w API,
                   via the C++ mirror in host/ (pybind11 module _rw_quant)
 """
-from ._abi import (  # noqa: F401
+
+
+def _one_hip_runtime() -> None:
+    """PyTorch-ROCm wheels carry their own libamdhip64.so.  A process that
+    loads librw_rocm.so (linked against /opt/rocm's libamdhip64.so.7) before
+    torch ends up with two HIP runtimes, and torch then sees no GPU.  When
+    torch is installed it is imported first, so the dynamic linker hands its
+    runtime (same SONAME) to librw_rocm.so and the process holds one."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
+_one_hip_runtime()
+
+from ._abi import (  # noqa: E402,F401
     DTYPES, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, QK, DeviceWeight, RwError, block_bytes, check, device_count,
     init, lib, quantize_acts, workspace_size,
 )

@@ -64,6 +64,9 @@ _SIGNATURES = {
     "rw_rocm_matmul_grouped_dev": (C.c_int, [C.POINTER(rw_linear), C.c_size_t, C.c_void_p, C.c_size_t,
                                              C.c_void_p]),
     "rw_rocm_grouped_workspace_size": (C.c_size_t, [C.POINTER(rw_linear), C.c_size_t]),
+    "rw_rocm_group_create": (C.c_int, [C.POINTER(rw_linear), C.c_size_t, C.POINTER(C.c_void_p)]),
+    "rw_rocm_group_run": (C.c_int, [C.c_void_p, C.c_void_p]),
+    "rw_rocm_group_free": (None, [C.c_void_p]),
     "rw_rocm_dequant_rows": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p]),
     "rw_rocm_quantize_acts": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p,
                                         C.c_void_p]),
@@ -229,3 +232,28 @@ def grouped_workspace_size(arr) -> int:
 
 def matmul_grouped_dev(arr, workspace=None, workspace_len: int = 0, stream: int | None = None) -> None:
     check(lib().rw_rocm_matmul_grouped_dev(arr, len(arr), _ptr(workspace), workspace_len, stream))
+
+
+class Group:
+    """A prepared group of decode-shape linears (rw_rocm_group_create): the
+    launch tables stay on the device and run() only launches."""
+
+    def __init__(self, arr):
+        h = C.c_void_p()
+        check(lib().rw_rocm_group_create(arr, len(arr), C.byref(h)))
+        self.handle = h.value
+        self._arr = arr  # the items' buffers must outlive the group
+
+    def run(self, stream: int | None = None) -> None:
+        check(lib().rw_rocm_group_run(self.handle, stream))
+
+    def free(self) -> None:
+        if self.handle:
+            lib().rw_rocm_group_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

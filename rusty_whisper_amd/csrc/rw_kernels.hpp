@@ -9,8 +9,9 @@
 //   k_block_dots    exact per-block integer sums via int8 MFMA (validation)
 //   k_gemm          encoder shape (m > 8): v_mfma_i32_32x32x32_i8, one MFMA
 //                   per 32x32 output tile per block, f32 combine on the VALU
-//   k_gemv          decoder shape (m <= 8): one lane per weight row,
-//                   v_dot4_i32_i8 against activations held in SGPRs
+//   k_gemv2         decoder shape (m <= 8): any number of linears in one
+//                   launch, activations quantized into LDS, one lane per
+//                   weight row, v_dot4_i32_i8
 //
 // One combine rule for every output element, in every kernel:
 //     acc  = fma(d_a*d_b, float(S), acc)      over blocks in order
@@ -192,6 +193,40 @@ __global__ __launch_bounds__(256) void k_dequant(WeightView w, int row0, int nro
 
 // ------------------------------------------------------------- k_quantize
 
+// quantize_acts_i8 (src/quant.rs:691-716) for one 32-element block held by
+// 8 consecutive lanes, 4 elements each: amax over the block by lane
+// shuffles, d = amax / 127 and inv = 1 / d correctly rounded, q = round half
+// away from zero of x * inv, clamped to +-127 (NaN -> 0), and sum(q).
+struct BlockQuant {
+  int q0, q1, q2, q3, sum;
+  float d;
+};
+
+__device__ inline BlockQuant quantize_block8(float4 x) {
+  float amax = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  amax = fmaxf(amax, __shfl_xor(amax, 4));
+  BlockQuant b;
+  b.d = __fdiv_rn(amax, 127.0f);
+  const float inv = b.d > 0.0f ? __fdiv_rn(1.0f, b.d) : 0.0f;
+  b.q0 = round_clamp_i8(__fmul_rn(x.x, inv));
+  b.q1 = round_clamp_i8(__fmul_rn(x.y, inv));
+  b.q2 = round_clamp_i8(__fmul_rn(x.z, inv));
+  b.q3 = round_clamp_i8(__fmul_rn(x.w, inv));
+  int s = b.q0 + b.q1 + b.q2 + b.q3;
+  s += __shfl_xor(s, 1);
+  s += __shfl_xor(s, 2);
+  s += __shfl_xor(s, 4);
+  b.sum = s;
+  return b;
+}
+
+__device__ inline uint32_t pack_q4(const BlockQuant &b) {
+  return (uint32_t)(b.q0 & 0xff) | ((uint32_t)(b.q1 & 0xff) << 8) | ((uint32_t)(b.q2 & 0xff) << 16) |
+         ((uint32_t)(b.q3 & 0xff) << 24);
+}
+
 // 8 lanes per (row, block), 4 elements per lane; a wavefront covers 8
 // consecutive rows of one row group for one block.  Padded rows (i >= m)
 // are written as zeros.
@@ -211,37 +246,22 @@ __global__ __launch_bounds__(256) void k_quantize(const float *__restrict__ a, i
   int i = g * RG + r;
   float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
   if (i < m) x = *reinterpret_cast<const float4 *>(a + (size_t)i * k + (size_t)bl * QK + 4 * lt);
-  float amax = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
-  amax = fmaxf(amax, __shfl_xor(amax, 1));
-  amax = fmaxf(amax, __shfl_xor(amax, 2));
-  amax = fmaxf(amax, __shfl_xor(amax, 4));
-  float d = __fdiv_rn(amax, 127.0f);
-  float inv = d > 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
-  int q0 = round_clamp_i8(__fmul_rn(x.x, inv));
-  int q1 = round_clamp_i8(__fmul_rn(x.y, inv));
-  int q2 = round_clamp_i8(__fmul_rn(x.z, inv));
-  int q3 = round_clamp_i8(__fmul_rn(x.w, inv));
-  int s = q0 + q1 + q2 + q3;
-  s += __shfl_xor(s, 1);
-  s += __shfl_xor(s, 2);
-  s += __shfl_xor(s, 4);
-  uint32_t packed = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
-                    ((uint32_t)(q3 & 0xff) << 24);
+  const BlockQuant bq = quantize_block8(x);
   size_t slot = act_slot(nb, g, bl, r);
-  *reinterpret_cast<uint32_t *>(qa + slot * QK + mfma_pos(4 * lt)) = packed;
+  *reinterpret_cast<uint32_t *>(qa + slot * QK + mfma_pos(4 * lt)) = pack_q4(bq);
   if (qh16) {
-    h2v lo2 = {(_Float16)q0, (_Float16)q1}, hi2 = {(_Float16)q2, (_Float16)q3};
+    h2v lo2 = {(_Float16)bq.q0, (_Float16)bq.q1}, hi2 = {(_Float16)bq.q2, (_Float16)bq.q3};
     uint2 hv = make_uint2(__builtin_bit_cast(uint32_t, lo2), __builtin_bit_cast(uint32_t, hi2));
     *reinterpret_cast<uint2 *>(qh16 + slot * QK + mfma_pos(4 * lt)) = hv;
   }
   if (lt == 0) {
-    const float p = __fmul_rn(d, (float)s);
-    da[slot] = d;
+    const float p = __fmul_rn(bq.d, (float)bq.sum);
+    da[slot] = bq.d;
     pa[slot] = p;
-    sa[slot] = s;
+    sa[slot] = bq.sum;
     if (ds16) {
       uint32_t hi, mid, lo;
-      split3_bf16(d, hi, mid, lo);
+      split3_bf16(bq.d, hi, mid, lo);
       *reinterpret_cast<uint4 *>(ds16 + slot * 4) = make_uint4(pair16(hi), pair16(mid), pair16(lo), 0u);
       split3_bf16(p, hi, mid, lo);
       *reinterpret_cast<uint4 *>(pm16 + slot * 4) = make_uint4(pair16(hi), pair16(mid), pair16(lo), 0u);
@@ -392,22 +412,110 @@ __global__ __launch_bounds__(256) void k_gemm(WeightView w, ActView a, int m, in
     }
 }
 
-// ---------------------------------------------------------------- k_gemv
+// ---------------------------------------------------------------- k_gemv2
 
-// m = MR <= 8 activation rows (all in row group 0 of the activation layout).
-// A workgroup is 4 wavefronts; KS of them share one set of 64 weight rows
-// (two row groups, one row per lane) and split its blocks KS ways by whole
-// octets.  Partial results meet in LDS and are added in wavefront order.
-template <int DT, int MR, int KS>
-__global__ __launch_bounds__(256) void k_gemv(WeightView w, ActView a, int n, const float *__restrict__ bias,
-                                              float *__restrict__ out) {
-  constexpr int SETS = 4 / KS;
-  const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int set = wv / KS, part = wv % KS;
-  const int g_raw = (blockIdx.x * SETS + set) * 2 + (l >> 5);
+// Loads and stores through pointers read out of a launch table: the
+// compiler cannot tell their address space, and flat accesses also count
+// against the LDS wait counter, so every LDS wait would hold for them.
+// Address space 1 makes them global_load / global_store (vector-memory
+// counter only).  16-byte values go through native vector types, which keep
+// the address space where HIP's vector classes do not.
+#define RW_GLOBAL_AS __attribute__((address_space(1)))
+typedef uint32_t rw_u32x4 __attribute__((ext_vector_type(4)));
+typedef float rw_f32x4 __attribute__((ext_vector_type(4)));
+__device__ inline uint4 ldg_u4(const void *p) {
+  const rw_u32x4 v = *(const rw_u32x4 RW_GLOBAL_AS *)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ inline float4 ldg_f4(const void *p) {
+  const rw_f32x4 v = *(const rw_f32x4 RW_GLOBAL_AS *)p;
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ inline float ldg_f(const void *p) { return *(const float RW_GLOBAL_AS *)p; }
+__device__ inline uint32_t ldg_u32(const void *p) { return *(const uint32_t RW_GLOBAL_AS *)p; }
+__device__ inline int32_t ldg_i32(const void *p) { return *(const int32_t RW_GLOBAL_AS *)p; }
+__device__ inline void stg_f(float *p, float v) { *(float RW_GLOBAL_AS *)(void *)p = v; }
+
+// One linear of a decode-shape launch: out[m, n] = a[m, k] W^T (+ bias).
+struct GemvItem {
+  WeightView w;
+  const float *a;         // f32 activations [m, k] (fused quantization), or
+  const int8_t *qa;       // ... an already quantized workspace (act layout)
+  const float *qda, *qpa;
+  const int32_t *qsa;
+  const float *bias;
+  float *out;
+  int n;
+  int wg0;  // first workgroup of this item in the launch
+  int lks;  // log2 of the number of wavefronts that split a row's octets
+  int pad;
+};
+
+// One octet (8 blocks) of one weight row, as loaded: quants, scales, mins and
+// (Q5) high-bit words.
+template <int DT>
+struct OctRegs {
+  uint4 q[DT == 8 ? 16 : 8];
+  uint4 d, m, h0, h1;
+};
+
+template <int DT>
+__device__ inline void load_oct(const WeightView &w, int g, int r, int o, OctRegs<DT> &x) {
+  const size_t sbase = (((size_t)g * w.noct + o) * RG + r) * OCT;
+  x.d = ldg_u4(w.d + sbase);
+  if (has_min(DT)) x.m = ldg_u4(w.m + sbase);
+  if (has_high(DT)) {
+    x.h0 = ldg_u4(w.qh + sbase);
+    x.h1 = ldg_u4(w.qh + sbase + 4);
+  }
+#pragma unroll
+  for (int b8 = 0; b8 < OCT; ++b8) {
+    const size_t slot = qs_slot(w, g, o * OCT + b8, r);
+    if (DT == 8) {
+      x.q[2 * b8] = ldg_u4(w.qs + slot * 32);
+      x.q[2 * b8 + 1] = ldg_u4(w.qs + slot * 32 + 16);
+    } else {
+      x.q[b8] = ldg_u4(w.qs + slot * 16);
+    }
+  }
+}
+
+// LDS record of one activation block for the decode kernel: MR x 32 int8
+// quants (natural order), MR x {d (f32), c (i32)}, MR x p (f32), padded to
+// 16 bytes.  c = -offset * sum(q) seeds the integer dot of the centered
+// formats (Q4_0: 8, Q5_0: 16) and is 0 otherwise; p = d * sum(q).
+RW_HD constexpr int gemv_rec_bytes(int mr) { return (mr * 44 + 15) & ~15; }
+
+// Decode shape (m = MR <= 8).  One launch covers any number of linears that
+// share (dtype, m); workgroup -> item through `wg_item` (GROUPED), or the
+// single item `one`.  The activation rows are quantized into LDS with the
+// arithmetic of k_quantize (so fused and separate quantization agree bit for
+// bit), `ch_oct` octets of blocks at a time, and weight rows stream past them
+// one per lane through v_dot4_i32_i8, a whole octet of loads in flight per
+// lane and the next octet prefetched.  2^lks of the 4 wavefronts split a
+// row's octets (the split depends on the weight only); each walks its blocks
+// in increasing order whatever the chunking, and the parts meet in LDS in
+// wavefront order: a row's result depends on its weight row and activation
+// row alone.  Blocks past nb in the last octet meet zero weight planes (the
+// upload writes the padding as zeros) and zero activation records: they add
+// exactly +0.
+template <int DT, int MR, bool GROUPED>
+__global__ __launch_bounds__(256) void k_gemv2(const GemvItem *__restrict__ items, const int *__restrict__ wg_item,
+                                               GemvItem one, int ch_oct) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int REC = gemv_rec_bytes(MR), SC = MR * QK, PO = MR * (QK + 8);
+  constexpr int OFF = DT == 2 ? 8 : DT == 6 ? 16 : 0;  // centering offset
+  // the descriptor is wave-uniform: scalar loads from the table or kernarg
+  const GemvItem I = GROUPED ? items[wg_item[blockIdx.x]] : one;
+  const WeightView &w = I.w;
+  const int nb = w.nb;
+  const int lks = I.lks, KS = 1 << lks;
+  const int t = threadIdx.x, l = t & 63, wv = t >> 6;
+  const int set = wv >> lks, part = wv & (KS - 1);
+  const int g_raw = (((int)blockIdx.x - (GROUPED ? I.wg0 : 0)) * (4 >> lks) + set) * 2 + (l >> 5);
   const int g = g_raw < w.ngroups ? g_raw : w.ngroups - 1;
   const int r = l & 31;
-  const int o0 = (w.noct * part) / KS, o1 = (w.noct * (part + 1)) / KS;
+  const int o0 = (w.noct * part) >> lks, o1 = (w.noct * (part + 1)) >> lks;
 
   float acc[MR], accm[MR];
 #pragma unroll
@@ -416,67 +524,120 @@ __global__ __launch_bounds__(256) void k_gemv(WeightView w, ActView a, int n, co
     accm[i] = 0.0f;
   }
 
-  for (int o = o0; o < o1; ++o) {
-    const size_t sbase = (((size_t)g * w.noct + o) * RG + r) * OCT;
-    uint4 dv = *reinterpret_cast<const uint4 *>(w.d + sbase);
-    uint4 mv = make_uint4(0, 0, 0, 0);
-    if (has_min(DT)) mv = *reinterpret_cast<const uint4 *>(w.m + sbase);
-    uint4 hv0 = make_uint4(0, 0, 0, 0), hv1 = make_uint4(0, 0, 0, 0);
-    if (has_high(DT)) {
-      hv0 = *reinterpret_cast<const uint4 *>(w.qh + sbase);
-      hv1 = *reinterpret_cast<const uint4 *>(w.qh + sbase + 4);
-    }
-    const uint32_t dw[4] = {dv.x, dv.y, dv.z, dv.w};
-    const uint32_t mw[4] = {mv.x, mv.y, mv.z, mv.w};
-    const uint32_t hw[8] = {hv0.x, hv0.y, hv0.z, hv0.w, hv1.x, hv1.y, hv1.z, hv1.w};
+  for (int c0 = 0; c0 < w.noct; c0 += ch_oct) {
+    const int c1 = min(w.noct, c0 + ch_oct);
+    const int bb0 = c0 * OCT, cnb = min(nb, c1 * OCT) - bb0;
+    if (c0) __syncthreads();  // every wavefront is done with the previous chunk
+    // --- activation records of blocks [bb0, bb0 + cnb) -> LDS; (row, block)
+    // pairs in row-major order, 4 passes of 32 per batch so their global
+    // loads are in flight together
+    const int total = MR * cnb;
+    if (I.a) {
+      for (int rb0 = 0; rb0 < total; rb0 += 128) {
+        float4 x[4];
 #pragma unroll
-    for (int b8 = 0; b8 < OCT; ++b8) {
-      const int bl = o * OCT + b8;
-      if (bl >= w.nb) break;
-      const float db = h2f((uint16_t)(dw[b8 >> 1] >> (16 * (b8 & 1))));
-      const float mb = has_min(DT) ? h2f((uint16_t)(mw[b8 >> 1] >> (16 * (b8 & 1)))) : 0.0f;
-      // the block's 32 quants as 8 "natural" dwords: dword t = elements 4t..4t+3
-      uint32_t wd[8];
-      const size_t slot = qs_slot(w, g, bl, r);
-      if (DT == 8) {
-        // stored in MFMA order: dword p holds natural dword nat[p]
-        const uint4 q0 = *reinterpret_cast<const uint4 *>(w.qs + slot * 32);
-        const uint4 q1 = *reinterpret_cast<const uint4 *>(w.qs + slot * 32 + 16);
-        wd[0] = q0.x; wd[1] = q0.y; wd[4] = q0.z; wd[5] = q0.w;
-        wd[2] = q1.x; wd[3] = q1.y; wd[6] = q1.z; wd[7] = q1.w;
-      } else {
-        const uint4 q = *reinterpret_cast<const uint4 *>(w.qs + slot * 16);
-        const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          wd[t] = qq[t] & 0x0f0f0f0fu;
-          wd[t + 4] = (qq[t] >> 4) & 0x0f0f0f0fu;
+        for (int u = 0; u < 4; ++u) {
+          const int rb = rb0 + 32 * u + (t >> 3), lt = t & 7;
+          x[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (rb < total) {
+            const int i = rb / cnb, bl = bb0 + rb % cnb;
+            x[u] = ldg_f4(I.a + ((size_t)i * nb + bl) * QK + 4 * lt);
+          }
         }
-        if (has_high(DT)) {
-          const uint32_t x = hw[b8];
 #pragma unroll
-          for (int t = 0; t < 8; ++t) wd[t] |= rotl(x, t) & 0x10101010u;
+        for (int u = 0; u < 4; ++u) {
+          const int rb = rb0 + 32 * u + (t >> 3), lt = t & 7;
+          const BlockQuant bq = quantize_block8(x[u]);
+          if (rb < total) {
+            const int i = rb / cnb, lb = rb % cnb;
+            uint8_t *rec = lds + lb * REC;
+            *reinterpret_cast<uint32_t *>(rec + i * QK + 4 * lt) = pack_q4(bq);
+            if (lt == 0) {
+              *reinterpret_cast<int2 *>(rec + SC + 8 * i) = make_int2(__float_as_int(bq.d), -OFF * bq.sum);
+              *reinterpret_cast<float *>(rec + PO + 4 * i) = __fmul_rn(bq.d, (float)bq.sum);
+            }
+          }
         }
       }
+    } else {
+      // already quantized: row group 0 of the activation layout, MFMA order
+      for (int idx = t; idx < total * 8; idx += 256) {
+        const int rb = idx >> 3, lt = idx & 7;
+        const int i = rb / cnb, lb = rb % cnb;
+        const size_t slot = act_slot(nb, 0, bb0 + lb, i);
+        uint8_t *rec = lds + lb * REC;
+        *reinterpret_cast<uint32_t *>(rec + i * QK + 4 * lt) = ldg_u32(I.qa + slot * QK + mfma_pos(4 * lt));
+        if (lt == 0) {
+          *reinterpret_cast<int2 *>(rec + SC + 8 * i) =
+              make_int2(__float_as_int(ldg_f(I.qda + slot)), -OFF * ldg_i32(I.qsa + slot));
+          *reinterpret_cast<float *>(rec + PO + 4 * i) = ldg_f(I.qpa + slot);
+        }
+      }
+    }
+    // records of the tail blocks of the last octet: zeros
+    const int dead = (c1 - c0) * OCT - cnb;
+    for (int z = t; z < dead * (REC / 16); z += 256)
+      reinterpret_cast<uint4 *>(lds + cnb * REC)[z] = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+
+    // --- weights: one row per lane, this part's octets inside the chunk,
+    // each loaded whole (the planes are padded to whole octets)
+    const int p0 = max(o0, c0), p1 = min(o1, c1);
+    if (p0 < p1) {
+      OctRegs<DT> cur, nxt;
+      load_oct<DT>(w, g, r, p0, cur);
+      for (int o = p0; o < p1; ++o) {
+        load_oct<DT>(w, g, r, o + 1 < p1 ? o + 1 : o, nxt);
+        const uint32_t dw[4] = {cur.d.x, cur.d.y, cur.d.z, cur.d.w};
+        const uint32_t mw[4] = {cur.m.x, cur.m.y, cur.m.z, cur.m.w};
+        const uint32_t hw[8] = {cur.h0.x, cur.h0.y, cur.h0.z, cur.h0.w, cur.h1.x, cur.h1.y, cur.h1.z, cur.h1.w};
+        const uint8_t *orec = lds + (o - c0) * OCT * REC;
 #pragma unroll
-      for (int i = 0; i < MR; ++i) {
-        const size_t as = act_slot(a.nb, 0, bl, i);
-        const int *ap = reinterpret_cast<const int *>(a.qa + as * QK);
-        // activation dwords are in MFMA order: natural dword t sits at ap[pos]
-        int s = 0;
-        s = __builtin_amdgcn_sdot4((int)wd[0], ap[0], s, false);
-        s = __builtin_amdgcn_sdot4((int)wd[1], ap[1], s, false);
-        s = __builtin_amdgcn_sdot4((int)wd[2], ap[4], s, false);
-        s = __builtin_amdgcn_sdot4((int)wd[3], ap[5], s, false);
-        s = __builtin_amdgcn_sdot4((int)wd[4], ap[2], s, false);
-        s = __builtin_amdgcn_sdot4((int)wd[5], ap[3], s, false);
-        s = __builtin_amdgcn_sdot4((int)wd[6], ap[6], s, false);
-        s = __builtin_amdgcn_sdot4((int)wd[7], ap[7], s, false);
-        // centered formats: sum(q_a*(q-c)) = sum(q_a*q) - c*sum(q_a)
-        if (DT == 2) s -= 8 * a.sa[as];
-        if (DT == 6) s -= 16 * a.sa[as];
-        acc[i] = __builtin_fmaf(a.da[as] * db, (float)s, acc[i]);
-        if (has_min(DT)) accm[i] = __builtin_fmaf(mb, a.pa[as], accm[i]);
+        for (int b8 = 0; b8 < OCT; ++b8) {
+          const float db = h2f((uint16_t)(dw[b8 >> 1] >> (16 * (b8 & 1))));
+          const float mb = has_min(DT) ? h2f((uint16_t)(mw[b8 >> 1] >> (16 * (b8 & 1)))) : 0.0f;
+          // the block's 32 quants as 8 natural dwords: dword u = elements 4u..4u+3
+          uint32_t wd[8];
+          if (DT == 8) {
+            // stored in MFMA order: stored dwords 0..7 hold natural dwords 0,1,4,5,2,3,6,7
+            const uint4 q0 = cur.q[2 * b8], q1 = cur.q[2 * b8 + 1];
+            wd[0] = q0.x; wd[1] = q0.y; wd[4] = q0.z; wd[5] = q0.w;
+            wd[2] = q1.x; wd[3] = q1.y; wd[6] = q1.z; wd[7] = q1.w;
+          } else {
+            const uint4 q = cur.q[b8];
+            const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              wd[u] = qq[u] & 0x0f0f0f0fu;
+              wd[u + 4] = (qq[u] >> 4) & 0x0f0f0f0fu;
+            }
+            if (has_high(DT)) {
+              const uint32_t x = hw[b8];
+#pragma unroll
+              for (int u = 0; u < 8; ++u) wd[u] |= rotl(x, u) & 0x10101010u;
+            }
+          }
+          const uint8_t *rec = orec + b8 * REC;
+#pragma unroll
+          for (int i = 0; i < MR; ++i) {
+            const int4 a0 = *reinterpret_cast<const int4 *>(rec + i * QK);
+            const int4 a1 = *reinterpret_cast<const int4 *>(rec + i * QK + 16);
+            const int2 sc = *reinterpret_cast<const int2 *>(rec + SC + 8 * i);
+            // centered formats: sum(q_a*(q-c)) = sum(q_a*q) - c*sum(q_a)
+            int s = sc.y;
+            s = __builtin_amdgcn_sdot4((int)wd[0], a0.x, s, false);
+            s = __builtin_amdgcn_sdot4((int)wd[1], a0.y, s, false);
+            s = __builtin_amdgcn_sdot4((int)wd[2], a0.z, s, false);
+            s = __builtin_amdgcn_sdot4((int)wd[3], a0.w, s, false);
+            s = __builtin_amdgcn_sdot4((int)wd[4], a1.x, s, false);
+            s = __builtin_amdgcn_sdot4((int)wd[5], a1.y, s, false);
+            s = __builtin_amdgcn_sdot4((int)wd[6], a1.z, s, false);
+            s = __builtin_amdgcn_sdot4((int)wd[7], a1.w, s, false);
+            acc[i] = __builtin_fmaf(__int_as_float(sc.x) * db, (float)s, acc[i]);
+            if (has_min(DT)) accm[i] = __builtin_fmaf(mb, *reinterpret_cast<const float *>(rec + PO + 4 * i), accm[i]);
+          }
+        }
+        cur = nxt;
       }
     }
   }
@@ -485,25 +646,34 @@ __global__ __launch_bounds__(256) void k_gemv(WeightView w, ActView a, int n, co
 #pragma unroll
   for (int i = 0; i < MR; ++i) y[i] = has_min(DT) ? acc[i] + accm[i] : acc[i];
 
+  const int n = I.n;
   const int col = g_raw * RG + r;
   if (KS == 1) {
     if (g_raw < w.ngroups && col < n)
 #pragma unroll
-      for (int i = 0; i < MR; ++i) out[(size_t)i * n + col] = bias ? y[i] + bias[col] : y[i];
+      for (int i = 0; i < MR; ++i) stg_f(I.out + (size_t)i * n + col, I.bias ? y[i] + ldg_f(I.bias + col) : y[i]);
     return;
   }
-  __shared__ float red[4][MR][64];
+  __syncthreads();  // the activation LDS is reused for the partial sums
+  float *red = reinterpret_cast<float *>(lds);  // [4 wavefronts][MR][64]
 #pragma unroll
-  for (int i = 0; i < MR; ++i) red[wv][i][l] = y[i];
+  for (int i = 0; i < MR; ++i) red[(wv * MR + i) * 64 + l] = y[i];
   __syncthreads();
   if (part == 0 && g_raw < w.ngroups && col < n) {
 #pragma unroll
     for (int i = 0; i < MR; ++i) {
-      float t = red[wv][i][l];
-      for (int p = 1; p < KS; ++p) t = t + red[wv + p][i][l];
-      out[(size_t)i * n + col] = bias ? t + bias[col] : t;
+      float tt = red[(wv * MR + i) * 64 + l];
+      for (int p = 1; p < KS; ++p) tt = tt + red[((wv + p) * MR + i) * 64 + l];
+      stg_f(I.out + (size_t)i * n + col, I.bias ? tt + ldg_f(I.bias + col) : tt);
     }
   }
+}
+
+// LDS bytes k_gemv2 needs for m rows and chunks of ch_oct octets
+RW_HD inline size_t gemv_lds_bytes(int m, int ch_oct) {
+  const size_t act = (size_t)ch_oct * OCT * gemv_rec_bytes(m);
+  const size_t red = (size_t)4 * m * 64 * 4;
+  return act > red ? act : red;
 }
 
 // ---------------------------------------------------------------- k_gemm2

@@ -9,7 +9,7 @@
 //   - one-time upload + repack of a weight (QTensor::new plus the packed int8
 //     cache, src/quant.rs:553-563, 589-639);
 //   - regime dispatch (src/quant.rs:754-1051 picks tiers by CPU; here m
-//     picks the kernel: m <= 8 -> k_gemv, else k_gemm);
+//     picks the kernel: m <= 8 -> k_gemv2, else k_quantize + k_gemm2);
 //   - thread safety: host-pointer calls borrow a (stream, buffers) context
 //     from a per-device pool, so concurrent callers never share buffers.
 #include <hip/hip_fp16.h>
@@ -19,9 +19,11 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "rw_kernels.hpp"
@@ -279,37 +281,63 @@ static void launch_gemm_dt(const rw_weight *w, const ActView &av, int m, const f
   }
 }
 
-// the split of a row's blocks over wavefronts depends on the weight only
-static int gemv_ks(const rw_weight *w) { return w->noct >= 4 ? 4 : w->noct >= 2 ? 2 : 1; }
+// ------------------------------------------------------ decode GEMV
 
-template <int DT, int MR, int KS>
-static void launch_gemv_ks(const rw_weight *w, const ActView &av, const float *bias, float *out, hipStream_t s) {
-  constexpr int SETS = 4 / KS;
-  dim3 grid((unsigned)cdiv(w->ngroups, 2 * SETS));
-  hipLaunchKernelGGL((k_gemv<DT, MR, KS>), grid, dim3(256), 0, s, w->view, av, (int)w->n, bias, out);
+// The split of a row's octets over wavefronts depends on the weight only:
+// split while every wavefront keeps at least 4 octets.
+static int gemv_ks(const rw_weight *w) {
+  int ks = 1;
+  while (ks < 4 && w->noct / (2 * ks) >= 4) ks *= 2;
+  return ks;
+}
+static int gemv_wgs(const rw_weight *w, int ks) { return (int)cdiv(w->ngroups, 2 * (4 / ks)); }
+
+// LDS per workgroup is held to GEMV_LDS_CAP bytes: activations go through
+// LDS in chunks of this many octets (the arithmetic does not depend on it).
+constexpr size_t GEMV_LDS_CAP = 32768;
+static int gemv_chunk(int m, int noct_max) {
+  int cap = (int)(GEMV_LDS_CAP / ((size_t)OCT * gemv_rec_bytes(m)));
+  if (cap < 1) cap = 1;
+  return noct_max < cap ? noct_max : cap;
+}
+
+static GemvItem gemv_item(const rw_weight *w, const float *a, const float *bias, float *out) {
+  GemvItem it{};
+  it.w = w->view;
+  it.a = a;
+  it.bias = bias;
+  it.out = out;
+  it.n = (int)w->n;
+  const int ks = gemv_ks(w);
+  it.lks = ks == 4 ? 2 : ks == 2 ? 1 : 0;
+  return it;
 }
 
 template <int DT, int MR>
-static void launch_gemv_mr(const rw_weight *w, const ActView &av, const float *bias, float *out, hipStream_t s) {
-  switch (gemv_ks(w)) {
-    case 4: launch_gemv_ks<DT, MR, 4>(w, av, bias, out, s); break;
-    case 2: launch_gemv_ks<DT, MR, 2>(w, av, bias, out, s); break;
-    default: launch_gemv_ks<DT, MR, 1>(w, av, bias, out, s); break;
-  }
+static void launch_gemv_mr(const GemvItem *items, const int *wg_item, const GemvItem &one, int wgs, int ch_oct,
+                           hipStream_t s) {
+  if (items)
+    hipLaunchKernelGGL((k_gemv2<DT, MR, true>), dim3((unsigned)wgs), dim3(256), gemv_lds_bytes(MR, ch_oct), s,
+                       items, wg_item, one, ch_oct);
+  else
+    hipLaunchKernelGGL((k_gemv2<DT, MR, false>), dim3((unsigned)wgs), dim3(256), gemv_lds_bytes(MR, ch_oct), s,
+                       items, wg_item, one, ch_oct);
 }
 
+// one k_gemv2 launch: `items` (device) + `wg_item` (device) for a group, or
+// items == NULL and the single item `one`
 template <int DT>
-static void launch_gemv_dt(const rw_weight *w, const ActView &av, int m, const float *bias, float *out,
-                           hipStream_t s) {
+static void launch_gemv_dt(int m, const GemvItem *items, const int *wg_item, const GemvItem &one, int wgs,
+                           int ch_oct, hipStream_t s) {
   switch (m) {
-    case 1: launch_gemv_mr<DT, 1>(w, av, bias, out, s); break;
-    case 2: launch_gemv_mr<DT, 2>(w, av, bias, out, s); break;
-    case 3: launch_gemv_mr<DT, 3>(w, av, bias, out, s); break;
-    case 4: launch_gemv_mr<DT, 4>(w, av, bias, out, s); break;
-    case 5: launch_gemv_mr<DT, 5>(w, av, bias, out, s); break;
-    case 6: launch_gemv_mr<DT, 6>(w, av, bias, out, s); break;
-    case 7: launch_gemv_mr<DT, 7>(w, av, bias, out, s); break;
-    default: launch_gemv_mr<DT, 8>(w, av, bias, out, s); break;
+    case 1: launch_gemv_mr<DT, 1>(items, wg_item, one, wgs, ch_oct, s); break;
+    case 2: launch_gemv_mr<DT, 2>(items, wg_item, one, wgs, ch_oct, s); break;
+    case 3: launch_gemv_mr<DT, 3>(items, wg_item, one, wgs, ch_oct, s); break;
+    case 4: launch_gemv_mr<DT, 4>(items, wg_item, one, wgs, ch_oct, s); break;
+    case 5: launch_gemv_mr<DT, 5>(items, wg_item, one, wgs, ch_oct, s); break;
+    case 6: launch_gemv_mr<DT, 6>(items, wg_item, one, wgs, ch_oct, s); break;
+    case 7: launch_gemv_mr<DT, 7>(items, wg_item, one, wgs, ch_oct, s); break;
+    default: launch_gemv_mr<DT, 8>(items, wg_item, one, wgs, ch_oct, s); break;
   }
 }
 
@@ -322,29 +350,158 @@ static void launch_gemv_dt(const rw_weight *w, const ActView &av, int m, const f
     default: FN<RW_Q8_0>(__VA_ARGS__); break;        \
   }
 
+#define RW_DISPATCH_GEMV(w, m, ...)                                              \
+  switch ((w)->dtype) {                                                          \
+    case RW_Q4_0: launch_gemv_dt<RW_Q4_0>((int)(m), __VA_ARGS__); break;         \
+    case RW_Q4_1: launch_gemv_dt<RW_Q4_1>((int)(m), __VA_ARGS__); break;         \
+    case RW_Q5_0: launch_gemv_dt<RW_Q5_0>((int)(m), __VA_ARGS__); break;         \
+    case RW_Q5_1: launch_gemv_dt<RW_Q5_1>((int)(m), __VA_ARGS__); break;         \
+    default: launch_gemv_dt<RW_Q8_0>((int)(m), __VA_ARGS__); break;              \
+  }
+
 // the product from an already quantized workspace, on `s`
 static int run_product(const rw_weight *w, size_t m, const float *bias, float *out, const void *ws,
                        hipStream_t s) {
   ActLayout L = act_layout(m, w->k);
   ActView av = act_view(L, (void *)ws);
   if (m <= GEMV_MAX_M) {
-    RW_DISPATCH_DT(w->dtype, launch_gemv_dt, w, av, (int)m, bias, out, s);
-    LAUNCH_TRY("k_gemv");
+    GemvItem one = gemv_item(w, nullptr, bias, out);
+    one.qa = av.qa;
+    one.qda = av.da;
+    one.qpa = av.pa;
+    one.qsa = av.sa;
+    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, gemv_wgs(w, gemv_ks(w)), gemv_chunk((int)m, w->noct), s);
+    LAUNCH_TRY("k_gemv2");
   } else {
     RW_DISPATCH_DT(w->dtype, launch_gemm_dt, w, av, (int)m, bias, out, s);
-    LAUNCH_TRY("k_gemm");
+    LAUNCH_TRY("k_gemm2");
   }
   return RW_OK;
 }
 
-// quantize + product on `s`, all pointers on the device
+// quantize + product on `s`, all pointers on the device; the decode shape
+// quantizes inside its one launch and does not touch `ws`
 static int run_matmul(const rw_weight *w, const float *a, size_t m, const float *bias, float *out, void *ws,
                       hipStream_t s) {
   if (m == 0) return RW_OK;
+  if (m <= GEMV_MAX_M) {
+    GemvItem one = gemv_item(w, a, bias, out);
+    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, gemv_wgs(w, gemv_ks(w)), gemv_chunk((int)m, w->noct), s);
+    LAUNCH_TRY("k_gemv2");
+    return RW_OK;
+  }
   ActLayout L = act_layout(m, w->k);
   int rc = launch_quantize(a, m, w->k, L, ws, s);
   if (rc) return rc;
   return run_product(w, m, bias, out, ws, s);
+}
+
+// ------------------------------------------------- grouped decode GEMV
+
+// A grouped call becomes one k_gemv2 launch per distinct (dtype, m);
+// the item table and the workgroup -> item map go to the device in one copy.
+struct GroupLaunch {
+  int dt, m, wgs, ch_oct, wg_first;
+};
+
+struct GroupPlan {
+  std::vector<size_t> order;               // non-empty items, in launch order
+  std::vector<int> wg0, wgs, wg_first;     // per ordered item
+  std::vector<GroupLaunch> launches;
+  size_t map_off = 0, bytes = 0;
+};
+
+static GroupPlan group_plan(const rw_linear *items, size_t count) {
+  GroupPlan P;
+  auto key = [&](size_t i) {
+    const rw_weight *w = items[i].w;
+    return std::make_tuple(w->dtype, (int)items[i].m);
+  };
+  for (size_t i = 0; i < count; ++i)
+    if (items[i].w && items[i].m > 0 && items[i].m <= GEMV_MAX_M) P.order.push_back(i);
+  std::stable_sort(P.order.begin(), P.order.end(), [&](size_t x, size_t y) { return key(x) < key(y); });
+  int total = 0;
+  for (size_t j = 0; j < P.order.size(); ++j) {
+    const rw_weight *w = items[P.order[j]].w;
+    const int ks = gemv_ks(w);
+    if (j == 0 || key(P.order[j]) != key(P.order[j - 1])) {
+      P.launches.push_back(GroupLaunch{w->dtype, (int)items[P.order[j]].m, 0, 0, total});
+    }
+    GroupLaunch &L = P.launches.back();
+    const int n = gemv_wgs(w, ks);
+    P.wg0.push_back(L.wgs);
+    P.wgs.push_back(n);
+    P.wg_first.push_back(total);
+    L.wgs += n;
+    L.ch_oct = std::max(L.ch_oct, w->noct);
+    total += n;
+  }
+  for (GroupLaunch &L : P.launches) L.ch_oct = gemv_chunk(L.m, L.ch_oct);
+  P.map_off = align_up(P.order.size() * sizeof(GemvItem), 256);
+  P.bytes = P.order.empty() ? 0 : align_up(P.map_off + (size_t)total * sizeof(int), 256);
+  return P;
+}
+
+// a prepared group: its tables stay on the device, a run only launches
+struct rw_group {
+  int device;
+  std::vector<GroupLaunch> launches;
+  void *table;
+  size_t map_off, bytes;
+};
+
+// pinned staging for launch tables, one per (device, stream); `ev` marks the
+// end of the last copy out of it
+struct Stage {
+  void *host = nullptr;
+  size_t cap = 0;
+  hipEvent_t ev = nullptr;
+  bool pending = false;
+};
+static std::mutex g_stage_mu;
+static std::map<std::pair<int, void *>, Stage> g_stage;
+
+static int check_matmul_args(const rw_weight *w, const void *a, size_t m, size_t k, const void *out);
+
+static int check_group_items(const rw_linear *items, size_t count) {
+  for (size_t i = 0; i < count; ++i) {
+    const rw_linear &it = items[i];
+    int rc = check_matmul_args(it.w, it.a, it.m, it.w ? it.w->k : 0, it.out);
+    if (rc) return fail(rc, "item %zu: %s", i, g_err.c_str());
+    if (it.m > GEMV_MAX_M) return fail(RW_EINVAL, "item %zu: m = %zu > %zu", i, it.m, GEMV_MAX_M);
+    if (it.w->device != items[0].w->device) return fail(RW_EINVAL, "item %zu is on another device", i);
+  }
+  return RW_OK;
+}
+
+// item table, then the workgroup -> item map, as the plan lays them out
+static void fill_tables(const GroupPlan &P, const rw_linear *items, void *host) {
+  GemvItem *tab = (GemvItem *)host;
+  int *map = (int *)((char *)host + P.map_off);
+  for (size_t j = 0; j < P.order.size(); ++j) {
+    const rw_linear &it = items[P.order[j]];
+    tab[j] = gemv_item(it.w, it.a, it.bias, it.out);
+    tab[j].wg0 = P.wg0[j];
+    for (int q = 0; q < P.wgs[j]; ++q) map[P.wg_first[j] + q] = (int)j;
+  }
+}
+
+static int launch_group(const std::vector<GroupLaunch> &launches, const void *table, size_t map_off,
+                        hipStream_t s) {
+  const GemvItem *dtab = (const GemvItem *)table;
+  const int *dmap = (const int *)((const char *)table + map_off);
+  const GemvItem none{};
+  for (const GroupLaunch &L : launches) {
+    switch (L.dt) {
+      case RW_Q4_0: launch_gemv_dt<RW_Q4_0>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.ch_oct, s); break;
+      case RW_Q4_1: launch_gemv_dt<RW_Q4_1>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.ch_oct, s); break;
+      case RW_Q5_0: launch_gemv_dt<RW_Q5_0>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.ch_oct, s); break;
+      case RW_Q5_1: launch_gemv_dt<RW_Q5_1>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.ch_oct, s); break;
+      default: launch_gemv_dt<RW_Q8_0>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.ch_oct, s); break;
+    }
+    LAUNCH_TRY("k_gemv2 (grouped)");
+  }
+  return RW_OK;
 }
 
 static int check_matmul_args(const rw_weight *w, const void *a, size_t m, size_t k, const void *out) {
@@ -509,7 +666,9 @@ int rw_rocm_matmul_t_q_dev(const rw_weight *w, const float *a, size_t m, size_t 
   HIP_TRY(hipSetDevice(w->device));
   size_t need = act_layout(m, k).bytes;
   void *ws = workspace;
-  if (ws) {
+  if (m <= GEMV_MAX_M) {
+    ws = nullptr;  // the decode shape quantizes inside its launch
+  } else if (ws) {
     if (workspace_len < need) return fail(RW_EINVAL, "workspace of %zu bytes < %zu needed", workspace_len, need);
   } else {
     rc = stream_workspace(w->device, stream, need, &ws);
@@ -570,44 +729,101 @@ int rw_rocm_matmul_t_q(const rw_weight *w, const float *a, size_t m, size_t k, c
 }
 
 size_t rw_rocm_grouped_workspace_size(const rw_linear *items, size_t count) {
-  size_t best = 0;
-  for (size_t i = 0; items && i < count; ++i)
-    if (items[i].w && items[i].m > 0) {
-      size_t b = act_layout(items[i].m, items[i].w->k).bytes;
-      best += align_up(b, 256);
-    }
-  return best;
+  if (!items) return 0;
+  return group_plan(items, count).bytes;
 }
 
 int rw_rocm_matmul_grouped_dev(const rw_linear *items, size_t count, void *workspace, size_t workspace_len,
                                void *stream) {
   if (count == 0) return RW_OK;
   if (!items) return fail(RW_EINVAL, "items is NULL");
-  size_t need = rw_rocm_grouped_workspace_size(items, count);
-  for (size_t i = 0; i < count; ++i) {
-    const rw_linear &it = items[i];
-    int rc = check_matmul_args(it.w, it.a, it.m, it.w ? it.w->k : 0, it.out);
-    if (rc) return fail(rc, "item %zu: %s", i, g_err.c_str());
-    if (it.m > GEMV_MAX_M) return fail(RW_EINVAL, "item %zu: m = %zu > %zu", i, it.m, GEMV_MAX_M);
-    if (it.w->device != items[0].w->device) return fail(RW_EINVAL, "item %zu is on another device", i);
-  }
-  HIP_TRY(hipSetDevice(items[0].w->device));
+  int rc0 = check_group_items(items, count);
+  if (rc0) return rc0;
+  GroupPlan P = group_plan(items, count);
+  if (P.order.empty()) return RW_OK;
+  const int device = items[0].w->device;
+  HIP_TRY(hipSetDevice(device));
   void *ws = workspace;
   if (ws) {
-    if (workspace_len < need) return fail(RW_EINVAL, "workspace of %zu bytes < %zu needed", workspace_len, need);
+    if (workspace_len < P.bytes) return fail(RW_EINVAL, "workspace of %zu bytes < %zu needed", workspace_len, P.bytes);
   } else {
-    int rc = stream_workspace(items[0].w->device, stream, need, &ws);
+    int rc = stream_workspace(device, stream, P.bytes, &ws);
     if (rc) return rc;
   }
-  char *p = (char *)ws;
-  for (size_t i = 0; i < count; ++i) {
-    const rw_linear &it = items[i];
-    if (it.m == 0) continue;
-    int rc = run_matmul(it.w, it.a, it.m, it.bias, it.out, p, (hipStream_t)stream);
-    if (rc) return fail(rc, "item %zu: %s", i, g_err.c_str());
-    p += align_up(act_layout(it.m, it.w->k).bytes, 256);
+  hipStream_t s = (hipStream_t)stream;
+  {
+    // the tables go up through pinned memory of this (device, stream); the
+    // previous copy out of it must have finished before it is rewritten
+    std::lock_guard<std::mutex> lk(g_stage_mu);
+    Stage &st = g_stage[std::make_pair(device, stream)];
+    if (st.pending) {
+      HIP_TRY(hipEventSynchronize(st.ev));
+      st.pending = false;
+    }
+    if (!st.ev) HIP_TRY(hipEventCreateWithFlags(&st.ev, hipEventDisableTiming));
+    if (st.cap < P.bytes) {
+      if (st.host) HIP_TRY(hipHostFree(st.host));
+      st.host = nullptr;
+      st.cap = 0;
+      size_t want = align_up(P.bytes, (size_t)1 << 16);
+      if (hipHostMalloc(&st.host, want, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        st.host = nullptr;
+        return fail(RW_ENOMEM, "hipHostMalloc(%zu) for a launch table failed", want);
+      }
+      st.cap = want;
+    }
+    fill_tables(P, items, st.host);
+    HIP_TRY(hipMemcpyAsync(ws, st.host, P.bytes, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipEventRecord(st.ev, s));
+    st.pending = true;
   }
+  return launch_group(P.launches, ws, P.map_off, s);
+}
+
+int rw_rocm_group_create(const rw_linear *items, size_t count, rw_group **out) {
+  if (!out) return fail(RW_EINVAL, "out is NULL");
+  *out = nullptr;
+  if (count == 0 || !items) return fail(RW_EINVAL, "a group needs at least one item");
+  int rc = check_group_items(items, count);
+  if (rc) return rc;
+  GroupPlan P = group_plan(items, count);
+  if (P.order.empty()) return fail(RW_EINVAL, "every item has m = 0");
+  const int device = items[0].w->device;
+  HIP_TRY(hipSetDevice(device));
+  std::vector<char> host(P.bytes);
+  fill_tables(P, items, host.data());
+  rw_group *g = new rw_group;
+  g->device = device;
+  g->launches = P.launches;
+  g->map_off = P.map_off;
+  g->bytes = P.bytes;
+  if (hipMalloc(&g->table, P.bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    delete g;
+    return fail(RW_ENOMEM, "hipMalloc(%zu) for a launch table failed", P.bytes);
+  }
+  hipError_t e = hipMemcpy(g->table, host.data(), P.bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(g->table);
+    delete g;
+    return fail(RW_EHIP, "hipMemcpy: %s", hipGetErrorString(e));
+  }
+  *out = g;
   return RW_OK;
+}
+
+int rw_rocm_group_run(const rw_group *g, void *stream) {
+  if (!g) return fail(RW_EINVAL, "group is NULL");
+  HIP_TRY(hipSetDevice(g->device));
+  return launch_group(g->launches, g->table, g->map_off, (hipStream_t)stream);
+}
+
+void rw_rocm_group_free(rw_group *g) {
+  if (!g) return;
+  if (hipSetDevice(g->device) == hipSuccess) (void)hipFree(g->table);
+  (void)hipGetLastError();
+  delete g;
 }
 
 int rw_rocm_dequant_rows(const rw_weight *w, size_t row0, size_t nrows, float *out) {

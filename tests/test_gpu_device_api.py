@@ -1,0 +1,190 @@
+"""Device-pointer entry points on the GPU, through the C ABI.
+
+Bars (written in each test):
+  * quantizing inside the decode launch and quantizing separately
+    (rw_rocm_quantize_dev + rw_rocm_matmul_prequant_dev) give bitwise the
+    same outputs, in both regimes;
+  * a grouped launch and a prepared group give, per item, bitwise what the
+    same linear gives alone;
+  * device and host entry points agree bitwise;
+  * outputs stay within 1e-3 of the reference CPU path (max error over the
+    reference row's L2 norm), also when the activations go through LDS in
+    several chunks.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from rusty_whisper_amd import _abi as A
+
+from _data import DTYPES, NAMES, activations, rel_row_l2, weights
+
+pytestmark = pytest.mark.gpu
+
+NORTH_STAR_TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    A.init(0)
+    return t
+
+
+def _dev(torch, x):
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0")
+
+
+def _bits(x):
+    return np.ascontiguousarray(x).view(np.uint32)
+
+
+def _single(torch, w, a, bias=None):
+    m = a.shape[0]
+    out = torch.empty(m, w.n, device="cuda:0")
+    w.matmul_dev(_dev(torch, a), m, out, None if bias is None else _dev(torch, bias))
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: NAMES[d])
+@pytest.mark.parametrize("m", [1, 5, 8, 9, 40])
+def test_device_matches_host_bitwise(torch, dtype, m):
+    k, n = 416, 75
+    raw = weights(dtype, n, k, seed=5 + m)
+    w = A.DeviceWeight(dtype, n, k, raw)
+    a = activations(m, k, seed=7 * m + dtype)
+    bias = np.random.default_rng(m).standard_normal(n).astype(np.float32)
+    assert np.array_equal(_bits(_single(torch, w, a, bias)), _bits(w.matmul(a, bias)))
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: NAMES[d])
+@pytest.mark.parametrize("m", [1, 3, 8, 9, 70])
+def test_prequant_matches_fused_bitwise(torch, dtype, m):
+    k, n = 1280, 96
+    raw = weights(dtype, n, k, seed=31 + m)
+    w = A.DeviceWeight(dtype, n, k, raw)
+    a = activations(m, k, seed=m + 100 * dtype, outliers=0.01)
+    fused = _single(torch, w, a)
+    wsz = A.workspace_size(m, k)
+    ws = torch.empty(wsz, dtype=torch.uint8, device="cuda:0")
+    out = torch.empty(m, n, device="cuda:0")
+    A.quantize_dev(_dev(torch, a), m, k, ws, wsz)
+    w.matmul_prequant_dev(ws, m, out)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(out.cpu().numpy()), _bits(fused))
+    assert rel_row_l2(fused, O.matmul_emul(a, dtype, raw, n)) <= NORTH_STAR_TOL
+
+
+# (dtype, m, n, k, bias): every k split (k = 384 -> 2, 768 / 1280 -> 1,
+# 5120 -> 4), ragged n, an m = 0 entry, two entries that share a launch, and
+# one large enough in k (m = 8) that its activations pass through LDS in
+# several chunks
+GROUP = [
+    (7, 5, 1280, 1280, True),
+    (6, 5, 96, 5120, False),
+    (2, 1, 41, 384, True),
+    (3, 8, 70, 768, True),
+    (8, 3, 33, 96, False),
+    (7, 5, 200, 1280, False),
+    (6, 0, 10, 64, False),
+    (8, 8, 64, 16384, True),
+    (3, 2, 1, 32, True),
+]
+
+
+def _group_items(torch, specs, seed):
+    rng = np.random.default_rng(seed)
+    items, host = [], []
+    for j, (dt, m, n, k, has_b) in enumerate(specs):
+        raw = weights(dt, n, k, seed=seed + 13 * j)
+        w = A.DeviceWeight(dt, n, k, raw)
+        a = activations(m, k, seed=seed + 7 * j) if m else np.zeros((0, k), np.float32)
+        b = rng.standard_normal(n).astype(np.float32) if has_b else None
+        da = _dev(torch, a) if m else torch.empty(1, device="cuda:0")
+        db = None if b is None else _dev(torch, b)
+        out = torch.full((max(m, 1), n), float("nan"), device="cuda:0")
+        items.append((w, da, db, out, m))
+        host.append((w, a, b, raw))
+    return items, host
+
+
+def test_grouped_matches_single_bitwise(torch):
+    items, host = _group_items(torch, GROUP, seed=900)
+    arr = A.make_linears(items)
+    wsz = A.grouped_workspace_size(arr)
+    ws = torch.empty(wsz, dtype=torch.uint8, device="cuda:0")
+    A.matmul_grouped_dev(arr, ws, wsz)
+    torch.cuda.synchronize()
+    for (w, _, _, out, m), (_, a, b, raw) in zip(items, host):
+        if m == 0:
+            assert torch.isnan(out).all(), "an m = 0 entry must write nothing"
+            continue
+        got = out.cpu().numpy()
+        assert np.array_equal(_bits(got), _bits(_single(torch, w, a, b))), (w.dtype, m, w.n, w.k)
+        ref = O.matmul_emul(a, w.dtype, raw, w.n, bias=b)
+        assert rel_row_l2(got, ref) <= NORTH_STAR_TOL, (w.dtype, m, w.n, w.k)
+
+
+def test_prepared_group_matches_grouped_bitwise(torch):
+    items, _ = _group_items(torch, GROUP, seed=901)
+    arr = A.make_linears(items)
+    A.matmul_grouped_dev(arr)  # the library's own workspace for this stream
+    torch.cuda.synchronize()
+    first = [o.cpu().numpy().copy() for (_, _, _, o, m) in items]
+    g = A.Group(arr)
+    for _ in range(3):  # repeated runs of one prepared group
+        for (_, _, _, o, m) in items:
+            if m:
+                o.fill_(float("nan"))
+        g.run()
+        torch.cuda.synchronize()
+        for (_, _, _, o, m), f in zip(items, first):
+            assert np.array_equal(_bits(o.cpu().numpy()), _bits(f))
+    g.free()
+
+
+def test_grouped_back_to_back_calls_keep_their_tables(torch):
+    # two different groups queued on one stream with no host wait between:
+    # the second call's tables must not overwrite what the first launch reads
+    items1, host1 = _group_items(torch, GROUP[:4], seed=902)
+    items2, host2 = _group_items(torch, GROUP[4:], seed=903)
+    arr1, arr2 = A.make_linears(items1), A.make_linears(items2)
+    for _ in range(2):
+        A.matmul_grouped_dev(arr1)
+        A.matmul_grouped_dev(arr2)
+    torch.cuda.synchronize()
+    for items, host in ((items1, host1), (items2, host2)):
+        for (w, _, _, out, m), (_, a, b, _) in zip(items, host):
+            if m:
+                assert np.array_equal(_bits(out.cpu().numpy()), _bits(_single(torch, w, a, b)))
+
+
+@pytest.mark.parametrize("dtype", [2, 7], ids=["Q4_0", "Q5_1"])
+def test_gemv_chunked_k_rows_independent_of_m(torch, dtype):
+    # k = 16384: at m = 8 the activations go through LDS in several chunks, at
+    # m = 1 in one; a row's result must not depend on that
+    k, n = 16384, 40
+    raw = weights(dtype, n, k, seed=77)
+    w = A.DeviceWeight(dtype, n, k, raw)
+    a = activations(8, k, seed=78, outliers=0.01)
+    got8 = _single(torch, w, a)
+    got1 = _single(torch, w, a[:1])
+    assert np.array_equal(_bits(got8[:1]), _bits(got1))
+    assert rel_row_l2(got8, O.matmul_emul(a, dtype, raw, n)) <= NORTH_STAR_TOL
+
+
+def test_grouped_rejects_bad_items(torch):
+    w = A.DeviceWeight(8, 32, 64, weights(8, 32, 64, seed=1))
+    a = torch.zeros(9, 64, device="cuda:0")
+    o = torch.zeros(9, 32, device="cuda:0")
+    with pytest.raises(A.RwError, match="m = 9"):
+        A.matmul_grouped_dev(A.make_linears([(w, a, None, o, 9)]))
+    arr = A.make_linears([(w, a, None, o, 5)])
+    wsz = A.grouped_workspace_size(arr)
+    assert wsz > 0
+    ws = torch.empty(wsz, dtype=torch.uint8, device="cuda:0")
+    with pytest.raises(A.RwError, match="workspace"):
+        A.matmul_grouped_dev(arr, ws, wsz - 1)
+    with pytest.raises(A.RwError, match="m = 0"):
+        A.Group(A.make_linears([(w, a, None, o, 0)]))
