@@ -6,18 +6,18 @@
 //                   (src/quant.rs:528-537)
 //   k_quantize      f32 activations -> int8 blocks + d_a + sums, bit-exact
 //                   with quantize_acts_i8 (src/quant.rs:691-716)
+//   k_quantize_f16  the same quantization, stored as f16 values d_a*q_a
+//                   (row-scaled by a power of two) for the encoder GEMM
 //   k_block_dots    exact per-block integer sums via int8 MFMA (validation)
-//   k_gemm          encoder shape (m > 8): v_mfma_i32_32x32x32_i8, one MFMA
-//                   per 32x32 output tile per block, f32 combine on the VALU
+//   k_gemm          encoder shape (m > 8): f16 MFMA GEMM of the quantized
+//                   activations' values against weights dequantized in
+//                   registers (d_b*q_b + m_b, one rounding to f16)
 //   k_gemv2         decoder shape (m <= 8): any number of linears in one
 //                   launch, activations quantized into LDS, one lane per
-//                   weight row, v_dot4_i32_i8
+//                   weight row, v_dot4_i32_i8 exact block sums
 //
-// One combine rule for every output element, in every kernel:
-//     acc  = fma(d_a*d_b, float(S), acc)      over blocks in order
-//     accm = fma(m_b, pa, accm)               (_1 formats only)
-//     y    = acc (+ accm) (+ bias)
-// so a row's result does not depend on m within a kernel family.
+// Within a kernel family a row's result never depends on m: every choice
+// of order (k splits, chunking) depends on the weight's shape alone.
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -30,7 +30,6 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
-typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 // ------------------------------------------------------------ scalar helpers
 
@@ -70,28 +69,6 @@ __device__ inline uint32_t sub_bytes(uint32_t x, uint32_t c) {
 
 __device__ inline uint32_t rotl(uint32_t x, int t) { return t == 0 ? x : (x << t) | (x >> (32 - t)); }
 
-// Exact split of an f32 into bf16 parts by truncation: x = hi + r1,
-// r1 = mid + lo, each difference exact.  Returns the bf16 bit patterns.
-__device__ inline void split3_bf16(float x, uint32_t &hi, uint32_t &mid, uint32_t &lo) {
-  const uint32_t hb = __float_as_uint(x) & 0xffff0000u;
-  const float r1 = __fsub_rn(x, __uint_as_float(hb));
-  const uint32_t mb = __float_as_uint(r1) & 0xffff0000u;
-  const float r2 = __fsub_rn(r1, __uint_as_float(mb));
-  hi = hb >> 16;
-  mid = mb >> 16;
-  lo = __float_as_uint(r2) >> 16;
-}
-
-// f16-exact value (an f16 scale or min widened to f32) as two bf16 parts,
-// packed low half = high part: 8 + 3 significant bits, exact.
-__device__ inline uint32_t split2_bf16_packed(float x) {
-  const uint32_t hb = __float_as_uint(x) & 0xffff0000u;
-  const float r = __fsub_rn(x, __uint_as_float(hb));
-  return (hb >> 16) | (__float_as_uint(r) & 0xffff0000u);
-}
-
-__device__ inline uint32_t pair16(uint32_t v) { return v | (v << 16); }
-
 // --------------------------------------------------------------- k_repack
 
 template <int DT>
@@ -126,8 +103,8 @@ __device__ inline void read_block(const uint8_t *p, uint16_t &d, uint16_t &m, ui
 // one thread per (row, block) of the padded matrix
 template <int DT>
 __global__ __launch_bounds__(256) void k_repack(const uint8_t *__restrict__ raw, int n, int nb, uint8_t *qs,
-                                                uint32_t *qh, uint16_t *dd, uint16_t *mm, uint32_t *dsp, uint32_t *msp,
-                                                int nb_pad, int noct, int ngroups) {
+                                                uint32_t *qh, uint16_t *dd, uint16_t *mm, uint32_t *dm,
+                                                uint32_t *qhb, int nb_pad, int noct, int ngroups) {
   constexpr int BB = DT == 2 ? 18 : DT == 3 ? 20 : DT == 6 ? 22 : DT == 7 ? 24 : 34;
   constexpr int QSB = DT == 8 ? 32 : 16;
   size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -152,12 +129,12 @@ __global__ __launch_bounds__(256) void k_repack(const uint8_t *__restrict__ raw,
   dd[si] = d;
   if (has_min(DT)) mm[si] = m;
   const size_t slot = qs_slot(w, g, bl, r);
-  dsp[slot] = split2_bf16_packed(h2f_exact(d));
-  if (has_min(DT)) msp[slot] = split2_bf16_packed(h2f_exact(m));
+  dm[slot] = (uint32_t)d | ((uint32_t)m << 16);
   if (has_high(DT)) {
     uint32_t x = 0;
     for (int e = 0; e < 32; ++e) x |= ((h >> e) & 1u) << qh_bit(e);
     qh[si] = x;
+    qhb[slot] = x;
   }
 }
 
@@ -232,9 +209,7 @@ __device__ inline uint32_t pack_q4(const BlockQuant &b) {
 // are written as zeros.
 __global__ __launch_bounds__(256) void k_quantize(const float *__restrict__ a, int m, int k, int nb, int mgroups,
                                                   int8_t *__restrict__ qa, float *__restrict__ da,
-                                                  float *__restrict__ pa, int32_t *__restrict__ sa,
-                                                  uint16_t *__restrict__ qh16, uint32_t *__restrict__ ds16,
-                                                  uint32_t *__restrict__ pm16) {
+                                                  float *__restrict__ pa, int32_t *__restrict__ sa) {
   size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   size_t rb = t >> 3;
   int lt = (int)(t & 7);
@@ -249,24 +224,65 @@ __global__ __launch_bounds__(256) void k_quantize(const float *__restrict__ a, i
   const BlockQuant bq = quantize_block8(x);
   size_t slot = act_slot(nb, g, bl, r);
   *reinterpret_cast<uint32_t *>(qa + slot * QK + mfma_pos(4 * lt)) = pack_q4(bq);
-  if (qh16) {
-    h2v lo2 = {(_Float16)bq.q0, (_Float16)bq.q1}, hi2 = {(_Float16)bq.q2, (_Float16)bq.q3};
-    uint2 hv = make_uint2(__builtin_bit_cast(uint32_t, lo2), __builtin_bit_cast(uint32_t, hi2));
-    *reinterpret_cast<uint2 *>(qh16 + slot * QK + mfma_pos(4 * lt)) = hv;
-  }
   if (lt == 0) {
-    const float p = __fmul_rn(bq.d, (float)bq.sum);
     da[slot] = bq.d;
-    pa[slot] = p;
+    pa[slot] = __fmul_rn(bq.d, (float)bq.sum);
     sa[slot] = bq.sum;
-    if (ds16) {
-      uint32_t hi, mid, lo;
-      split3_bf16(bq.d, hi, mid, lo);
-      *reinterpret_cast<uint4 *>(ds16 + slot * 4) = make_uint4(pair16(hi), pair16(mid), pair16(lo), 0u);
-      split3_bf16(p, hi, mid, lo);
-      *reinterpret_cast<uint4 *>(pm16 + slot * 4) = make_uint4(pair16(hi), pair16(mid), pair16(lo), 0u);
+  }
+}
+
+// Activations for the encoder GEMM, one workgroup per row of the padded
+// row groups (rows >= m are written as zeros); 8 lanes per block, 32 blocks
+// per pass.  The quantization is quantize_acts_i8's (src/quant.rs:691-716)
+// bit for bit; each element is stored as f16(d_a * q_a * 2^-e), in the MFMA
+// order of the int8 layout, with e chosen from the row's largest |x| so that
+// the largest value lands in [2^14, 2^15): no value overflows, and every
+// value keeps f16's full precision unless it is below 2^-28 of the row's
+// largest.  rs[row] = 2^e undoes the scaling exactly in the GEMM's epilogue.
+__global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ a, int m, int k, int nb,
+                                                      uint16_t *__restrict__ a16, float *__restrict__ rs) {
+  __shared__ float wmax[4];
+  const int row = blockIdx.x;
+  const int t = threadIdx.x, lb = t >> 3, lt = t & 7;
+  const int g = row / RG, r = row % RG;
+  if (row >= m) {  // uniform per workgroup
+    for (int bl = lb; bl < nb; bl += 32)
+      *reinterpret_cast<uint2 *>(a16 + act_slot(nb, g, bl, r) * QK + mfma_pos(4 * lt)) = make_uint2(0u, 0u);
+    if (t == 0) rs[row] = 0.0f;
+    return;
+  }
+  const float *x = a + (size_t)row * k;
+  float amax = 0.0f;
+  for (int bl = lb; bl < nb; bl += 32) {
+    const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)bl * QK + 4 * lt);
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  if ((t & 63) == 0) wmax[t >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  int e = 15;  // zero, inf or NaN rows: no scaling
+  if (amax > 0.0f && amax <= 3.4028235e38f) {
+    frexpf(amax, &e);  // amax in [2^(e-1), 2^e)
+    e = max(e, -110);
+  }
+  const float down = ldexpf(1.0f, 15 - e);
+  // whole wavefronts run every pass (the shuffles need all 8 lanes of a
+  // block); lanes past the row's blocks quantize zeros and store nothing
+  for (int b0 = 0; b0 < nb; b0 += 32) {
+    const int bl = b0 + lb;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (bl < nb) v = *reinterpret_cast<const float4 *>(x + (size_t)bl * QK + 4 * lt);
+    const BlockQuant bq = quantize_block8(v);
+    if (bl < nb) {
+      h2v lo2 = {(_Float16)(__fmul_rn(bq.d, (float)bq.q0) * down), (_Float16)(__fmul_rn(bq.d, (float)bq.q1) * down)};
+      h2v hi2 = {(_Float16)(__fmul_rn(bq.d, (float)bq.q2) * down), (_Float16)(__fmul_rn(bq.d, (float)bq.q3) * down)};
+      *reinterpret_cast<uint2 *>(a16 + act_slot(nb, g, bl, r) * QK + mfma_pos(4 * lt)) =
+          make_uint2(__builtin_bit_cast(uint32_t, lo2), __builtin_bit_cast(uint32_t, hi2));
     }
   }
+  if (t == 0) rs[row] = ldexpf(1.0f, e - 15);
 }
 
 // --------------------------------------------------- MFMA operand unpack
@@ -319,97 +335,6 @@ __global__ __launch_bounds__(64) void k_block_dots(WeightView w, ActView a, int 
     int i = gm * RG + 8 * (v >> 2) + 4 * h + (v & 3);
     if (i < m && j < n) S[((size_t)i * n + j) * a.nb + bl] = s[v];
   }
-}
-
-// ---------------------------------------------------------------- k_gemm
-
-// Workgroup: 4 wavefronts in a 2x2 grid; each wavefront owns TM x TN tiles of
-// 32x32 outputs (activation rows x weight rows).  Per block: one int8 MFMA
-// per tile gives the exact S, then the f32 combine.
-template <int DT, int TM, int TN>
-__global__ __launch_bounds__(256) void k_gemm(WeightView w, ActView a, int m, int n, const float *__restrict__ bias,
-                                              float *__restrict__ out) {
-  const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int h = l >> 5, r = l & 31;
-  const int wm = wv & 1, wn = wv >> 1;
-  int rt[TM], ct[TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i) rt[i] = (blockIdx.y * 2 + wm) * TM + i;
-#pragma unroll
-  for (int j = 0; j < TN; ++j) ct[j] = (blockIdx.x * 2 + wn) * TN + j;
-  int rtc[TM], ctc[TN];  // clamped for loads; results of clamped tiles are dropped
-#pragma unroll
-  for (int i = 0; i < TM; ++i) rtc[i] = rt[i] < a.mgroups ? rt[i] : a.mgroups - 1;
-#pragma unroll
-  for (int j = 0; j < TN; ++j) ctc[j] = ct[j] < w.ngroups ? ct[j] : w.ngroups - 1;
-
-  float acc[TM][TN][16];
-  float accm[TM][TN][16];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        acc[i][j][v] = 0.0f;
-        accm[i][j][v] = 0.0f;
-      }
-
-  const v16i zero = {};
-  for (int bl = 0; bl < w.nb; ++bl) {
-    v4i aop[TM];
-    float4 dav[TM][4], pav[TM][4];
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      size_t base = act_slot(a.nb, rtc[i], bl, 0);
-      aop[i] = *reinterpret_cast<const v4i *>(a.qa + (base + r) * QK + 16 * h);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        dav[i][q] = *reinterpret_cast<const float4 *>(a.da + base + 8 * q + 4 * h);
-        if (has_min(DT)) pav[i][q] = *reinterpret_cast<const float4 *>(a.pa + base + 8 * q + 4 * h);
-      }
-    }
-    v4i bop[TN];
-    float db[TN], mb[TN];
-#pragma unroll
-    for (int j = 0; j < TN; ++j) bop[j] = weight_operand<DT>(w, ctc[j], bl, r, h, db[j], mb[j]);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        v16i s = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[i], bop[j], zero, 0, 0, 0);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float dq[4] = {dav[i][q].x, dav[i][q].y, dav[i][q].z, dav[i][q].w};
-          const float pq[4] = {pav[i][q].x, pav[i][q].y, pav[i][q].z, pav[i][q].w};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int v = 4 * q + e;
-            acc[i][j][v] = __builtin_fmaf(dq[e] * db[j], (float)s[v], acc[i][j][v]);
-            if (has_min(DT)) accm[i][j][v] = __builtin_fmaf(mb[j], pq[e], accm[i][j][v]);
-          }
-        }
-      }
-  }
-
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      if (rt[i] >= a.mgroups || ct[j] >= w.ngroups) continue;
-      const int col = ct[j] * RG + r;
-      if (col >= n) continue;
-      const float b = bias ? bias[col] : 0.0f;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = rt[i] * RG + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (row >= m) continue;
-        float y = acc[i][j][v];
-        if (has_min(DT)) y = y + accm[i][j][v];
-        if (bias) y = y + b;
-        out[(size_t)row * n + col] = y;
-      }
-    }
 }
 
 // ---------------------------------------------------------------- k_gemv2
@@ -676,46 +601,7 @@ RW_HD inline size_t gemv_lds_bytes(int m, int ch_oct) {
   return act > red ? act : red;
 }
 
-// ---------------------------------------------------------------- k_gemm2
-
-__device__ inline v8bf bf16x8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-  return __builtin_bit_cast(v8bf, make_uint4(a, b, c, d));
-}
-
-// Raw operands of one block for a wave tile, as loaded from HBM / L2: the
-// f16 activation quants and d_a splits of TM row groups, the packed weight
-// quants, high bits and d_b split of TN row groups.
-template <int TM, int TN>
-struct BlockOps {
-  uint4 qa0[TM], qa1[TM], sa[TM];
-  uint4 qw[TN];  // packed nibbles in .x/.y, or the 16 Q8_0 bytes
-  uint32_t qh[TN], ds[TN];
-};
-
-template <int DT, int TM, int TN>
-__device__ inline void load_block_ops(BlockOps<TM, TN> &o, const WeightView &w, const GemmPlanes &gp,
-                                      const ActView &a, const int (&rt)[TM], const int (&ct)[TN], int bl, int r,
-                                      int h) {
-#pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const size_t as = act_slot(a.nb, rt[i], bl, r);
-    o.qa0[i] = *reinterpret_cast<const uint4 *>(a.qh16 + as * QK + 16 * h);
-    o.qa1[i] = *reinterpret_cast<const uint4 *>(a.qh16 + as * QK + 16 * h + 8);
-    o.sa[i] = *reinterpret_cast<const uint4 *>(a.ds16 + as * 4);
-  }
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const size_t slot = qs_slot(w, ct[j], bl, r);
-    if (DT == 8) {
-      o.qw[j] = *reinterpret_cast<const uint4 *>(w.qs + slot * 32 + 16 * h);
-    } else {
-      const uint2 v = *reinterpret_cast<const uint2 *>(w.qs + slot * 16 + 8 * h);
-      o.qw[j] = make_uint4(v.x, v.y, 0u, 0u);
-    }
-    o.qh[j] = has_high(DT) ? w.qh[sc_index(w, ct[j], bl, r)] : 0u;
-    o.ds[j] = gp.dsp[slot];
-  }
-}
+// ---------------------------------------------------------------- k_gemm
 
 // Nibble bytes (plus high-bit flags) of one lane's 16 quants -> the two f16
 // B operands.  Each byte b becomes the f16 1024 + b (bits 0x6400 | b, one
@@ -758,56 +644,57 @@ __device__ inline void weight_f16_from(int h, uint4 qs, uint32_t qhw, v8h &b0, v
   quants_to_f16<DT>(q, b0, b1);
 }
 
-// One block of a wave tile: per tile two f16 MFMAs for the exact sums, one
-// bf16 MFMA for the scale outer product, then acc += s * S.  valid == false
-// (a clamped, missing block) zeroes d_b so the block adds nothing.
-template <int DT, int TM, int TN>
-__device__ inline void gemm_block(v16f (&acc)[TM][TN], const BlockOps<TM, TN> &o, int h, bool valid) {
-  const v16f zero = {};
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    v8h wb0, wb1;
-    weight_f16_from<DT>(h, o.qw[j], o.qh[j], wb0, wb1);
-    const uint32_t dsv = valid ? o.ds[j] : 0u;
-    const v8bf bs = bf16x8(dsv, dsv, dsv, 0u);
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const uint4 sv = h ? make_uint4(0u, 0u, 0u, 0u) : o.sa[i];
-      v16f S = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, o.qa0[i]), wb0, zero, 0, 0, 0);
-      S = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, o.qa1[i]), wb1, S, 0, 0, 0);
-      const v16f sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, sv), bs, zero, 0, 0, 0);
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = __builtin_fmaf(sc[v], S[v], acc[i][j][v]);
-    }
-  }
-}
+// Stage layout of k_gemm, in bytes.  A stage holds two blocks, one per
+// k-wave; per k-wave: 2 activation row groups of f16 values (32 rows of
+// 64 B, 80 B apart so a wavefront's 16-byte reads cover every LDS bank),
+// then 4 weight row groups x {quants, high-bit words (Q5), (d, m) pairs}.
+// Each piece is a contiguous run of a device plane copied in 16-byte
+// chunks, so chunk c of a stage always comes from one plane offset plus
+// (block index) x (that plane's block stride).
+template <int DT>
+struct GL {
+  static constexpr int QSB = DT == 8 ? 32 : 16;  // quant bytes per row-block
+  static constexpr bool HH = DT == 6 || DT == 7;
+  static constexpr int A_PITCH = 80, A_ROWC = 4, A_CH = RG * A_ROWC, A_BYTES = RG * A_PITCH;
+  static constexpr int B_ROWC = QSB / 16, B_QSCH = RG * B_ROWC, B_QHCH = HH ? 8 : 0, B_DMCH = 8;
+  static constexpr int B_CH = B_QSCH + B_QHCH + B_DMCH;
+  static constexpr int B_QS = RG * QSB, B_QH = 16 * B_QHCH, B_BYTES = B_QS + B_QH + 16 * B_DMCH;
+  static constexpr int KW_BYTES = 2 * A_BYTES + 4 * B_BYTES;
+  static constexpr int STAGE = 2 * KW_BYTES;
+  static constexpr int KWC = 2 * A_CH + 4 * B_CH;  // chunks per k-wave
+  static constexpr int NCH = 2 * KWC;              // chunks per stage
+  static constexpr int LPT = (NCH + 255) / 256;    // chunks per thread per stage
+  static constexpr int RED = 2 * 64 * 64 * 4;      // k-wave reduction buffer
+  static constexpr int LDS = 2 * STAGE > RED ? 2 * STAGE : RED;
+};
 
-// Encoder-shape GEMM (m > 8).  Per 32x32 output tile and block:
-//   S  = two v_mfma_f32_32x32x16_f16 on exact small integers (exact in f32)
-//   s  = one v_mfma_f32_32x32x16_bf16 outer product of the exact bf16
-//        splits of d_a (rows) and d_b (columns): d_a*d_b, rounded once
-//   acc = fma(s, S, acc)                         (the only VALU op)
-// For the _1 formats one more bf16 MFMA per block pair adds the min term
-// m_b * d_a * sum(q_a) of both blocks (each lane half carries one block of
-// the pair) straight into acc.
-// A wavefront owns TM x TN tiles (TM activation row groups x TN weight row
-// groups), so each operand it loads feeds TN or TM tiles, and it loads block
-// b+1's raw operands while block b computes.  A workgroup is 4 wavefronts:
-// 4/SK wave tiles side by side along n, each split over SK wavefronts along k
-// (SK depends on the weight's shape only, so a row's result never depends on
-// m).  Partials meet in LDS and are added in k order; y = sum of acc + bias.
-template <int DT, int TM, int TN, int SK>
-__global__ __launch_bounds__(256, 2) void k_gemm2(WeightView w, GemmPlanes gp, ActView a, int m, int n,
-                                                  const float *__restrict__ bias, float *__restrict__ out) {
-  constexpr int TILES = 4 / SK;
-  const int l = threadIdx.x & 63, wv = threadIdx.x >> 6;
+// Encoder-shape GEMM (m > 8): out = rs * (A' W'^T) (+ bias), with A' the f16
+// values of the quantized activations (k_quantize_f16) and W' = f16(d_b*q_b
+// + m_b) formed in registers with one packed f16 fma per two weights (a
+// single rounding).  Products of f16 operands are exact and accumulate in
+// f32 inside v_mfma_f32_32x32x16_f16, so |y - exact| <= 2^-10 sum|a||w|
+// plus the f32 accumulation error.
+// A workgroup is 4 wavefronts: 2 along n (64 weight rows each) x 2 along k
+// (even / odd blocks); its tile is 64 activation rows x 128 weight rows, a
+// wavefront owns 2 x 2 tiles of 32 x 32.  Stages move global -> registers ->
+// LDS: the loads for stage s+2 are issued before stage s is computed and
+// stage s+1 is written to the other LDS buffer after it, then one barrier.
+// The k-waves' partials meet in LDS (even + odd); the order depends on nb
+// alone, so a row's result never depends on m.
+template <int DT>
+__global__ __launch_bounds__(256, 2) void k_gemm(WeightView w, GemmPlanes gp, ActView a, int m, int n,
+                                                 const float *__restrict__ bias, float *__restrict__ out) {
+  using L = GL<DT>;
+  constexpr int TM = 2, TN = 2;
+  __shared__ __align__(16) uint8_t lds[L::LDS];
+  const int t = threadIdx.x, l = t & 63, wv = t >> 6;
   const int h = l >> 5, r = l & 31;
-  const int tile = wv / SK, part = wv % SK;
-  // XCD-aware order: consecutive workgroup ids go to different XCDs (id % 8),
-  // so hand each XCD one contiguous band of the row-major tile order; its L2
-  // then holds one band of activation rows instead of all of them.
+  const int nw = wv & 1, kw = wv >> 1;
   int bx, by;
   {
+    // XCD-aware order: consecutive workgroup ids go to different XCDs (id % 8);
+    // each XCD gets one contiguous band of the row-major tile order, so its
+    // L2 holds one band of activation rows.
     const int nx = gridDim.x, total = nx * gridDim.y;
     const int id = blockIdx.y * nx + blockIdx.x;
     const int per = total / 8, rem = total % 8, xcd = id % 8, slot = id / 8;
@@ -815,21 +702,67 @@ __global__ __launch_bounds__(256, 2) void k_gemm2(WeightView w, GemmPlanes gp, A
     bx = lin % nx;
     by = lin / nx;
   }
-  int ct_raw[TN], ct[TN], rt[TM];
+  const int nb = w.nb, ns = (nb + 1) >> 1;
+
+  // per-thread copy plan: chunk c = t + 256u of a stage comes from
+  // src[u] + bl * stride[u] (bl = min(2s + kwc[u], nb - 1)) and goes to LDS
+  // byte dst[u] of the stage; chunks past the stage re-read chunk 0 and are
+  // not stored, so every load is unconditional
+  const uint8_t *src[L::LPT];
+  int stride[L::LPT], kwc[L::LPT], dst[L::LPT];
+  bool cok[L::LPT];
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    ct_raw[j] = (bx * TILES + tile) * TN + j;
-    ct[j] = ct_raw[j] < w.ngroups ? ct_raw[j] : w.ngroups - 1;
+  for (int u = 0; u < L::LPT; ++u) {
+    const int c0 = t + 256 * u;
+    cok[u] = c0 < L::NCH;
+    const int c = cok[u] ? c0 : t;
+    kwc[u] = c / L::KWC;
+    const int cc = c % L::KWC;
+    const int kbase = kwc[u] * L::KW_BYTES;
+    if (cc < 2 * L::A_CH) {
+      const int i = cc / L::A_CH, q = cc % L::A_CH;
+      const int g = min(by * TM + i, a.mgroups - 1);
+      src[u] = reinterpret_cast<const uint8_t *>(a.a16 + act_slot(a.nb, g, 0, 0) * QK) + 16 * q;
+      stride[u] = RG * QK * 2;
+      dst[u] = kbase + i * L::A_BYTES + (q / L::A_ROWC) * L::A_PITCH + (q % L::A_ROWC) * 16;
+    } else {
+      const int cb = cc - 2 * L::A_CH;
+      const int j = cb / L::B_CH, q = cb % L::B_CH;
+      const int g = min(bx * 2 * TN + j, w.ngroups - 1);
+      const size_t s0 = qs_slot(w, g, 0, 0);
+      const int gbase = kbase + 2 * L::A_BYTES + j * L::B_BYTES;
+      if (q < L::B_QSCH) {
+        src[u] = w.qs + s0 * L::QSB + 16 * q;
+        stride[u] = RG * L::QSB;
+        dst[u] = gbase + 16 * q;
+      } else if (q < L::B_QSCH + L::B_QHCH) {
+        src[u] = reinterpret_cast<const uint8_t *>(gp.qhb + s0) + 16 * (q - L::B_QSCH);
+        stride[u] = RG * 4;
+        dst[u] = gbase + L::B_QS + 16 * (q - L::B_QSCH);
+      } else {
+        src[u] = reinterpret_cast<const uint8_t *>(gp.dm + s0) + 16 * (q - L::B_QSCH - L::B_QHCH);
+        stride[u] = RG * 4;
+        dst[u] = gbase + L::B_QS + L::B_QH + 16 * (q - L::B_QSCH - L::B_QHCH);
+      }
+    }
   }
+  struct Regs {
+    uint4 v[L::LPT];
+  };
+  auto load_stage = [&](int s) __attribute__((always_inline)) {
+    Regs x;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int t = by * TM + i;
-    rt[i] = t < a.mgroups ? t : a.mgroups - 1;
-  }
-  const int nb = w.nb;
-  const int npairs = (nb + 1) >> 1;
-  const int p0 = (npairs * part) / SK, p1 = (npairs * (part + 1)) / SK;
-  const int b1 = 2 * p1 < nb ? 2 * p1 : nb;
+    for (int u = 0; u < L::LPT; ++u) {
+      const int bl = min(2 * s + kwc[u], nb - 1);
+      x.v[u] = *reinterpret_cast<const uint4 *>(src[u] + (size_t)bl * stride[u]);
+    }
+    return x;
+  };
+  auto store_stage = [&](int buf, Regs x) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < L::LPT; ++u)
+      if (cok[u]) *reinterpret_cast<uint4 *>(lds + buf * L::STAGE + dst[u]) = x.v[u];
+  };
 
   v16f acc[TM][TN];
 #pragma unroll
@@ -837,89 +770,96 @@ __global__ __launch_bounds__(256, 2) void k_gemm2(WeightView w, GemmPlanes gp, A
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = (v16f){};
 
-  if (p0 < p1) {
-    BlockOps<TM, TN> cur;
-    load_block_ops<DT, TM, TN>(cur, w, gp, a, rt, ct, 2 * p0, r, h);
-    for (int pr = p0; pr < p1; ++pr) {
-      // min-term operands of this pair (lane half h carries block 2*pr + h),
-      // issued now and consumed after both blocks; the load is unconditional
-      // (an odd last block re-reads block nb-1 and is zeroed after)
-      const int mbl = 2 * pr + h;
-      const bool mok = mbl < nb;
-      const int mld = mok ? mbl : nb - 1;
-      uint32_t msv[TN];
-      uint4 pv[TM];
-      if (has_min(DT)) {
-#pragma unroll
-        for (int j = 0; j < TN; ++j) msv[j] = gp.msp[qs_slot(w, ct[j], mld, r)];
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-          pv[i] = *reinterpret_cast<const uint4 *>(a.pm16 + act_slot(a.nb, rt[i], mld, r) * 4);
-      }
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int bl = 2 * pr + half;
-        if (bl >= b1) break;
-        // prefetch the next block (the last one re-loads its own block)
-        BlockOps<TM, TN> nxt;
-        load_block_ops<DT, TM, TN>(nxt, w, gp, a, rt, ct, bl + 1 < b1 ? bl + 1 : bl, r, h);
-        gemm_block<DT, TM, TN>(acc, cur, h, true);
-        cur = nxt;
-      }
-      if (has_min(DT)) {
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          const uint4 pz = mok ? pv[i] : make_uint4(0u, 0u, 0u, 0u);
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, pz),
-                                                                bf16x8(msv[j], msv[j], msv[j], 0u), acc[i][j], 0,
-                                                                0, 0);
-        }
-      }
-    }
-  }
-
-  if (SK > 1) {
-    __shared__ float red[SK > 1 ? SK - 1 : 1][TILES][TM * TN * 16][64];
-    if (part > 0) {
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) red[part - 1][tile][(i * TN + j) * 16 + v][l] = acc[i][j][v];
-    }
-    __syncthreads();
-    if (part > 0) return;
-#pragma unroll 1
-    for (int p = 1; p < SK; ++p)
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) acc[i][j][v] = acc[i][j][v] + red[p - 1][tile][(i * TN + j) * 16 + v][l];
-  }
-
-#pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    if (ct_raw[j] >= w.ngroups) continue;
-    const int col = ct_raw[j] * RG + r;
-    if (col >= n) continue;
-    const float b = bias ? bias[col] : 0.0f;
+  // stage s: the loads for stage s+2 are issued before stage s computes,
+  // and `st` (stage s+1, loaded one stage ago) goes to the other LDS buffer
+  // after it.  Two stages per loop trip, so the two register sets trade
+  // roles without copies; an odd stage count gets one more stage whose
+  // blocks are all past nb ((d, m) = 0: it adds +0).
+  auto step = [&](int s, Regs st, bool more) __attribute__((always_inline)) {
+    const Regs ld = load_stage(s + 2);
+    const uint8_t *kb = lds + (s & 1) * L::STAGE + kw * L::KW_BYTES;
+    const bool valid = 2 * s + kw < nb;
+    v8h alo[TM], ahi[TM];
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      const int t = by * TM + i;
-      if (t >= a.mgroups) break;
+      const uint8_t *ap = kb + i * L::A_BYTES + r * L::A_PITCH + 32 * h;
+      alo[i] = *reinterpret_cast<const v8h *>(ap);
+      ahi[i] = *reinterpret_cast<const v8h *>(ap + 16);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const uint8_t *bg = kb + 2 * L::A_BYTES + (2 * nw + j) * L::B_BYTES;
+      uint4 qw;
+      if (DT == 8) {
+        qw = *reinterpret_cast<const uint4 *>(bg + r * 32 + 16 * h);
+      } else {
+        const uint2 v = *reinterpret_cast<const uint2 *>(bg + r * 16 + 8 * h);
+        qw = make_uint4(v.x, v.y, 0u, 0u);
+      }
+      const uint32_t qhw = L::HH ? *reinterpret_cast<const uint32_t *>(bg + L::B_QS + 4 * r) : 0u;
+      const uint32_t dmw = valid ? *reinterpret_cast<const uint32_t *>(bg + L::B_QS + L::B_QH + 4 * r) : 0u;
+      v8h q0, q1;
+      weight_f16_from<DT>(h, qw, qhw, q0, q1);
+      const h2v dmh = __builtin_bit_cast(h2v, dmw);
+      const v8h dv = dmh.x, mv = dmh.y;
+      const v8h wb0 = __builtin_elementwise_fma(q0, dv, mv);
+      const v8h wb1 = __builtin_elementwise_fma(q1, dv, mv);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo[i], wb0, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[i], wb1, acc[i][j], 0, 0, 0);
+      }
+    }
+    if (more) store_stage((s + 1) & 1, st);
+    __syncthreads();
+    return ld;
+  };
+
+  Regs ra = load_stage(0), rb = load_stage(1);
+  store_stage(0, ra);
+  __syncthreads();
+  const int ns2 = (ns + 1) & ~1;
+  for (int s = 0; s < ns2; s += 2) {
+    ra = step(s, rb, true);
+    rb = step(s + 1, ra, s + 2 < ns2);
+  }
+
+  // k-wave 1 hands its partials to k-wave 0 through LDS (the stage buffers
+  // are free after the last barrier)
+  float *red = reinterpret_cast<float *>(lds);  // [2 n-waves][64 values][64 lanes]
+  if (kw == 1) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) red[(nw * 64 + (i * TN + j) * 16 + v) * 64 + l] = acc[i][j][v];
+  }
+  __syncthreads();
+  if (kw == 1) return;
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int tg = by * TM + i;
+    if (tg >= a.mgroups) break;
+    float sc[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) sc[v] = a.rs[tg * RG + 8 * (v >> 2) + 4 * h + (v & 3)];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int cg = (bx * 2 + nw) * TN + j;
+      if (cg >= w.ngroups) continue;
+      const int col = cg * RG + r;
+      if (col >= n) continue;
+      const float b = bias ? bias[col] : 0.0f;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int row = t * RG + 8 * (v >> 2) + 4 * h + (v & 3);
+        const int row = tg * RG + 8 * (v >> 2) + 4 * h + (v & 3);
         if (row >= m) continue;
-        out[(size_t)row * n + col] = bias ? acc[i][j][v] + b : acc[i][j][v];
+        const float y = (acc[i][j][v] + red[(nw * 64 + (i * TN + j) * 16 + v) * 64 + l]) * sc[v];
+        out[(size_t)row * n + col] = bias ? y + b : y;
       }
     }
   }
 }
-
 }  // namespace rw

@@ -86,20 +86,24 @@ struct WeightView {
   int nb, nb_pad, noct, ngroups;
 };
 
+// Quantized activations.  The int8 layout (qa, da, pa, sa) serves the
+// decode kernels and the validation entries; the GEMM layout (a16, rs) the
+// encoder GEMM.  Both index (row group, block, row) by act_slot.
 struct ActView {
-  const int8_t *qa;
-  const float *da;
-  const float *pa;
-  const int32_t *sa;
-  const uint16_t *qh16;
-  const uint32_t *ds16;
-  const uint32_t *pm16;
+  const int8_t *qa;     // int8 quants, MFMA order within a block
+  const float *da;      // d_a
+  const float *pa;      // d_a * sum(q_a)
+  const int32_t *sa;    // sum(q_a)
+  const uint16_t *a16;  // f16(d_a * q_a * 2^-e_row), MFMA order
+  const float *rs;      // 2^e_row per row
   int nb, mgroups;
 };
 
+// Per-block weight planes for the encoder GEMM, indexed like qs
+// ([group][nb_pad][32]).
 struct GemmPlanes {
-  const uint32_t *dsp;
-  const uint32_t *msp;
+  const uint32_t *dm;   // f16 d_b (low half) and m_b (high half, 0 for _0 formats)
+  const uint32_t *qhb;  // permuted high-bit word (Q5)
 };
 
 // element offsets

@@ -191,94 +191,83 @@ static int stream_workspace(int device, void *stream, size_t bytes, void **out) 
 
 // ----------------------------------------------- activation workspace
 
-// The GEMM-only planes (f16 quants, bf16 splits) are written only when m is
-// in the GEMM regime; the layout depends on (m, k) alone.
+// Products with m <= GEMV_MAX_M read the int8 layout (qa, da, pa, sa); the
+// encoder GEMM reads the f16 layout (a16, rs).  The layout depends on (m, k)
+// alone; the validation entries always use the int8 one.
 constexpr size_t GEMV_MAX_M = 8;
 
 struct ActLayout {
   int nb, mgroups;
-  bool gemm;
-  size_t off_qa, off_da, off_pa, off_sa, off_q16, off_ds16, off_pm16, bytes;
+  bool f16;
+  size_t off_qa, off_da, off_pa, off_sa, off_a16, off_rs, bytes;
 };
 
-static ActLayout act_layout(size_t m, size_t k) {
+static ActLayout act_layout_kind(size_t m, size_t k, bool f16) {
   ActLayout L;
   L.nb = (int)(k / QK);
   L.mgroups = (int)cdiv(m, RG);
-  L.gemm = m > GEMV_MAX_M;
+  L.f16 = f16;
   size_t rows = (size_t)L.mgroups * RG;
   size_t nsc = rows * L.nb;
-  L.off_qa = 0;
-  L.off_da = align_up(rows * k, 256);
-  L.off_pa = align_up(L.off_da + nsc * 4, 256);
-  L.off_sa = align_up(L.off_pa + nsc * 4, 256);
-  size_t end = align_up(L.off_sa + nsc * 4, 256);
-  L.off_q16 = L.off_ds16 = L.off_pm16 = 0;
-  if (L.gemm) {
-    L.off_q16 = end;
-    L.off_ds16 = align_up(L.off_q16 + rows * k * 2, 256);
-    L.off_pm16 = align_up(L.off_ds16 + nsc * 16, 256);
-    end = align_up(L.off_pm16 + nsc * 16, 256);
+  L.off_qa = L.off_da = L.off_pa = L.off_sa = L.off_a16 = L.off_rs = 0;
+  if (f16) {
+    L.off_a16 = 0;
+    L.off_rs = align_up(rows * k * 2, 256);
+    L.bytes = align_up(L.off_rs + rows * 4, 256);
+  } else {
+    L.off_qa = 0;
+    L.off_da = align_up(rows * k, 256);
+    L.off_pa = align_up(L.off_da + nsc * 4, 256);
+    L.off_sa = align_up(L.off_pa + nsc * 4, 256);
+    L.bytes = align_up(L.off_sa + nsc * 4, 256);
   }
-  L.bytes = end;
   return L;
 }
 
+static ActLayout act_layout(size_t m, size_t k) { return act_layout_kind(m, k, m > GEMV_MAX_M); }
+
 static ActView act_view(const ActLayout &L, void *ws) {
   char *b = (char *)ws;
-  return ActView{(const int8_t *)(b + L.off_qa),
-                 (const float *)(b + L.off_da),
-                 (const float *)(b + L.off_pa),
-                 (const int32_t *)(b + L.off_sa),
-                 L.gemm ? (const uint16_t *)(b + L.off_q16) : nullptr,
-                 L.gemm ? (const uint32_t *)(b + L.off_ds16) : nullptr,
-                 L.gemm ? (const uint32_t *)(b + L.off_pm16) : nullptr,
-                 L.nb,
-                 L.mgroups};
+  ActView v{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, L.nb, L.mgroups};
+  if (L.f16) {
+    v.a16 = (const uint16_t *)(b + L.off_a16);
+    v.rs = (const float *)(b + L.off_rs);
+  } else {
+    v.qa = (const int8_t *)(b + L.off_qa);
+    v.da = (const float *)(b + L.off_da);
+    v.pa = (const float *)(b + L.off_pa);
+    v.sa = (const int32_t *)(b + L.off_sa);
+  }
+  return v;
 }
 
 // --------------------------------------------------------- launches
 
 static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &L, void *ws, hipStream_t s) {
   char *b = (char *)ws;
+  if (L.f16) {
+    const size_t rows = (size_t)L.mgroups * RG;
+    hipLaunchKernelGGL(k_quantize_f16, dim3((unsigned)rows), dim3(256), 0, s, a, (int)m, (int)k, L.nb,
+                       (uint16_t *)(b + L.off_a16), (float *)(b + L.off_rs));
+    LAUNCH_TRY("k_quantize_f16");
+    return RW_OK;
+  }
   size_t threads = (size_t)L.mgroups * RG * L.nb * 8;
   hipLaunchKernelGGL(k_quantize, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0, s, a, (int)m, (int)k, L.nb,
                      L.mgroups, (int8_t *)(b + L.off_qa), (float *)(b + L.off_da), (float *)(b + L.off_pa),
-                     (int32_t *)(b + L.off_sa), L.gemm ? (uint16_t *)(b + L.off_q16) : nullptr,
-                     L.gemm ? (uint32_t *)(b + L.off_ds16) : nullptr,
-                     L.gemm ? (uint32_t *)(b + L.off_pm16) : nullptr);
+                     (int32_t *)(b + L.off_sa));
   LAUNCH_TRY("k_quantize");
   return RW_OK;
 }
 
-// GEMM tiling: a wave tile is GEMM_TM activation row groups x GEMM_TN weight
-// row groups (32 rows each).  The k split is chosen from the weight's shape
-// alone (never from m): split more when there are few weight rows to spread.
-constexpr int GEMM_TM = 2, GEMM_TN = 2;
-static int gemm_sk(const rw_weight *w) {
-  if (w->nb < 16) return 1;
-  if (w->n <= 2048 && w->nb >= 32) return 4;
-  if (w->n <= 4096) return 2;
-  return 1;
-}
-
-template <int DT, int SK>
-static void launch_gemm_sk(const rw_weight *w, const ActView &av, int m, const float *bias, float *out,
-                           hipStream_t s) {
-  constexpr int TILES = 4 / SK;
-  dim3 grid((unsigned)cdiv(w->ngroups, TILES * GEMM_TN), (unsigned)cdiv(av.mgroups, GEMM_TM));
-  hipLaunchKernelGGL((k_gemm2<DT, GEMM_TM, GEMM_TN, SK>), grid, dim3(256), 0, s, w->view, w->gemm, av, m,
-                     (int)w->n, bias, out);
-}
-
+// GEMM: a workgroup tile is 2 activation row groups x 4 weight row groups
+// (64 x 128); the k split (even / odd blocks) is fixed, so a row's result
+// never depends on m.
 template <int DT>
 static void launch_gemm_dt(const rw_weight *w, const ActView &av, int m, const float *bias, float *out,
                            hipStream_t s) {
-  switch (gemm_sk(w)) {
-    case 4: launch_gemm_sk<DT, 4>(w, av, m, bias, out, s); break;
-    case 2: launch_gemm_sk<DT, 2>(w, av, m, bias, out, s); break;
-    default: launch_gemm_sk<DT, 1>(w, av, m, bias, out, s); break;
-  }
+  dim3 grid((unsigned)cdiv(w->ngroups, 4), (unsigned)cdiv(av.mgroups, 2));
+  hipLaunchKernelGGL((k_gemm<DT>), grid, dim3(256), 0, s, w->view, w->gemm, av, m, (int)w->n, bias, out);
 }
 
 // ------------------------------------------------------ decode GEMV
@@ -374,7 +363,7 @@ static int run_product(const rw_weight *w, size_t m, const float *bias, float *o
     LAUNCH_TRY("k_gemv2");
   } else {
     RW_DISPATCH_DT(w->dtype, launch_gemm_dt, w, av, (int)m, bias, out, s);
-    LAUNCH_TRY("k_gemm2");
+    LAUNCH_TRY("k_gemm");
   }
   return RW_OK;
 }
@@ -588,9 +577,9 @@ int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, siz
   size_t off_qh = align_up(qsz, 256);
   size_t off_d = align_up(off_qh + (has_high(dtype) ? nsc * 4 : 0), 256);
   size_t off_m = align_up(off_d + nsc * 2, 256);
-  size_t off_dsp = align_up(off_m + (has_min(dtype) ? nsc * 2 : 0), 256);
-  size_t off_msp = align_up(off_dsp + nsc * 4, 256);
-  w->bytes = align_up(off_msp + (has_min(dtype) ? nsc * 4 : 0), 256);
+  size_t off_dm = align_up(off_m + (has_min(dtype) ? nsc * 2 : 0), 256);
+  size_t off_qhb = align_up(off_dm + nsc * 4, 256);
+  w->bytes = align_up(off_qhb + (has_high(dtype) ? nsc * 4 : 0), 256);
   if (hipMalloc(&w->base, w->bytes) != hipSuccess) {
     (void)hipGetLastError();
     delete w;
@@ -599,7 +588,7 @@ int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, siz
   char *b = (char *)w->base;
   w->view = WeightView{(const uint8_t *)b, (const uint32_t *)(b + off_qh), (const uint16_t *)(b + off_d),
                        (const uint16_t *)(b + off_m), w->nb, w->nb_pad, w->noct, w->ngroups};
-  w->gemm = GemmPlanes{(const uint32_t *)(b + off_dsp), (const uint32_t *)(b + off_msp)};
+  w->gemm = GemmPlanes{(const uint32_t *)(b + off_dm), (const uint32_t *)(b + off_qhb)};
 
   void *tmp = nullptr;
   hipError_t e = hipMalloc(&tmp, raw_len);
@@ -610,7 +599,8 @@ int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, siz
 #define RW_REPACK(DT)                                                                                      \
   hipLaunchKernelGGL(k_repack<DT>, grid, dim3(256), 0, 0, (const uint8_t *)tmp, (int)n, (int)nb, (uint8_t *)b, \
                      (uint32_t *)(b + off_qh), (uint16_t *)(b + off_d), (uint16_t *)(b + off_m),                \
-                     (uint32_t *)(b + off_dsp), (uint32_t *)(b + off_msp), w->nb_pad, w->noct, w->ngroups)
+                     (uint32_t *)(b + off_dm), (uint32_t *)(b + off_qhb), w->nb_pad,                     \
+                     w->noct, w->ngroups)
     switch (dtype) {
       case RW_Q4_0: RW_REPACK(RW_Q4_0); break;
       case RW_Q4_1: RW_REPACK(RW_Q4_1); break;
@@ -867,7 +857,7 @@ int rw_rocm_quantize_acts(const float *a, size_t m, size_t k, int8_t *q, float *
   CtxGuard g;
   rc = ctx_acquire(dev, &g.c);
   if (rc) return rc;
-  ActLayout L = act_layout(m, k);
+  ActLayout L = act_layout_kind(m, k, false);
   size_t off_a = align_up(L.bytes, 256);
   rc = ctx_reserve(g.c, off_a + m * k * 4);
   if (rc) return rc;
@@ -899,7 +889,7 @@ int rw_rocm_block_dots(const rw_weight *w, const int8_t *qa, size_t m, int32_t *
   CtxGuard g;
   int rc = ctx_acquire(w->device, &g.c);
   if (rc) return rc;
-  ActLayout L = act_layout(m, w->k);
+  ActLayout L = act_layout_kind(m, w->k, false);
   size_t sbytes = m * w->n * (size_t)w->nb * 4;
   size_t off_s = align_up(L.bytes, 256);
   rc = ctx_reserve(g.c, off_s + sbytes);
