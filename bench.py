@@ -29,6 +29,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "Q-matmul TOPS @M=1500 encoder; decode GEMV HBM GB/s @M=5 (large-v3 Q5_1)"
+F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 MFMA
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 HBM_PEAK_GBS = 8000.0    # MI355X HBM3E
 
@@ -95,6 +96,34 @@ def time_encoder(A, torch, W, steps: int, warmup: int, stream):
     wall = time.perf_counter() - t0
     ms = start.elapsed_time(end) / steps
     return ms, wall
+
+
+def time_encoder_graph(A, torch, W, steps: int, warmup: int):
+    """The same step captured once in a HIP graph (torch.cuda.CUDAGraph over
+    the library's launches) and replayed: launches without host overhead,
+    as an encoder runs window after window."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        encoder_step(A, W, side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        encoder_step(A, W, torch.cuda.current_stream().cuda_stream)
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    del graph
+    return ms
 
 
 def time_gemm_kernel(A, torch, W, stream, reps: int = 2):
@@ -254,9 +283,12 @@ def main() -> int:
     dtype = synth.BY_NAME[args.quant]
 
     W = encoder_workload(A, synth, torch, dtype, args.m, seed0=1)
-    ms, wall = time_encoder(A, torch, W, args.steps, args.warmup, stream)
+    eager_ms, wall = time_encoder(A, torch, W, args.steps, args.warmup, stream)
+    eager_tops = W["ops"] / (eager_ms * 1e-3) / 1e12
+    log(f"encoder step, eager launches {eager_ms:.3f} ms  ({eager_tops:.1f} TOPS, wall {wall:.2f} s)")
+    ms = time_encoder_graph(A, torch, W, args.steps, args.warmup)
     tops = W["ops"] / (ms * 1e-3) / 1e12
-    log(f"encoder step {ms:.3f} ms  ({tops:.1f} TOPS, wall {wall:.2f} s for {args.steps} steps)")
+    log(f"encoder step, graph replay {ms:.3f} ms  ({tops:.1f} TOPS)")
 
     gemm_ms, gemm_ops, launches = time_gemm_kernel(A, torch, W, stream)
     gemm_tops = gemm_ops / (gemm_ms * 1e-3) / 1e12
@@ -270,14 +302,19 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "eager_ms_per_step": round(eager_ms, 4),
+        "launch": "one encoder step (320 launches) captured in a HIP graph and replayed; eager_ms_per_step "
+                  "launches the same kernels one by one from the host",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "i8",
+        "dtype": "f16",
         "data": "synthetic",
         "config": {
             "workload": f"large-v3 encoder linears, {args.quant}, M={args.m}: 32 layers x "
-                        f"(q,k,v,out 1280x1280; fc1 5120x1280; fc2 1280x5120), activations quantized on device",
+                        f"(q,k,v,out 1280x1280; fc1 5120x1280; fc2 1280x5120), activations quantized on device "
+                        f"to int8 blocks as the reference does, products on f16 MFMA (dequantized operands, "
+                        f"f32 accumulation)",
             "m": args.m,
             "layers": 32,
             "quant": args.quant,
@@ -286,12 +323,13 @@ def main() -> int:
         "roofline": {
             "bound": "mfma",
             "achieved": round(gemm_tops, 3),
-            "peak": INT8_PEAK_TOPS,
+            "peak": F16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": round(gemm_tops / INT8_PEAK_TOPS, 4),
+            "frac": round(gemm_tops / F16_PEAK_TFLOPS, 4),
             "traffic": None,
-            "kernel": f"k_gemm<{args.quant}> (int8 ops 2*M*N*K per launch; unit is tera-ops for int8)",
+            "kernel": f"k_gemm<{args.quant}> on v_mfma_f32_32x32x16_f16 (2*M*N*K per launch)",
             "avg_launch_us": round(gemm_ms * 1e3, 2),
+            "frac_of_int8_peak": round(gemm_tops / INT8_PEAK_TOPS, 4),
         },
     }
     del W

@@ -19,6 +19,7 @@
 // Within a kernel family a row's result never depends on m: every choice
 // of order (k splits, chunking) depends on the weight's shape alone.
 #pragma once
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
 #include "rw_layout.hpp"
@@ -239,15 +240,20 @@ __global__ __launch_bounds__(256) void k_quantize(const float *__restrict__ a, i
 // the largest value lands in [2^14, 2^15): no value overflows, and every
 // value keeps f16's full precision unless it is below 2^-28 of the row's
 // largest.  rs[row] = 2^e undoes the scaling exactly in the GEMM's epilogue.
+// Each row group of the plane is followed by GEMM_PAD_BLOCKS blocks of
+// zeros (act_slot16).
 __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ a, int m, int k, int nb,
                                                       uint16_t *__restrict__ a16, float *__restrict__ rs) {
   __shared__ float wmax[4];
   const int row = blockIdx.x;
   const int t = threadIdx.x, lb = t >> 3, lt = t & 7;
   const int g = row / RG, r = row % RG;
+  // the row's padding blocks (read past the last block by k_gemm): zeros
+  for (int bl = nb + lb; bl < nb + GEMM_PAD_BLOCKS; bl += 32)
+    *reinterpret_cast<uint2 *>(a16 + act_slot16(nb, g, bl, r) * QK + mfma_pos(4 * lt)) = make_uint2(0u, 0u);
   if (row >= m) {  // uniform per workgroup
     for (int bl = lb; bl < nb; bl += 32)
-      *reinterpret_cast<uint2 *>(a16 + act_slot(nb, g, bl, r) * QK + mfma_pos(4 * lt)) = make_uint2(0u, 0u);
+      *reinterpret_cast<uint2 *>(a16 + act_slot16(nb, g, bl, r) * QK + mfma_pos(4 * lt)) = make_uint2(0u, 0u);
     if (t == 0) rs[row] = 0.0f;
     return;
   }
@@ -278,7 +284,7 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
     if (bl < nb) {
       h2v lo2 = {(_Float16)(__fmul_rn(bq.d, (float)bq.q0) * down), (_Float16)(__fmul_rn(bq.d, (float)bq.q1) * down)};
       h2v hi2 = {(_Float16)(__fmul_rn(bq.d, (float)bq.q2) * down), (_Float16)(__fmul_rn(bq.d, (float)bq.q3) * down)};
-      *reinterpret_cast<uint2 *>(a16 + act_slot(nb, g, bl, r) * QK + mfma_pos(4 * lt)) =
+      *reinterpret_cast<uint2 *>(a16 + act_slot16(nb, g, bl, r) * QK + mfma_pos(4 * lt)) =
           make_uint2(__builtin_bit_cast(uint32_t, lo2), __builtin_bit_cast(uint32_t, hi2));
     }
   }
@@ -644,28 +650,52 @@ __device__ inline void weight_f16_from(int h, uint4 qs, uint32_t qhw, v8h &b0, v
   quants_to_f16<DT>(q, b0, b1);
 }
 
-// Stage layout of k_gemm, in bytes.  A stage holds two blocks, one per
-// k-wave; per k-wave: 2 activation row groups of f16 values (32 rows of
-// 64 B, 80 B apart so a wavefront's 16-byte reads cover every LDS bank),
-// then 4 weight row groups x {quants, high-bit words (Q5), (d, m) pairs}.
-// Each piece is a contiguous run of a device plane copied in 16-byte
-// chunks, so chunk c of a stage always comes from one plane offset plus
-// (block index) x (that plane's block stride).
-template <int DT>
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector
+// memory operations of this wavefront are outstanding, nothing else
+RW_HD constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+
+// One direct global -> LDS load of 16 bytes per lane: lane i's 16 bytes at
+// `g` land at LDS byte (m0 + 16 i); m0 (an LDS byte address) must be the
+// same in every lane.  Issued as inline asm so that the compiler's wait
+// counting never holds an LDS read for it: the caller waits (vmcnt_imm) and
+// synchronises before the data is read, and waits for all of them before
+// reusing LDS.
+__device__ inline void dma16(const void *g, uint32_t m0) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m0) : "memory");
+}
+__device__ inline uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+
+// Stage layout of k_gemm.  A stage holds KW blocks, one per k-wave, as
+// 16-byte chunks; per k-wave: TM activation row groups of f16 values (32
+// rows x 4 chunks; chunk c of row r sits at position 4r + (c ^ ((r >> 1) &
+// 3)) so the wavefront's 16-byte operand reads cover every LDS bank), then
+// 2*TN weight row groups x {quants, high-bit words (Q5), (d, m) pairs}.
+// Each piece is a contiguous run of a device plane, so chunk p of a stage
+// always comes from one plane offset plus (block index) x (that plane's
+// block stride).  A stage moves by direct global -> LDS loads of 64 chunks
+// (1 KB) per instruction, UPW per wavefront, padded with loads into an
+// unread tail.
+template <int DT, int TM, int TN, int KW_>
 struct GL {
-  static constexpr int QSB = DT == 8 ? 32 : 16;  // quant bytes per row-block
+  static constexpr int KW = KW_, WAVES = 2 * KW_;  // 2 n-waves x KW k-waves
+  static constexpr int R = 3;                      // LDS ring buffers
+  static constexpr int QSB = DT == 8 ? 32 : 16;   // quant bytes per row-block
   static constexpr bool HH = DT == 6 || DT == 7;
-  static constexpr int A_PITCH = 80, A_ROWC = 4, A_CH = RG * A_ROWC, A_BYTES = RG * A_PITCH;
-  static constexpr int B_ROWC = QSB / 16, B_QSCH = RG * B_ROWC, B_QHCH = HH ? 8 : 0, B_DMCH = 8;
+  static constexpr int A_CH = RG * 4;             // chunks per activation row group
+  static constexpr int B_QSCH = RG * QSB / 16, B_QHCH = HH ? 8 : 0, B_DMCH = 8;
   static constexpr int B_CH = B_QSCH + B_QHCH + B_DMCH;
-  static constexpr int B_QS = RG * QSB, B_QH = 16 * B_QHCH, B_BYTES = B_QS + B_QH + 16 * B_DMCH;
-  static constexpr int KW_BYTES = 2 * A_BYTES + 4 * B_BYTES;
-  static constexpr int STAGE = 2 * KW_BYTES;
-  static constexpr int KWC = 2 * A_CH + 4 * B_CH;  // chunks per k-wave
-  static constexpr int NCH = 2 * KWC;              // chunks per stage
-  static constexpr int LPT = (NCH + 255) / 256;    // chunks per thread per stage
-  static constexpr int RED = 2 * 64 * 64 * 4;      // k-wave reduction buffer
-  static constexpr int LDS = 2 * STAGE > RED ? 2 * STAGE : RED;
+  static constexpr int KWC = TM * A_CH + 2 * TN * B_CH;  // chunks per k-wave
+  static constexpr int NCH = KW * KWC;                   // chunks per stage
+  static constexpr int UPW = (NCH + 64 * WAVES - 1) / (64 * WAVES);
+  static constexpr int STAGE = UPW * WAVES * 1024;       // bytes per stage buffer
+  static constexpr int A_OFF = 0, B_OFF = TM * A_CH * 16, B_BYTES = B_CH * 16;
+  static constexpr int B_QH = B_QSCH * 16, B_DM = (B_QSCH + B_QHCH) * 16;
+  static constexpr int PART = TM * TN * 16 * 64 * 4;     // one wavefront's partial sums
+  static constexpr int RED = KW > 1 ? 2 * PART : 0;      // k-wave reduction slots
+  static constexpr int LDS = R * STAGE > RED ? R * STAGE : RED;
 };
 
 // Encoder-shape GEMM (m > 8): out = rs * (A' W'^T) (+ bias), with A' the f16
@@ -674,19 +704,27 @@ struct GL {
 // single rounding).  Products of f16 operands are exact and accumulate in
 // f32 inside v_mfma_f32_32x32x16_f16, so |y - exact| <= 2^-10 sum|a||w|
 // plus the f32 accumulation error.
-// A workgroup is 4 wavefronts: 2 along n (64 weight rows each) x 2 along k
-// (even / odd blocks); its tile is 64 activation rows x 128 weight rows, a
-// wavefront owns 2 x 2 tiles of 32 x 32.  Stages move global -> registers ->
-// LDS: the loads for stage s+2 are issued before stage s is computed and
-// stage s+1 is written to the other LDS buffer after it, then one barrier.
-// The k-waves' partials meet in LDS (even + odd); the order depends on nb
-// alone, so a row's result never depends on m.
-template <int DT>
-__global__ __launch_bounds__(256, 2) void k_gemm(WeightView w, GemmPlanes gp, ActView a, int m, int n,
-                                                 const float *__restrict__ bias, float *__restrict__ out) {
-  using L = GL<DT>;
-  constexpr int TM = 2, TN = 2;
-  __shared__ __align__(16) uint8_t lds[L::LDS];
+// A workgroup is 2*KW wavefronts: 2 along n x KW along k (block bl goes to
+// k-wave bl % KW); a wavefront owns TM x TN tiles of 32 x 32, the workgroup
+// tile is 32*TM activation rows x 64*TN weight rows.  Stages stream through
+// a ring of 3 LDS buffers by direct global -> LDS loads, two stages ahead:
+// at stage s a wavefront waits for its own loads of stage s, the barrier
+// makes the whole stage visible (and frees the buffer of stage s-1), it
+// reads its operands, issues stage s+2 and computes.  Each lane's load
+// addresses advance by a fixed stride per stage, which runs up to 5*KW
+// blocks past a row group's last block: into the activation plane's zeroed
+// per-group padding and the weight planes' tail padding (or the next
+// weight group), where the block gets zero (d, m), so it adds +0.  The k-waves'
+// partials are summed from the last k-wave down (((p3 + p2) + p1) + p0);
+// the configuration and the order depend on the weight alone, so a row's
+// result never depends on m.
+template <int DT, int TM, int TN, int KW>
+__global__ __launch_bounds__(128 * KW, 2) void k_gemm(WeightView w, GemmPlanes gp, ActView a, int m, int n,
+                                                      const float *__restrict__ bias, float *__restrict__ out) {
+  using L = GL<DT, TM, TN, KW>;
+  static_assert(5 * KW <= GEMM_PAD_BLOCKS, "loads past the last block stay in the padding");
+  constexpr int UPW = L::UPW, R = L::R;
+  __shared__ __align__(1024) uint8_t lds[L::LDS];
   const int t = threadIdx.x, l = t & 63, wv = t >> 6;
   const int h = l >> 5, r = l & 31;
   const int nw = wv & 1, kw = wv >> 1;
@@ -702,66 +740,60 @@ __global__ __launch_bounds__(256, 2) void k_gemm(WeightView w, GemmPlanes gp, Ac
     bx = lin % nx;
     by = lin / nx;
   }
-  const int nb = w.nb, ns = (nb + 1) >> 1;
+  const int nb = w.nb, ns = (nb + KW - 1) / KW;
 
-  // per-thread copy plan: chunk c = t + 256u of a stage comes from
-  // src[u] + bl * stride[u] (bl = min(2s + kwc[u], nb - 1)) and goes to LDS
-  // byte dst[u] of the stage; chunks past the stage re-read chunk 0 and are
-  // not stored, so every load is unconditional
-  const uint8_t *src[L::LPT];
-  int stride[L::LPT], kwc[L::LPT], dst[L::LPT];
-  bool cok[L::LPT];
+  // copy plan: this lane fills stage chunk p = (wv + WAVES u) * 64 + l; its
+  // source for stage s is ptr[u] + s * step[u] (block KW s + its k-wave);
+  // chunks past the stage re-read the first activation chunk into the
+  // unread tail
+  const uint8_t *ptr[UPW];
+  uint32_t stp[UPW];
 #pragma unroll
-  for (int u = 0; u < L::LPT; ++u) {
-    const int c0 = t + 256 * u;
-    cok[u] = c0 < L::NCH;
-    const int c = cok[u] ? c0 : t;
-    kwc[u] = c / L::KWC;
-    const int cc = c % L::KWC;
-    const int kbase = kwc[u] * L::KW_BYTES;
-    if (cc < 2 * L::A_CH) {
+  for (int u = 0; u < UPW; ++u) {
+    const int p = (wv + L::WAVES * u) * 64 + l;
+    const int pc = p < L::NCH ? p : 0;
+    const int kwc = pc / L::KWC;
+    const int cc = pc % L::KWC;
+    int stride;
+    if (cc < TM * L::A_CH) {
       const int i = cc / L::A_CH, q = cc % L::A_CH;
+      const int row = q >> 2, c = (q & 3) ^ ((row >> 1) & 3);
       const int g = min(by * TM + i, a.mgroups - 1);
-      src[u] = reinterpret_cast<const uint8_t *>(a.a16 + act_slot(a.nb, g, 0, 0) * QK) + 16 * q;
-      stride[u] = RG * QK * 2;
-      dst[u] = kbase + i * L::A_BYTES + (q / L::A_ROWC) * L::A_PITCH + (q % L::A_ROWC) * 16;
+      ptr[u] = reinterpret_cast<const uint8_t *>(a.a16 + act_slot16(a.nb, g, 0, 0) * QK) + row * 64 + c * 16;
+      stride = RG * QK * 2;
     } else {
-      const int cb = cc - 2 * L::A_CH;
+      const int cb = cc - TM * L::A_CH;
       const int j = cb / L::B_CH, q = cb % L::B_CH;
       const int g = min(bx * 2 * TN + j, w.ngroups - 1);
       const size_t s0 = qs_slot(w, g, 0, 0);
-      const int gbase = kbase + 2 * L::A_BYTES + j * L::B_BYTES;
       if (q < L::B_QSCH) {
-        src[u] = w.qs + s0 * L::QSB + 16 * q;
-        stride[u] = RG * L::QSB;
-        dst[u] = gbase + 16 * q;
+        ptr[u] = w.qs + s0 * L::QSB + 16 * q;
+        stride = RG * L::QSB;
       } else if (q < L::B_QSCH + L::B_QHCH) {
-        src[u] = reinterpret_cast<const uint8_t *>(gp.qhb + s0) + 16 * (q - L::B_QSCH);
-        stride[u] = RG * 4;
-        dst[u] = gbase + L::B_QS + 16 * (q - L::B_QSCH);
+        ptr[u] = reinterpret_cast<const uint8_t *>(gp.qhb + s0) + 16 * (q - L::B_QSCH);
+        stride = RG * 4;
       } else {
-        src[u] = reinterpret_cast<const uint8_t *>(gp.dm + s0) + 16 * (q - L::B_QSCH - L::B_QHCH);
-        stride[u] = RG * 4;
-        dst[u] = gbase + L::B_QS + L::B_QH + 16 * (q - L::B_QSCH - L::B_QHCH);
+        ptr[u] = reinterpret_cast<const uint8_t *>(gp.dm + s0) + 16 * (q - L::B_QSCH - L::B_QHCH);
+        stride = RG * 4;
       }
     }
+    if (p >= L::NCH) stride = 0;
+    ptr[u] += (size_t)kwc * stride;
+    stp[u] = (uint32_t)(KW * stride);
   }
-  struct Regs {
-    uint4 v[L::LPT];
-  };
-  auto load_stage = [&](int s) __attribute__((always_inline)) {
-    Regs x;
+  // LDS destinations of this wavefront's loads, per ring buffer (uniform)
+  uint32_t m0[R][UPW];
 #pragma unroll
-    for (int u = 0; u < L::LPT; ++u) {
-      const int bl = min(2 * s + kwc[u], nb - 1);
-      x.v[u] = *reinterpret_cast<const uint4 *>(src[u] + (size_t)bl * stride[u]);
+  for (int q = 0; q < R; ++q)
+#pragma unroll
+    for (int u = 0; u < UPW; ++u)
+      m0[q][u] = __builtin_amdgcn_readfirstlane(lds_addr(lds + q * L::STAGE + (wv + L::WAVES * u) * 1024));
+  auto issue = [&](int q) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < UPW; ++u) {
+      dma16(ptr[u], m0[q][u]);
+      ptr[u] += stp[u];
     }
-    return x;
-  };
-  auto store_stage = [&](int buf, Regs x) __attribute__((always_inline)) {
-#pragma unroll
-    for (int u = 0; u < L::LPT; ++u)
-      if (cok[u]) *reinterpret_cast<uint4 *>(lds + buf * L::STAGE + dst[u]) = x.v[u];
   };
 
   v16f acc[TM][TN];
@@ -769,38 +801,62 @@ __global__ __launch_bounds__(256, 2) void k_gemm(WeightView w, GemmPlanes gp, Ac
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = (v16f){};
+  // epilogue inputs (row scales, bias), loaded now so their latency hides
+  // under the k loop; rows and columns past the end read the last one
+  float sc[TM][16], bv[TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+      sc[i][v] = a.rs[min(by * TM + i, a.mgroups - 1) * RG + 8 * (v >> 2) + 4 * h + (v & 3)];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) bv[j] = bias ? bias[min(((bx * 2 + nw) * TN + j) * RG + r, n - 1)] : 0.0f;
 
-  // stage s: the loads for stage s+2 are issued before stage s computes,
-  // and `st` (stage s+1, loaded one stage ago) goes to the other LDS buffer
-  // after it.  Two stages per loop trip, so the two register sets trade
-  // roles without copies; an odd stage count gets one more stage whose
-  // blocks are all past nb ((d, m) = 0: it adds +0).
-  auto step = [&](int s, Regs st, bool more) __attribute__((always_inline)) {
-    const Regs ld = load_stage(s + 2);
-    const uint8_t *kb = lds + (s & 1) * L::STAGE + kw * L::KW_BYTES;
-    const bool valid = 2 * s + kw < nb;
+  // the A operand chunk positions of this lane (row r, chunks 2h, 2h+1)
+  const int sw = (r >> 1) & 3;
+  const int a_off0 = (4 * r + ((2 * h) ^ sw)) * 16, a_off1 = (4 * r + ((2 * h + 1) ^ sw)) * 16;
+  // stage s lives in buffer s % 3; the stage count is padded to a multiple
+  // of 3 with stages whose blocks are all past nb ((d, m) = 0: they add +0).
+  // A step reads all of its operands from LDS before it issues stage s+2.
+  auto step = [&](int q, int s) __attribute__((always_inline)) {
+    // own loads of stage s done, then everyone's (and stage s-1 read by all);
+    // the empty asm statements keep every LDS access on its side of the
+    // barrier
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(UPW));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const uint8_t *kb = lds + q * L::STAGE + kw * L::KWC * 16;
+    const bool valid = KW * s + kw < nb;
     v8h alo[TM], ahi[TM];
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      const uint8_t *ap = kb + i * L::A_BYTES + r * L::A_PITCH + 32 * h;
-      alo[i] = *reinterpret_cast<const v8h *>(ap);
-      ahi[i] = *reinterpret_cast<const v8h *>(ap + 16);
+      const uint8_t *ag = kb + L::A_OFF + i * L::A_CH * 16;
+      alo[i] = *reinterpret_cast<const v8h *>(ag + a_off0);
+      ahi[i] = *reinterpret_cast<const v8h *>(ag + a_off1);
     }
+    uint4 qw[TN];
+    uint32_t qhw[TN], dmw[TN];
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const uint8_t *bg = kb + 2 * L::A_BYTES + (2 * nw + j) * L::B_BYTES;
-      uint4 qw;
+      const uint8_t *bg = kb + L::B_OFF + (TN * nw + j) * L::B_BYTES;
       if (DT == 8) {
-        qw = *reinterpret_cast<const uint4 *>(bg + r * 32 + 16 * h);
+        qw[j] = *reinterpret_cast<const uint4 *>(bg + r * 32 + 16 * h);
       } else {
         const uint2 v = *reinterpret_cast<const uint2 *>(bg + r * 16 + 8 * h);
-        qw = make_uint4(v.x, v.y, 0u, 0u);
+        qw[j] = make_uint4(v.x, v.y, 0u, 0u);
       }
-      const uint32_t qhw = L::HH ? *reinterpret_cast<const uint32_t *>(bg + L::B_QS + 4 * r) : 0u;
-      const uint32_t dmw = valid ? *reinterpret_cast<const uint32_t *>(bg + L::B_QS + L::B_QH + 4 * r) : 0u;
+      qhw[j] = L::HH ? *reinterpret_cast<const uint32_t *>(bg + L::B_QH + 4 * r) : 0u;
+      dmw[j] = *reinterpret_cast<const uint32_t *>(bg + L::B_DM + 4 * r);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    issue((q + 2) % R);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
       v8h q0, q1;
-      weight_f16_from<DT>(h, qw, qhw, q0, q1);
-      const h2v dmh = __builtin_bit_cast(h2v, dmw);
+      weight_f16_from<DT>(h, qw[j], qhw[j], q0, q1);
+      const h2v dmh = __builtin_bit_cast(h2v, valid ? dmw[j] : 0u);
       const v8h dv = dmh.x, mv = dmh.y;
       const v8h wb0 = __builtin_elementwise_fma(q0, dv, mv);
       const v8h wb1 = __builtin_elementwise_fma(q1, dv, mv);
@@ -810,56 +866,67 @@ __global__ __launch_bounds__(256, 2) void k_gemm(WeightView w, GemmPlanes gp, Ac
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[i], wb1, acc[i][j], 0, 0, 0);
       }
     }
-    if (more) store_stage((s + 1) & 1, st);
-    __syncthreads();
-    return ld;
   };
-
-  Regs ra = load_stage(0), rb = load_stage(1);
-  store_stage(0, ra);
-  __syncthreads();
-  const int ns2 = (ns + 1) & ~1;
-  for (int s = 0; s < ns2; s += 2) {
-    ra = step(s, rb, true);
-    rb = step(s + 1, ra, s + 2 < ns2);
+  issue(0);
+  issue(1);
+  const int nsr = (ns + R - 1) / R * R;
+  for (int s = 0; s < nsr; s += R) {
+    step(0, s);
+    step(1, s + 1);
+    step(2, s + 2);
   }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the last (unused) stages' loads
+  __syncthreads();
 
-  // k-wave 1 hands its partials to k-wave 0 through LDS (the stage buffers
-  // are free after the last barrier)
-  float *red = reinterpret_cast<float *>(lds);  // [2 n-waves][64 values][64 lanes]
-  if (kw == 1) {
+  // partials from the last k-wave down, through LDS slots [n-wave] of PART
+  // bytes
+  float *red = reinterpret_cast<float *>(lds + nw * L::PART);
+  auto put = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) red[(nw * 64 + (i * TN + j) * 16 + v) * 64 + l] = acc[i][j][v];
+        for (int v = 0; v < 16; ++v) red[((i * TN + j) * 16 + v) * 64 + l] = acc[i][j][v];
+  };
+  auto add = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = red[((i * TN + j) * 16 + v) * 64 + l] + acc[i][j][v];
+  };
+#pragma unroll
+  for (int kk = KW - 1; kk > 0; --kk) {
+    if (kw == kk) {
+      if (kk < KW - 1) add();
+      put();
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  if (kw == 1) return;
+  if (kw != 0) return;
+  if (KW > 1) add();
 
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int tg = by * TM + i;
     if (tg >= a.mgroups) break;
-    float sc[16];
-#pragma unroll
-    for (int v = 0; v < 16; ++v) sc[v] = a.rs[tg * RG + 8 * (v >> 2) + 4 * h + (v & 3)];
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int cg = (bx * 2 + nw) * TN + j;
       if (cg >= w.ngroups) continue;
       const int col = cg * RG + r;
       if (col >= n) continue;
-      const float b = bias ? bias[col] : 0.0f;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int row = tg * RG + 8 * (v >> 2) + 4 * h + (v & 3);
         if (row >= m) continue;
-        const float y = (acc[i][j][v] + red[(nw * 64 + (i * TN + j) * 16 + v) * 64 + l]) * sc[v];
-        out[(size_t)row * n + col] = bias ? y + b : y;
+        const float y = acc[i][j][v] * sc[i][v];
+        out[(size_t)row * n + col] = bias ? y + bv[j] : y;
       }
     }
   }
 }
+
 }  // namespace rw

@@ -115,4 +115,11 @@ RW_HD inline size_t sc_index(const WeightView &w, int g, int bl, int r) {
 }
 RW_HD inline size_t act_slot(int nb, int g, int bl, int r) { return ((size_t)g * nb + bl) * RG + r; }
 
+// The encoder GEMM reads up to GEMM_PAD_BLOCKS blocks past a row group's last
+// block; its f16 activation plane gives every row group that many blocks of
+// zero padding, and every weight plane it reads carries that many blocks of
+// tail padding.
+constexpr int GEMM_PAD_BLOCKS = 20;
+RW_HD inline size_t act_slot16(int nb, int g, int bl, int r) { return act_slot(nb + GEMM_PAD_BLOCKS, g, bl, r); }
+
 }  // namespace rw

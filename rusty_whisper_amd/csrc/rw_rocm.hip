@@ -212,7 +212,7 @@ static ActLayout act_layout_kind(size_t m, size_t k, bool f16) {
   L.off_qa = L.off_da = L.off_pa = L.off_sa = L.off_a16 = L.off_rs = 0;
   if (f16) {
     L.off_a16 = 0;
-    L.off_rs = align_up(rows * k * 2, 256);
+    L.off_rs = align_up(rows * (k + (size_t)GEMM_PAD_BLOCKS * QK) * 2, 256);
     L.bytes = align_up(L.off_rs + rows * 4, 256);
   } else {
     L.off_qa = 0;
@@ -261,13 +261,32 @@ static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &
 }
 
 // GEMM: a workgroup tile is 2 activation row groups x 4 weight row groups
-// (64 x 128); the k split (even / odd blocks) is fixed, so a row's result
-// never depends on m.
+// (64 x 128) with KW wavefronts along k.  KW grows with the blocks per row
+// (about 40 blocks per wavefront) and is at least 2 when the weight has few
+// column tiles; it depends on the weight alone, so a row's result never
+// depends on m.
+static int gemm_kw(const rw_weight *w) {
+  int kw = w->nb >= 160 ? 4 : w->nb >= 80 ? 2 : 1;
+  if (cdiv(w->ngroups, 4) < 16 && kw < 2) kw = 2;
+  return kw;
+}
+
+template <int DT, int KW>
+static void launch_gemm_kw(const rw_weight *w, const ActView &av, int m, const float *bias, float *out,
+                           hipStream_t s) {
+  dim3 grid((unsigned)cdiv(w->ngroups, 4), (unsigned)cdiv(av.mgroups, 2));
+  hipLaunchKernelGGL((k_gemm<DT, 2, 2, KW>), grid, dim3(128 * KW), 0, s, w->view, w->gemm, av, m, (int)w->n, bias,
+                     out);
+}
+
 template <int DT>
 static void launch_gemm_dt(const rw_weight *w, const ActView &av, int m, const float *bias, float *out,
                            hipStream_t s) {
-  dim3 grid((unsigned)cdiv(w->ngroups, 4), (unsigned)cdiv(av.mgroups, 2));
-  hipLaunchKernelGGL((k_gemm<DT>), grid, dim3(256), 0, s, w->view, w->gemm, av, m, (int)w->n, bias, out);
+  switch (gemm_kw(w)) {
+    case 4: launch_gemm_kw<DT, 4>(w, av, m, bias, out, s); break;
+    case 2: launch_gemm_kw<DT, 2>(w, av, m, bias, out, s); break;
+    default: launch_gemm_kw<DT, 1>(w, av, m, bias, out, s); break;
+  }
 }
 
 // ------------------------------------------------------ decode GEMV
@@ -573,13 +592,14 @@ int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, siz
   w->ngroups = (int)cdiv(n, RG);
   size_t rows = (size_t)w->ngroups * RG;
   size_t nsc = rows * w->nb_pad;
-  size_t qsz = nsc * qs_bytes(dtype);
+  const size_t pad = (size_t)GEMM_PAD_BLOCKS * RG;  // tail padding read by k_gemm (slots)
+  size_t qsz = (nsc + pad) * qs_bytes(dtype);
   size_t off_qh = align_up(qsz, 256);
   size_t off_d = align_up(off_qh + (has_high(dtype) ? nsc * 4 : 0), 256);
   size_t off_m = align_up(off_d + nsc * 2, 256);
   size_t off_dm = align_up(off_m + (has_min(dtype) ? nsc * 2 : 0), 256);
-  size_t off_qhb = align_up(off_dm + nsc * 4, 256);
-  w->bytes = align_up(off_qhb + (has_high(dtype) ? nsc * 4 : 0), 256);
+  size_t off_qhb = align_up(off_dm + (nsc + pad) * 4, 256);
+  w->bytes = align_up(off_qhb + (has_high(dtype) ? (nsc + pad) * 4 : 0), 256);
   if (hipMalloc(&w->base, w->bytes) != hipSuccess) {
     (void)hipGetLastError();
     delete w;

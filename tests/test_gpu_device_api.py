@@ -188,3 +188,42 @@ def test_grouped_rejects_bad_items(torch):
         A.matmul_grouped_dev(arr, ws, wsz - 1)
     with pytest.raises(A.RwError, match="m = 0"):
         A.Group(A.make_linears([(w, a, None, o, 0)]))
+
+
+@pytest.mark.parametrize("dtype,n,m", [(7, 96, 5), (7, 160, 70), (2, 64, 9), (8, 33, 1)])
+def test_graph_replay_matches_eager(torch, dtype, n, m):
+    # the library's launches (separate quantize + product, and the fused
+    # decode call) captured in a HIP graph and replayed three times with eager
+    # work in between: every replay bitwise equal to the eager result
+    k = 1280
+    raw = weights(dtype, n, k, seed=60 + m)
+    w = A.DeviceWeight(dtype, n, k, raw)
+    a = _dev(torch, activations(m, k, seed=61 + m))
+    bias = _dev(torch, np.random.default_rng(m).standard_normal(n).astype(np.float32))
+    wsz = A.workspace_size(m, k)
+    ws = torch.empty(wsz, dtype=torch.uint8, device="cuda:0")
+    out1 = torch.empty(m, n, device="cuda:0")
+    out2 = torch.empty(m, n, device="cuda:0")
+
+    def calls(stream):
+        A.quantize_dev(a, m, k, ws, wsz, stream)
+        w.matmul_prequant_dev(ws, m, out1, bias, stream)
+        w.matmul_dev(a, m, out2, None, ws, wsz, stream)
+
+    calls(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    ref1, ref2 = out1.cpu().numpy().copy(), out2.cpu().numpy().copy()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        calls(torch.cuda.current_stream().cuda_stream)
+    for rep in range(3):
+        out1.fill_(float("nan"))
+        out2.fill_(float("nan"))
+        junk = torch.randn(1 << 16, device="cuda:0").sum()  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(out1.cpu().numpy()), _bits(ref1)), rep
+        assert np.array_equal(_bits(out2.cpu().numpy()), _bits(ref2)), rep
+        del junk
+    del graph

@@ -346,3 +346,46 @@ def test_matmul_t_q_parallel_matches_serial():
     par = w.matmul(a)
     one = w.matmul(a[:1])
     assert np.array_equal(par[0].view(np.uint32), one[0].view(np.uint32))
+
+
+# encoder-regime shapes that select each k split of the GEMM (1, 2 and 4
+# wavefronts along k) and an odd block count (the pipeline's tail reads past
+# the last block)
+KSPLIT_SHAPES = [
+    (70, 1280, 2080),  # nb 40, 65 weight row groups: split 1
+    (40, 2560, 100),   # nb 80: split 2
+    (40, 5120, 96),    # nb 160: split 4
+    (33, 5152, 70),    # nb 161: split 4, odd
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: NAMES[d])
+@pytest.mark.parametrize("m,k,n", KSPLIT_SHAPES, ids=lambda s: str(s))
+def test_gemm_k_splits(dtype, m, k, n):
+    a = activations(m, k, seed=m + k + dtype, outliers=0.01)
+    raw = weights(dtype, n, k, seed=n + k + dtype)
+    bias = np.random.default_rng(5).standard_normal(n).astype(np.float32)
+    w = A.DeviceWeight(dtype, n, k, raw)
+    got = w.matmul(a, bias)
+    ref = O.matmul_emul(a, dtype, raw, n, bias=bias)
+    assert rel_row_l2(got, ref) <= NORTH_STAR_TOL
+    _check_combine(got, a, dtype, raw, n, bias)
+    # a row's result does not depend on m
+    assert np.array_equal(w.matmul(a[:9], bias).view(np.uint32), got[:9].view(np.uint32))
+
+
+@pytest.mark.parametrize("m", [5, 70])
+def test_nonfinite_input_stays_in_its_row(m):
+    # an inf activation makes its own row non-finite (as in the reference:
+    # d_a = inf) and leaves every other row bitwise unchanged
+    k, n = 1312, 96  # nb 41: the GEMM reads past the last block
+    raw = weights(7, n, k, seed=8)
+    w = A.DeviceWeight(7, n, k, raw)
+    a = activations(m, k, seed=9)
+    clean = w.matmul(a)
+    a2 = a.copy()
+    a2[3, 1300] = np.inf
+    dirty = w.matmul(a2)
+    others = [i for i in range(m) if i != 3]
+    assert np.array_equal(dirty[others].view(np.uint32), clean[others].view(np.uint32))
+    assert not np.all(np.isfinite(dirty[3]))
