@@ -244,6 +244,7 @@ __global__ __launch_bounds__(256) void k_quantize(const float *__restrict__ a, i
 // zeros (act_slot16).
 __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ a, int m, int k, int nb,
                                                       uint16_t *__restrict__ a16, float *__restrict__ rs) {
+  constexpr int KEEP = 8;  // passes of 32 blocks held in registers (k <= 8192)
   __shared__ float wmax[4];
   const int row = blockIdx.x;
   const int t = threadIdx.x, lb = t >> 3, lt = t & 7;
@@ -258,8 +259,16 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
     return;
   }
   const float *x = a + (size_t)row * k;
+  float4 xv[KEEP];
   float amax = 0.0f;
-  for (int bl = lb; bl < nb; bl += 32) {
+#pragma unroll
+  for (int p = 0; p < KEEP; ++p) {
+    const int bl = 32 * p + lb;
+    xv[p] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (bl < nb) xv[p] = *reinterpret_cast<const float4 *>(x + (size_t)bl * QK + 4 * lt);
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(xv[p].x), fabsf(xv[p].y)), fmaxf(fabsf(xv[p].z), fabsf(xv[p].w))));
+  }
+  for (int bl = 32 * KEEP + lb; bl < nb; bl += 32) {
     const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)bl * QK + 4 * lt);
     amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
   }
@@ -276,10 +285,7 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
   const float down = ldexpf(1.0f, 15 - e);
   // whole wavefronts run every pass (the shuffles need all 8 lanes of a
   // block); lanes past the row's blocks quantize zeros and store nothing
-  for (int b0 = 0; b0 < nb; b0 += 32) {
-    const int bl = b0 + lb;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (bl < nb) v = *reinterpret_cast<const float4 *>(x + (size_t)bl * QK + 4 * lt);
+  auto emit = [&](float4 v, int bl) __attribute__((always_inline)) {
     const BlockQuant bq = quantize_block8(v);
     if (bl < nb) {
       h2v lo2 = {(_Float16)(__fmul_rn(bq.d, (float)bq.q0) * down), (_Float16)(__fmul_rn(bq.d, (float)bq.q1) * down)};
@@ -287,6 +293,15 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
       *reinterpret_cast<uint2 *>(a16 + act_slot16(nb, g, bl, r) * QK + mfma_pos(4 * lt)) =
           make_uint2(__builtin_bit_cast(uint32_t, lo2), __builtin_bit_cast(uint32_t, hi2));
     }
+  };
+#pragma unroll
+  for (int p = 0; p < KEEP; ++p)
+    if (32 * p < nb) emit(xv[p], 32 * p + lb);
+  for (int b0 = 32 * KEEP; b0 < nb; b0 += 32) {
+    const int bl = b0 + lb;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (bl < nb) v = *reinterpret_cast<const float4 *>(x + (size_t)bl * QK + 4 * lt);
+    emit(v, bl);
   }
   if (t == 0) rs[row] = ldexpf(1.0f, e - 15);
 }
@@ -358,6 +373,11 @@ __device__ inline uint4 ldg_u4(const void *p) {
   const rw_u32x4 v = *(const rw_u32x4 RW_GLOBAL_AS *)p;
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+typedef uint32_t rw_u32x2 __attribute__((ext_vector_type(2)));
+__device__ inline uint2 ldg_u2(const void *p) {
+  const rw_u32x2 v = *(const rw_u32x2 RW_GLOBAL_AS *)p;
+  return make_uint2(v.x, v.y);
+}
 __device__ inline float4 ldg_f4(const void *p) {
   const rw_f32x4 v = *(const rw_f32x4 RW_GLOBAL_AS *)p;
   return make_float4(v.x, v.y, v.z, v.w);
@@ -423,7 +443,8 @@ RW_HD constexpr int gemv_rec_bytes(int mr) { return (mr * 44 + 15) & ~15; }
 // arithmetic of k_quantize (so fused and separate quantization agree bit for
 // bit), `ch_oct` octets of blocks at a time, and weight rows stream past them
 // one per lane through v_dot4_i32_i8, a whole octet of loads in flight per
-// lane and the next octet prefetched.  2^lks of the 4 wavefronts split a
+// lane (four wavefronts per SIMD hide the latency; a second octet in
+// registers would cost one of them).  2^lks of the 4 wavefronts split a
 // row's octets (the split depends on the weight only); each walks its blocks
 // in increasing order whatever the chunking, and the parts meet in LDS in
 // wavefront order: a row's result depends on its weight row and activation
@@ -515,10 +536,9 @@ __global__ __launch_bounds__(256) void k_gemv2(const GemvItem *__restrict__ item
     // each loaded whole (the planes are padded to whole octets)
     const int p0 = max(o0, c0), p1 = min(o1, c1);
     if (p0 < p1) {
-      OctRegs<DT> cur, nxt;
-      load_oct<DT>(w, g, r, p0, cur);
       for (int o = p0; o < p1; ++o) {
-        load_oct<DT>(w, g, r, o + 1 < p1 ? o + 1 : o, nxt);
+        OctRegs<DT> cur;
+        load_oct<DT>(w, g, r, o, cur);
         const uint32_t dw[4] = {cur.d.x, cur.d.y, cur.d.z, cur.d.w};
         const uint32_t mw[4] = {cur.m.x, cur.m.y, cur.m.z, cur.m.w};
         const uint32_t hw[8] = {cur.h0.x, cur.h0.y, cur.h0.z, cur.h0.w, cur.h1.x, cur.h1.y, cur.h1.z, cur.h1.w};
@@ -568,7 +588,6 @@ __global__ __launch_bounds__(256) void k_gemv2(const GemvItem *__restrict__ item
             if (has_min(DT)) accm[i] = __builtin_fmaf(mb, *reinterpret_cast<const float *>(rec + PO + 4 * i), accm[i]);
           }
         }
-        cur = nxt;
       }
     }
   }
