@@ -265,6 +265,9 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="first copy this many MiB device to device (a kernel of known traffic, to scale "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -280,6 +283,13 @@ def main() -> int:
     A.init(0)
     torch.cuda.set_device(0)
     stream = torch.cuda.current_stream().cuda_stream
+    if args.copy_probe_mb:
+        src = torch.ones(args.copy_probe_mb << 18, device="cuda:0")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: {args.copy_probe_mb} MiB read + {args.copy_probe_mb} MiB written")
+        del src, dst
     dtype = synth.BY_NAME[args.quant]
 
     W = encoder_workload(A, synth, torch, dtype, args.m, seed0=1)

@@ -9,12 +9,17 @@
  *   QTensor::{row_f32,to_dense}  src/quant.rs:566-576
  *   matmul_t_q              src/quant.rs:754-1051
  *   linear_w                src/quant.rs:1054-1063
- * Each entry below names the reference function it replaces.  Arithmetic is
- * the reference's: activations are quantized per 32-block to int8 exactly as
- * quantize_acts_i8 (src/quant.rs:691-716) does, the per-block integer sums
- * sum(q_a*q_b) are exact, and each output is
+ * Each entry below names the reference function it replaces.  Activations
+ * are quantized per 32-block to int8 exactly as quantize_acts_i8
+ * (src/quant.rs:691-716) does, and each output is
  *     sum_bl d_a*d_b*S + m_b*d_a*sum(q_a)   (+ bias, added last)
- * combined in f32.
+ * with S = sum(q_a*q_b) the per-block integer sum.  Decode-shape products
+ * (m <= 8) form S exactly and combine in f32 as the reference does.
+ * Encoder-shape products (m > 8) multiply the same values as f16 operands
+ * d_a*q_a and d_b*q_b + m_b (one rounding each) with exact products and f32
+ * accumulation on the matrix cores: within 2^-10 * sum|a||w| plus f32
+ * accumulation error of the exact result, far inside the 1e-3 (row-L2)
+ * agreement with the reference CPU path.
  *
  * Conventions (the crate's existing C ABI, src/wasm.rs:25-110, returns an
  * i32 status and keeps error text separately):
@@ -96,9 +101,12 @@ int rw_rocm_matmul_t_q(const rw_weight *w, const float *a, size_t m, size_t k, c
 /* Device-resident form of rw_rocm_matmul_t_q: a, bias and out are device
  * pointers on the weight's device; the work is queued on `stream` (a
  * hipStream_t; NULL = the default stream) and the call returns without
- * waiting.  `workspace` (device memory, >= rw_rocm_matmul_workspace_size(m,
- * k) bytes) holds the quantized activations; NULL makes the library use a
- * buffer of its own for this stream (grown as needed, so it may allocate).
+ * waiting.  For m > 8, `workspace` (device memory, >=
+ * rw_rocm_matmul_workspace_size(m, k) bytes) holds the quantized
+ * activations; NULL makes the library use a buffer of its own for this
+ * stream (grown as needed, so it may allocate).  For m <= 8 the activations
+ * are quantized inside the product's one launch and `workspace` is not
+ * used.
  * Has no reference counterpart as such: it is matmul_t_q without the host
  * copies, for callers that keep activations on the device. */
 int rw_rocm_matmul_t_q_dev(const rw_weight *w, const float *a, size_t m, size_t k,
@@ -132,8 +140,8 @@ typedef struct rw_linear {
 } rw_linear;
 
 /* Run `count` independent linears, each with m <= 8 (the decode-GEMV
- * regime), in one launch per distinct (dtype, m, k-split); entries with
- * m == 0 are skipped.  Device pointers, asynchronous on `stream`.  Each
+ * regime), in one launch per distinct (dtype, m); entries with m == 0 are
+ * skipped.  Device pointers, asynchronous on `stream`.  Each
  * result is bitwise identical to the same linear run alone through
  * rw_rocm_matmul_t_q_dev.  The launch tables go to `workspace` (>=
  * rw_rocm_grouped_workspace_size bytes; NULL = a buffer of the library's own
@@ -174,8 +182,9 @@ int rw_rocm_quantize_acts(const float *a, size_t m, size_t k, int8_t *q, float *
 
 /* Validation entry: the exact per-block integer sums
  * S[i, j, bl] = sum_e qa[i, bl*32+e] * q_b[j, bl*32+e] for host int8
- * activations qa[m, k] (natural order) against W, computed with the same
- * int8 MFMA tiles as the matmul.  S is host [m, n, k/32]. */
+ * activations qa[m, k] (natural order) against W, computed on the device's
+ * int8 matrix cores (v_mfma_i32_32x32x32_i8) from the resident weight
+ * planes.  S is host [m, n, k/32]. */
 int rw_rocm_block_dots(const rw_weight *w, const int8_t *qa, size_t m, int32_t *S);
 
 /* Copy the calling thread's last error text (NUL-terminated, truncated to
