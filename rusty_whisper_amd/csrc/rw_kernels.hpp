@@ -105,7 +105,7 @@ __device__ inline void read_block(const uint8_t *p, uint16_t &d, uint16_t &m, ui
 template <int DT>
 __global__ __launch_bounds__(256) void k_repack(const uint8_t *__restrict__ raw, int n, int nb, uint8_t *qs,
                                                 uint32_t *qh, uint16_t *dd, uint16_t *mm, uint32_t *dm,
-                                                uint32_t *qhb, int nb_pad, int noct, int ngroups) {
+                                                uint8_t *q8, int nb_pad, int noct, int ngroups) {
   constexpr int BB = DT == 2 ? 18 : DT == 3 ? 20 : DT == 6 ? 22 : DT == 7 ? 24 : 34;
   constexpr int QSB = DT == 8 ? 32 : 16;
   size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -120,22 +120,30 @@ __global__ __launch_bounds__(256) void k_repack(const uint8_t *__restrict__ raw,
   if (j < n && bl < nb) read_block<DT>(raw + ((size_t)j * nb + bl) * BB, d, m, h, q);
   WeightView w{nullptr, nullptr, nullptr, nullptr, nb, nb_pad, noct, ngroups};
   int g = j / RG, r = j % RG;
-  uint8_t *dst = qs + qs_slot(w, g, bl, r) * QSB;
+  const size_t slot = qs_slot(w, g, bl, r);
+  uint8_t *dst = qs + slot * QSB;
   if (DT == 8) {
     for (int p = 0; p < 32; ++p) dst[p] = q[mfma_pos(p)];
   } else {
     for (int p = 0; p < 16; ++p) dst[p] = q[p];
+    // the GEMM's byte plane: element e = low nibble of byte e (e < 16) or
+    // high nibble of byte e - 16, plus its fifth bit for Q5
+    uint8_t *d8 = q8 + slot * 32;
+    for (int p = 0; p < 32; ++p) {
+      const int e = mfma_pos(p);
+      uint32_t v = (q[e & 15] >> (4 * (e >> 4))) & 15u;
+      if (has_high(DT)) v |= ((h >> e) & 1u) << 4;
+      d8[p] = (uint8_t)v;
+    }
   }
   size_t si = sc_index(w, g, bl, r);
   dd[si] = d;
   if (has_min(DT)) mm[si] = m;
-  const size_t slot = qs_slot(w, g, bl, r);
   dm[slot] = (uint32_t)d | ((uint32_t)m << 16);
   if (has_high(DT)) {
     uint32_t x = 0;
     for (int e = 0; e < 32; ++e) x |= ((h >> e) & 1u) << qh_bit(e);
     qh[si] = x;
-    qhb[slot] = x;
   }
 }
 
@@ -235,13 +243,11 @@ __global__ __launch_bounds__(256) void k_quantize(const float *__restrict__ a, i
 // Activations for the encoder GEMM, one workgroup per row of the padded
 // row groups (rows >= m are written as zeros); 8 lanes per block, 32 blocks
 // per pass.  The quantization is quantize_acts_i8's (src/quant.rs:691-716)
-// bit for bit; each element is stored as f16(d_a * q_a * 2^-e), in the MFMA
-// order of the int8 layout, with e chosen from the row's largest |x| so that
-// the largest value lands in [2^14, 2^15): no value overflows, and every
-// value keeps f16's full precision unless it is below 2^-28 of the row's
-// largest.  rs[row] = 2^e undoes the scaling exactly in the GEMM's epilogue.
-// Each row group of the plane is followed by GEMM_PAD_BLOCKS blocks of
-// zeros (act_slot16).
+// bit for bit; each element is stored as f16(d_a * q_a * 2^-e), at its
+// a16_index position, with e chosen from the row's largest |x| so that the
+// largest value lands in [2^14, 2^15): no value overflows, and every value
+// keeps f16's full precision unless it is below 2^-28 of the row's largest.
+// rs[row] = 2^e undoes the scaling exactly in the GEMM's epilogue.
 __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ a, int m, int k, int nb,
                                                       uint16_t *__restrict__ a16, float *__restrict__ rs) {
   constexpr int KEEP = 8;  // passes of 32 blocks held in registers (k <= 8192)
@@ -249,12 +255,9 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
   const int row = blockIdx.x;
   const int t = threadIdx.x, lb = t >> 3, lt = t & 7;
   const int g = row / RG, r = row % RG;
-  // the row's padding blocks (read past the last block by k_gemm): zeros
-  for (int bl = nb + lb; bl < nb + GEMM_PAD_BLOCKS; bl += 32)
-    *reinterpret_cast<uint2 *>(a16 + act_slot16(nb, g, bl, r) * QK + mfma_pos(4 * lt)) = make_uint2(0u, 0u);
   if (row >= m) {  // uniform per workgroup
     for (int bl = lb; bl < nb; bl += 32)
-      *reinterpret_cast<uint2 *>(a16 + act_slot16(nb, g, bl, r) * QK + mfma_pos(4 * lt)) = make_uint2(0u, 0u);
+      *reinterpret_cast<uint2 *>(a16 + a16_index(nb, g, bl, r, 4 * lt)) = make_uint2(0u, 0u);
     if (t == 0) rs[row] = 0.0f;
     return;
   }
@@ -290,7 +293,7 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
     if (bl < nb) {
       h2v lo2 = {(_Float16)(__fmul_rn(bq.d, (float)bq.q0) * down), (_Float16)(__fmul_rn(bq.d, (float)bq.q1) * down)};
       h2v hi2 = {(_Float16)(__fmul_rn(bq.d, (float)bq.q2) * down), (_Float16)(__fmul_rn(bq.d, (float)bq.q3) * down)};
-      *reinterpret_cast<uint2 *>(a16 + act_slot16(nb, g, bl, r) * QK + mfma_pos(4 * lt)) =
+      *reinterpret_cast<uint2 *>(a16 + a16_index(nb, g, bl, r, 4 * lt)) =
           make_uint2(__builtin_bit_cast(uint32_t, lo2), __builtin_bit_cast(uint32_t, hi2));
     }
   };
@@ -646,107 +649,68 @@ __device__ inline void quants_to_f16(const uint32_t (&q)[4], v8h &b0, v8h &b1) {
   b1 = (v8h){e[4].x, e[4].y, e[5].x, e[5].y, e[6].x, e[6].y, e[7].x, e[7].y};
 }
 
-// The B operand of the two f16 MFMAs of one block for lane half h: items
-// 0-7 (first MFMA) are elements 8h..8h+7, items 8-15 (second MFMA) elements
-// 16+8h..16+8h+7 -- the order of the activation f16 plane.
-template <int DT>
-__device__ inline void weight_f16_from(int h, uint4 qs, uint32_t qhw, v8h &b0, v8h &b1) {
-  uint32_t q[4];
-  if (DT == 8) {
-    q[0] = qs.x ^ 0x80808080u; q[1] = qs.y ^ 0x80808080u; q[2] = qs.z ^ 0x80808080u; q[3] = qs.w ^ 0x80808080u;
-  } else {
-    q[0] = qs.x & 0x0f0f0f0fu;
-    q[1] = qs.y & 0x0f0f0f0fu;
-    q[2] = (qs.x >> 4) & 0x0f0f0f0fu;
-    q[3] = (qs.y >> 4) & 0x0f0f0f0fu;
-    if (has_high(DT)) {
-      q[0] |= rotl(qhw, 2 * h) & 0x10101010u;
-      q[1] |= rotl(qhw, 2 * h + 1) & 0x10101010u;
-      q[2] |= rotl(qhw, 4 + 2 * h) & 0x10101010u;
-      q[3] |= rotl(qhw, 5 + 2 * h) & 0x10101010u;
-    }
-  }
-  quants_to_f16<DT>(q, b0, b1);
-}
-
 // s_waitcnt immediate (gfx9 encoding) that waits until at most n vector
 // memory operations of this wavefront are outstanding, nothing else
 RW_HD constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
-// One direct global -> LDS load of 16 bytes per lane: lane i's 16 bytes at
-// `g` land at LDS byte (m0 + 16 i); m0 (an LDS byte address) must be the
-// same in every lane.  Issued as inline asm so that the compiler's wait
-// counting never holds an LDS read for it: the caller waits (vmcnt_imm) and
-// synchronises before the data is read, and waits for all of them before
-// reusing LDS.
-__device__ inline void dma16(const void *g, uint32_t m0) {
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m0) : "memory");
-}
-__device__ inline uint32_t lds_addr(const void *p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
-}
-
-
-// Stage layout of k_gemm.  A stage holds KW blocks, one per k-wave, as
-// 16-byte chunks; per k-wave: TM activation row groups of f16 values (32
-// rows x 4 chunks; chunk c of row r sits at position 4r + (c ^ ((r >> 1) &
-// 3)) so the wavefront's 16-byte operand reads cover every LDS bank), then
-// 2*TN weight row groups x {quants, high-bit words (Q5), (d, m) pairs}.
-// Each piece is a contiguous run of a device plane, so chunk p of a stage
-// always comes from one plane offset plus (block index) x (that plane's
-// block stride).  A stage moves by direct global -> LDS loads of 64 chunks
-// (1 KB) per instruction, UPW per wavefront, padded with loads into an
-// unread tail.
-template <int DT, int TM, int TN, int KW_>
-struct GL {
-  static constexpr int KW = KW_, WAVES = 2 * KW_;  // 2 n-waves x KW k-waves
-  static constexpr int R = 3;                      // LDS ring buffers
-  static constexpr int QSB = DT == 8 ? 32 : 16;   // quant bytes per row-block
-  static constexpr bool HH = DT == 6 || DT == 7;
-  static constexpr int A_CH = RG * 4;             // chunks per activation row group
-  static constexpr int B_QSCH = RG * QSB / 16, B_QHCH = HH ? 8 : 0, B_DMCH = 8;
-  static constexpr int B_CH = B_QSCH + B_QHCH + B_DMCH;
-  static constexpr int KWC = TM * A_CH + 2 * TN * B_CH;  // chunks per k-wave
-  static constexpr int NCH = KW * KWC;                   // chunks per stage
-  static constexpr int UPW = (NCH + 64 * WAVES - 1) / (64 * WAVES);
-  static constexpr int STAGE = UPW * WAVES * 1024;       // bytes per stage buffer
-  static constexpr int A_OFF = 0, B_OFF = TM * A_CH * 16, B_BYTES = B_CH * 16;
-  static constexpr int B_QH = B_QSCH * 16, B_DM = (B_QSCH + B_QHCH) * 16;
-  static constexpr int PART = TM * TN * 16 * 64 * 4;     // one wavefront's partial sums
-  static constexpr int RED = KW > 1 ? 2 * PART : 0;      // k-wave reduction slots
-  static constexpr int LDS = R * STAGE > RED ? R * STAGE : RED;
+// One lane's operands of one block of k_gemm: A (its 16-byte chunk of each
+// of the two MFMAs, for TM activation row groups) and B raw (its 16 quant
+// bytes and the block's (d, m), for TN weight row groups).
+template <int TM, int TN>
+struct GemmStage {
+  uint4 a[TM][2];
+  uint4 q[TN];
+  uint32_t dm[TN];
 };
+template <int TN>
+struct GemmB {
+  v8h b[TN][2];
+};
+
+// B operands of one block for lane half h: the 16 quant bytes (MFMA order)
+// -> exact centered quants in f16 -> f16(d_b * q_b + m_b), one rounding
+template <int DT>
+__device__ inline void weight_f16(uint4 qb, uint32_t dmw, v8h &b0, v8h &b1) {
+  uint32_t q[4] = {qb.x, qb.y, qb.z, qb.w};
+  if (DT == 8) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) q[t] ^= 0x80808080u;
+  }
+  v8h q0, q1;
+  quants_to_f16<DT>(q, q0, q1);
+  const h2v dmh = __builtin_bit_cast(h2v, dmw);
+  const v8h dv = dmh.x, mv = dmh.y;
+  b0 = __builtin_elementwise_fma(q0, dv, mv);
+  b1 = __builtin_elementwise_fma(q1, dv, mv);
+}
+
+constexpr int GEMM_TM = 4, GEMM_TN = 2, GEMM_P = 2;
 
 // Encoder-shape GEMM (m > 8): out = rs * (A' W'^T) (+ bias), with A' the f16
 // values of the quantized activations (k_quantize_f16) and W' = f16(d_b*q_b
-// + m_b) formed in registers with one packed f16 fma per two weights (a
-// single rounding).  Products of f16 operands are exact and accumulate in
-// f32 inside v_mfma_f32_32x32x16_f16, so |y - exact| <= 2^-10 sum|a||w|
-// plus the f32 accumulation error.
-// A workgroup is 2*KW wavefronts: 2 along n x KW along k (block bl goes to
-// k-wave bl % KW); a wavefront owns TM x TN tiles of 32 x 32, the workgroup
-// tile is 32*TM activation rows x 64*TN weight rows.  Stages stream through
-// a ring of 3 LDS buffers by direct global -> LDS loads, two stages ahead:
-// at stage s a wavefront waits for its own loads of stage s, the barrier
-// makes the whole stage visible (and frees the buffer of stage s-1), it
-// reads its operands, issues stage s+2 and computes.  Each lane's load
-// addresses advance by a fixed stride per stage, which runs up to 5*KW
-// blocks past a row group's last block: into the activation plane's zeroed
-// per-group padding and the weight planes' tail padding (or the next
-// weight group), where the block gets zero (d, m), so it adds +0.  The k-waves'
-// partials are summed from the last k-wave down (((p3 + p2) + p1) + p0);
-// the configuration and the order depend on the weight alone, so a row's
-// result never depends on m.
-template <int DT, int TM, int TN, int KW>
-__global__ __launch_bounds__(128 * KW, 2) void k_gemm(WeightView w, GemmPlanes gp, ActView a, int m, int n,
-                                                      const float *__restrict__ bias, float *__restrict__ out) {
-  using L = GL<DT, TM, TN, KW>;
-  static_assert(5 * KW <= GEMM_PAD_BLOCKS, "loads past the last block stay in the padding");
-  constexpr int UPW = L::UPW, R = L::R;
-  __shared__ __align__(1024) uint8_t lds[L::LDS];
-  const int t = threadIdx.x, l = t & 63, wv = t >> 6;
+// + m_b) formed in registers from the byte plane with one packed f16 fma per
+// two weights (a single rounding).  Products of f16 operands are exact and
+// accumulate in f32 inside v_mfma_f32_32x32x16_f16, so |y - exact| <=
+// 2^-10 sum|a||w| plus the f32 accumulation error.
+// A workgroup owns one tile of TM activation row groups x TN weight row
+// groups (128 x 64) and has KW wavefronts, each taking every KW-th block
+// (block kw, kw + KW, ...).  A wavefront loads its operands straight into
+// registers, P blocks ahead, and needs no other wavefront until the end: no
+// LDS and no barrier in the k loop.  Each step issues the loads of block
+// s + P, then runs the 16 MFMAs of block s while the VALU dequantizes the
+// weights of block s + 1 (one MFMA, then three VALU instructions).  At the
+// end the KW partial tiles meet in LDS and are summed in kw order, each
+// wavefront finishing TM / KW row groups.  KW comes from the weight's shape
+// alone, so a row's result never depends on m.
+template <int DT, int KW>
+__global__ __launch_bounds__(64 * KW, 1) void k_gemm(WeightView w, GemmPlanes gp, ActView a, int m, int n,
+                                                     const float *__restrict__ bias, float *__restrict__ out) {
+  constexpr int TM = GEMM_TM, TN = GEMM_TN, P = GEMM_P, S = P + 1;
+  constexpr int RED = KW > 1 ? KW * TM * TN * 16 * 64 * 4 : 16;
+  __shared__ __align__(16) uint8_t lds[RED];
+  const int l = threadIdx.x & 63;
+  const int kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = l >> 5, r = l & 31;
-  const int nw = wv & 1, kw = wv >> 1;
   int bx, by;
   {
     // XCD-aware order: consecutive workgroup ids go to different XCDs (id % 8);
@@ -759,190 +723,170 @@ __global__ __launch_bounds__(128 * KW, 2) void k_gemm(WeightView w, GemmPlanes g
     bx = lin % nx;
     by = lin / nx;
   }
-  const int nb = w.nb, ns = (nb + KW - 1) / KW;
+  const int nb = w.nb;
+  const int nsw = nb > kw ? (nb - kw + KW - 1) / KW : 0;  // this wavefront's block count
 
-  // copy plan: this lane fills stage chunk p = (wv + WAVES u) * 64 + l; its
-  // source for stage s is ptr[u] + s * step[u] (block KW s + its k-wave);
-  // chunks past the stage re-read the first activation chunk into the
-  // unread tail
-  const uint8_t *ptr[UPW];
-  uint32_t stp[UPW];
+  // uniform bases at block kw (row groups past the end repeat the last one)
+  const uint8_t *abase[TM];
 #pragma unroll
-  for (int u = 0; u < UPW; ++u) {
-    const int p = (wv + L::WAVES * u) * 64 + l;
-    const int pc = p < L::NCH ? p : 0;
-    const int kwc = pc / L::KWC;
-    const int cc = pc % L::KWC;
-    int stride;
-    if (cc < TM * L::A_CH) {
-      const int i = cc / L::A_CH, q = cc % L::A_CH;
-      const int row = q >> 2, c = (q & 3) ^ ((row >> 1) & 3);
-      const int g = min(by * TM + i, a.mgroups - 1);
-      ptr[u] = reinterpret_cast<const uint8_t *>(a.a16 + act_slot16(a.nb, g, 0, 0) * QK) + row * 64 + c * 16;
-      stride = RG * QK * 2;
-    } else {
-      const int cb = cc - TM * L::A_CH;
-      const int j = cb / L::B_CH, q = cb % L::B_CH;
-      const int g = min(bx * 2 * TN + j, w.ngroups - 1);
-      const size_t s0 = qs_slot(w, g, 0, 0);
-      if (q < L::B_QSCH) {
-        ptr[u] = w.qs + s0 * L::QSB + 16 * q;
-        stride = RG * L::QSB;
-      } else if (q < L::B_QSCH + L::B_QHCH) {
-        ptr[u] = reinterpret_cast<const uint8_t *>(gp.qhb + s0) + 16 * (q - L::B_QSCH);
-        stride = RG * 4;
-      } else {
-        ptr[u] = reinterpret_cast<const uint8_t *>(gp.dm + s0) + 16 * (q - L::B_QSCH - L::B_QHCH);
-        stride = RG * 4;
-      }
-    }
-    if (p >= L::NCH) stride = 0;
-    ptr[u] += (size_t)kwc * stride;
-    stp[u] = (uint32_t)(KW * stride);
+  for (int i = 0; i < TM; ++i) {
+    const int g = min(by * TM + i, a.mgroups - 1);
+    abase[i] = reinterpret_cast<const uint8_t *>(a.a16 + a16_index(nb, g, kw, 0, 0));
   }
-  // LDS destinations of this wavefront's loads, per ring buffer (uniform)
-  uint32_t m0[R][UPW];
+  const uint8_t *qbase[TN], *dbase[TN];
 #pragma unroll
-  for (int q = 0; q < R; ++q)
+  for (int j = 0; j < TN; ++j) {
+    const int g = min(bx * TN + j, w.ngroups - 1);
+    const size_t s0 = qs_slot(w, g, kw, 0);
+    qbase[j] = gp.q8 + s0 * 32;
+    dbase[j] = reinterpret_cast<const uint8_t *>(gp.dm + s0);
+  }
+  const int aof = l * 16, qof = r * 32 + 16 * h, dof = r * 4;
+  auto load = [&](GemmStage<TM, TN> &st, int s) __attribute__((always_inline)) {
+    const size_t ao = (size_t)s * KW * 2048, qo = (size_t)s * KW * 1024, dmo = (size_t)s * KW * 128;
 #pragma unroll
-    for (int u = 0; u < UPW; ++u)
-      m0[q][u] = __builtin_amdgcn_readfirstlane(lds_addr(lds + q * L::STAGE + (wv + L::WAVES * u) * 1024));
-  auto issue = [&](int q) __attribute__((always_inline)) {
+    for (int i = 0; i < TM; ++i) {
+      st.a[i][0] = ldg_u4(abase[i] + ao + aof);
+      st.a[i][1] = ldg_u4(abase[i] + ao + 1024 + aof);
+    }
 #pragma unroll
-    for (int u = 0; u < UPW; ++u) {
-      dma16(ptr[u], m0[q][u]);
-      ptr[u] += stp[u];
+    for (int j = 0; j < TN; ++j) {
+      st.q[j] = ldg_u4(qbase[j] + qo + qof);
+      st.dm[j] = ldg_u32(dbase[j] + dmo + dof);
     }
   };
-
+  auto deq = [&](const GemmStage<TM, TN> &st) __attribute__((always_inline)) {
+    GemmB<TN> o;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) weight_f16<DT>(st.q[j], st.dm[j], o.b[j][0], o.b[j][1]);
+    return o;
+  };
   v16f acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = (v16f){};
-  // epilogue inputs (row scales, bias), loaded now so their latency hides
-  // under the k loop; rows and columns past the end read the last one
-  float sc[TM][16], bv[TN];
+  auto mma = [&](const GemmStage<TM, TN> &st, const GemmB<TN> &b) __attribute__((always_inline)) {
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int v = 0; v < 16; ++v)
-      sc[i][v] = a.rs[min(by * TM + i, a.mgroups - 1) * RG + 8 * (v >> 2) + 4 * h + (v & 3)];
-#pragma unroll
-  for (int j = 0; j < TN; ++j) bv[j] = bias ? bias[min(((bx * 2 + nw) * TN + j) * RG + r, n - 1)] : 0.0f;
-
-  // the A operand chunk positions of this lane (row r, chunks 2h, 2h+1)
-  const int sw = (r >> 1) & 3;
-  const int a_off0 = (4 * r + ((2 * h) ^ sw)) * 16, a_off1 = (4 * r + ((2 * h + 1) ^ sw)) * 16;
-  // stage s lives in buffer s % 3; the stage count is padded to a multiple
-  // of 3 with stages whose blocks are all past nb ((d, m) = 0: they add +0).
-  // A step reads all of its operands from LDS before it issues stage s+2.
-  auto step = [&](int q, int s) __attribute__((always_inline)) {
-    // own loads of stage s done, then everyone's (and stage s-1 read by all);
-    // the empty asm statements keep every LDS access on its side of the
-    // barrier
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(UPW));
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    const uint8_t *kb = lds + q * L::STAGE + kw * L::KWC * 16;
-    const bool valid = KW * s + kw < nb;
-    v8h alo[TM], ahi[TM];
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const uint8_t *ag = kb + L::A_OFF + i * L::A_CH * 16;
-      alo[i] = *reinterpret_cast<const v8h *>(ag + a_off0);
-      ahi[i] = *reinterpret_cast<const v8h *>(ag + a_off1);
-    }
-    uint4 qw[TN];
-    uint32_t qhw[TN], dmw[TN];
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const uint8_t *bg = kb + L::B_OFF + (TN * nw + j) * L::B_BYTES;
-      if (DT == 8) {
-        qw[j] = *reinterpret_cast<const uint4 *>(bg + r * 32 + 16 * h);
-      } else {
-        const uint2 v = *reinterpret_cast<const uint2 *>(bg + r * 16 + 8 * h);
-        qw[j] = make_uint4(v.x, v.y, 0u, 0u);
-      }
-      qhw[j] = L::HH ? *reinterpret_cast<const uint32_t *>(bg + L::B_QH + 4 * r) : 0u;
-      dmw[j] = *reinterpret_cast<const uint32_t *>(bg + L::B_DM + 4 * r);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    issue((q + 2) % R);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      v8h q0, q1;
-      weight_f16_from<DT>(h, qw[j], qhw[j], q0, q1);
-      const h2v dmh = __builtin_bit_cast(h2v, valid ? dmw[j] : 0u);
-      const v8h dv = dmh.x, mv = dmh.y;
-      const v8h wb0 = __builtin_elementwise_fma(q0, dv, mv);
-      const v8h wb1 = __builtin_elementwise_fma(q1, dv, mv);
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(alo[i], wb0, acc[i][j], 0, 0, 0);
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahi[i], wb1, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, st.a[i][0]), b.b[j][0],
+                                                           acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, st.a[i][1]), b.b[j][1],
+                                                           acc[i][j], 0, 0, 0);
       }
-    }
   };
-  issue(0);
-  issue(1);
-  const int nsr = (ns + R - 1) / R * R;
-  for (int s = 0; s < nsr; s += R) {
-    step(0, s);
-    step(1, s + 1);
-    step(2, s + 2);
-  }
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the last (unused) stages' loads
-  __syncthreads();
 
-  // partials from the last k-wave down, through LDS slots [n-wave] of PART
-  // bytes
-  float *red = reinterpret_cast<float *>(lds + nw * L::PART);
-  auto put = [&]() __attribute__((always_inline)) {
+  // loads never pass this wavefront's last block: later stages re-read it
+  GemmStage<TM, TN> st[S];
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+  for (int u = 0; u < P; ++u) load(st[u], min(u, max(nsw - 1, 0)));
+  GemmB<TN> bc = deq(st[0]);
+  int s = 0;
+  for (; s + S <= nsw; s += S) {
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+    for (int u = 0; u < S; ++u) {
+      __builtin_amdgcn_sched_barrier(0);
+      load(st[(u + P) % S], min(s + u + P, nsw - 1));
+      __builtin_amdgcn_sched_barrier(0);
+      const GemmB<TN> bn = deq(st[(u + 1) % S]);
+      mma(st[u], bc);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) red[((i * TN + j) * 16 + v) * 64 + l] = acc[i][j][v];
-  };
-  auto add = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][j][v] = red[((i * TN + j) * 16 + v) * 64 + l] + acc[i][j][v];
-  };
-#pragma unroll
-  for (int kk = KW - 1; kk > 0; --kk) {
-    if (kw == kk) {
-      if (kk < KW - 1) add();
-      put();
+      for (int k = 0; k < 2 * TM * TN; ++k) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      bc = bn;
     }
+  }
+  // the last nsw - s (< S) blocks are already in st[0 ..]
+#pragma unroll
+  for (int u = 0; u < S - 1; ++u)
+    if (s + u < nsw) {
+      const GemmB<TN> bn = deq(st[(u + 1) % S]);
+      mma(st[u], bc);
+      bc = bn;
+    }
+
+  // epilogue inputs for this wavefront's row groups and columns, in flight
+  // while the partials meet in LDS (rows and columns past the end read the
+  // last one)
+  constexpr int TPW = KW > 1 ? TM / KW : TM;  // row groups finished per wavefront
+  static_assert(KW == 1 || TM % KW == 0, "row groups split evenly over the k-waves");
+  float4 sc[TPW][4];
+  float bv[TN];
+#pragma unroll
+  for (int ii = 0; ii < TPW; ++ii) {
+    const int tg = min(by * TM + (KW > 1 ? kw * TPW + ii : ii), a.mgroups - 1);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sc[ii][q] = ldg_f4(a.rs + tg * RG + 8 * q + 4 * h);
+  }
+#pragma unroll
+  for (int j = 0; j < TN; ++j) bv[j] = bias ? ldg_f(bias + min((bx * TN + j) * RG + r, n - 1)) : 0.0f;
+  float4 *red = reinterpret_cast<float4 *>(lds);
+  if (KW > 1) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          red[(((kw * TM + i) * TN + j) * 4 + q) * 64 + l] =
+              make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
     __syncthreads();
   }
-  if (kw != 0) return;
-  if (KW > 1) add();
-
+  // every epilogue load has landed before the first store: stores count in
+  // the same counter, and a wait placed behind them would wait for them
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
+  for (int ii = 0; ii < TPW; ++ii) {
+    const int i = KW > 1 ? kw * TPW + ii : ii;
     const int tg = by * TM + i;
     if (tg >= a.mgroups) break;
+    const bool rows_full = (tg + 1) * RG <= m;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const int cg = (bx * 2 + nw) * TN + j;
+      const int cg = bx * TN + j;
       if (cg >= w.ngroups) continue;
       const int col = cg * RG + r;
-      if (col >= n) continue;
+      float y[16];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = tg * RG + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (row >= m) continue;
-        const float y = acc[i][j][v] * sc[i][v];
-        out[(size_t)row * n + col] = bias ? y + bv[j] : y;
+      for (int q = 0; q < 4; ++q) {
+        float4 v;
+        if (KW > 1) {
+          v = red[((i * TN + j) * 4 + q) * 64 + l];
+#pragma unroll
+          for (int kk = 1; kk < KW; ++kk) {
+            const float4 p = red[(((kk * TM + i) * TN + j) * 4 + q) * 64 + l];
+            v.x += p.x;
+            v.y += p.y;
+            v.z += p.z;
+            v.w += p.w;
+          }
+        } else {
+          v = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+        }
+        const float4 c = sc[ii][q];
+        y[4 * q] = v.x * c.x;
+        y[4 * q + 1] = v.y * c.y;
+        y[4 * q + 2] = v.z * c.z;
+        y[4 * q + 3] = v.w * c.w;
+        if (bias) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[4 * q + e] += bv[j];
+        }
+      }
+      // lane (h, r) holds rows 8q + 4h + e (e < 4) of column col
+      float *o = out + (size_t)(tg * RG + 4 * h) * n + col;
+      if (rows_full && (cg + 1) * RG <= n) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) stg_f(o + (size_t)(8 * (v >> 2) + (v & 3)) * n, y[v]);
+      } else if (col < n) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if (tg * RG + 4 * h + 8 * (v >> 2) + (v & 3) < m) stg_f(o + (size_t)(8 * (v >> 2) + (v & 3)) * n, y[v]);
       }
     }
   }

@@ -94,16 +94,18 @@ struct ActView {
   const float *da;      // d_a
   const float *pa;      // d_a * sum(q_a)
   const int32_t *sa;    // sum(q_a)
-  const uint16_t *a16;  // f16(d_a * q_a * 2^-e_row), MFMA order
+  const uint16_t *a16;  // f16(d_a * q_a * 2^-e_row), GEMM operand order (a16_index)
   const float *rs;      // 2^e_row per row
   int nb, mgroups;
 };
 
-// Per-block weight planes for the encoder GEMM, indexed like qs
-// ([group][nb_pad][32]).
+// Weight planes for the encoder GEMM, indexed like qs ([group][nb_pad][32]).
+// q8 holds every quant as one byte, in MFMA order within the block, biased to
+// unsigned: the 4/5-bit quants as stored (0..15 / 0..31), Q8_0 as q + 128
+// (for Q8_0 the plane is qs itself, read with the sign bit flipped).
 struct GemmPlanes {
-  const uint32_t *dm;   // f16 d_b (low half) and m_b (high half, 0 for _0 formats)
-  const uint32_t *qhb;  // permuted high-bit word (Q5)
+  const uint8_t *q8;   // [group][nb_pad][32][32]
+  const uint32_t *dm;  // f16 d_b (low half) and m_b (high half, 0 for _0 formats)
 };
 
 // element offsets
@@ -115,11 +117,12 @@ RW_HD inline size_t sc_index(const WeightView &w, int g, int bl, int r) {
 }
 RW_HD inline size_t act_slot(int nb, int g, int bl, int r) { return ((size_t)g * nb + bl) * RG + r; }
 
-// The encoder GEMM reads up to GEMM_PAD_BLOCKS blocks past a row group's last
-// block; its f16 activation plane gives every row group that many blocks of
-// zero padding, and every weight plane it reads carries that many blocks of
-// tail padding.
-constexpr int GEMM_PAD_BLOCKS = 20;
-RW_HD inline size_t act_slot16(int nb, int g, int bl, int r) { return act_slot(nb + GEMM_PAD_BLOCKS, g, bl, r); }
+// The f16 activation plane of the encoder GEMM: the 1024 values of (row
+// group g, block bl) sit in the order the GEMM's lanes load them,
+// [operand p][lane 32h + r][8]: lane (h, r) of the block's p-th MFMA reads
+// elements 16p + 8h .. 16p + 8h + 7 of row r as one 16-byte load.
+RW_HD inline size_t a16_index(int nb, int g, int bl, int r, int e) {
+  return act_slot(nb, g, bl, 0) * QK + (e >> 4) * 512 + (32 * ((e >> 3) & 1) + r) * 8 + (e & 7);
+}
 
 }  // namespace rw

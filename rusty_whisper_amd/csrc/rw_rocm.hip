@@ -212,7 +212,7 @@ static ActLayout act_layout_kind(size_t m, size_t k, bool f16) {
   L.off_qa = L.off_da = L.off_pa = L.off_sa = L.off_a16 = L.off_rs = 0;
   if (f16) {
     L.off_a16 = 0;
-    L.off_rs = align_up(rows * (k + (size_t)GEMM_PAD_BLOCKS * QK) * 2, 256);
+    L.off_rs = align_up(rows * k * 2, 256);
     L.bytes = align_up(L.off_rs + rows * 4, 256);
   } else {
     L.off_qa = 0;
@@ -260,23 +260,24 @@ static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &
   return RW_OK;
 }
 
-// GEMM: a workgroup tile is 2 activation row groups x 4 weight row groups
-// (64 x 128) with KW wavefronts along k.  KW grows with the blocks per row
-// (about 40 blocks per wavefront) and is at least 2 when the weight has few
-// column tiles; it depends on the weight alone, so a row's result never
-// depends on m.
+// GEMM: a workgroup tile is 4 activation row groups x 2 weight row groups
+// (128 x 64) with KW wavefronts along k.  KW is chosen from the weight's
+// column tiles so that a 1500-row input (12 row tiles) gives about one
+// wavefront per SIMD or more -- 1 from 48 column tiles up, 2 from 24, else 4
+// -- and every wavefront keeps at least 4 blocks.  It depends on the weight
+// alone, so a row's result never depends on m.
 static int gemm_kw(const rw_weight *w) {
-  int kw = w->nb >= 160 ? 4 : w->nb >= 80 ? 2 : 1;
-  if (cdiv(w->ngroups, 4) < 16 && kw < 2) kw = 2;
+  const size_t tiles = cdiv(w->ngroups, GEMM_TN);
+  int kw = tiles >= 48 ? 1 : tiles >= 24 ? 2 : 4;
+  while (kw > 1 && w->nb < 4 * kw) kw /= 2;
   return kw;
 }
 
 template <int DT, int KW>
 static void launch_gemm_kw(const rw_weight *w, const ActView &av, int m, const float *bias, float *out,
                            hipStream_t s) {
-  dim3 grid((unsigned)cdiv(w->ngroups, 4), (unsigned)cdiv(av.mgroups, 2));
-  hipLaunchKernelGGL((k_gemm<DT, 2, 2, KW>), grid, dim3(128 * KW), 0, s, w->view, w->gemm, av, m, (int)w->n, bias,
-                     out);
+  dim3 grid((unsigned)cdiv(w->ngroups, GEMM_TN), (unsigned)cdiv(av.mgroups, GEMM_TM));
+  hipLaunchKernelGGL((k_gemm<DT, KW>), grid, dim3(64 * KW), 0, s, w->view, w->gemm, av, m, (int)w->n, bias, out);
 }
 
 template <int DT>
@@ -592,14 +593,13 @@ int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, siz
   w->ngroups = (int)cdiv(n, RG);
   size_t rows = (size_t)w->ngroups * RG;
   size_t nsc = rows * w->nb_pad;
-  const size_t pad = (size_t)GEMM_PAD_BLOCKS * RG;  // tail padding read by k_gemm (slots)
-  size_t qsz = (nsc + pad) * qs_bytes(dtype);
+  size_t qsz = nsc * qs_bytes(dtype);
   size_t off_qh = align_up(qsz, 256);
   size_t off_d = align_up(off_qh + (has_high(dtype) ? nsc * 4 : 0), 256);
   size_t off_m = align_up(off_d + nsc * 2, 256);
   size_t off_dm = align_up(off_m + (has_min(dtype) ? nsc * 2 : 0), 256);
-  size_t off_qhb = align_up(off_dm + (nsc + pad) * 4, 256);
-  w->bytes = align_up(off_qhb + (has_high(dtype) ? (nsc + pad) * 4 : 0), 256);
+  size_t off_q8 = align_up(off_dm + nsc * 4, 256);  // the GEMM's byte plane (Q8_0 reads qs)
+  w->bytes = align_up(off_q8 + (dtype == RW_Q8_0 ? 0 : nsc * 32), 256);
   if (hipMalloc(&w->base, w->bytes) != hipSuccess) {
     (void)hipGetLastError();
     delete w;
@@ -608,7 +608,7 @@ int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, siz
   char *b = (char *)w->base;
   w->view = WeightView{(const uint8_t *)b, (const uint32_t *)(b + off_qh), (const uint16_t *)(b + off_d),
                        (const uint16_t *)(b + off_m), w->nb, w->nb_pad, w->noct, w->ngroups};
-  w->gemm = GemmPlanes{(const uint32_t *)(b + off_dm), (const uint32_t *)(b + off_qhb)};
+  w->gemm = GemmPlanes{(const uint8_t *)(dtype == RW_Q8_0 ? b : b + off_q8), (const uint32_t *)(b + off_dm)};
 
   void *tmp = nullptr;
   hipError_t e = hipMalloc(&tmp, raw_len);
@@ -619,7 +619,7 @@ int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, siz
 #define RW_REPACK(DT)                                                                                      \
   hipLaunchKernelGGL(k_repack<DT>, grid, dim3(256), 0, 0, (const uint8_t *)tmp, (int)n, (int)nb, (uint8_t *)b, \
                      (uint32_t *)(b + off_qh), (uint16_t *)(b + off_d), (uint16_t *)(b + off_m),                \
-                     (uint32_t *)(b + off_dm), (uint32_t *)(b + off_qhb), w->nb_pad,                     \
+                     (uint32_t *)(b + off_dm), (uint8_t *)(b + off_q8), w->nb_pad,                        \
                      w->noct, w->ngroups)
     switch (dtype) {
       case RW_Q4_0: RW_REPACK(RW_Q4_0); break;

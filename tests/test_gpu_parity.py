@@ -349,13 +349,16 @@ def test_matmul_t_q_parallel_matches_serial():
 
 
 # encoder-regime shapes that select each k split of the GEMM (1, 2 and 4
-# wavefronts along k) and an odd block count (the pipeline's tail reads past
-# the last block)
+# wavefronts along k, from the weight's 64-row column tiles and its blocks),
+# a block count that does not divide evenly over the wavefronts, and splits
+# cut back because the row has few blocks
 KSPLIT_SHAPES = [
-    (70, 1280, 2080),  # nb 40, 65 weight row groups: split 1
-    (40, 2560, 100),   # nb 80: split 2
-    (40, 5120, 96),    # nb 160: split 4
-    (33, 5152, 70),    # nb 161: split 4, odd
+    (70, 512, 3100),   # 49 column tiles: split 1
+    (40, 1280, 1600),  # 25 column tiles: split 2
+    (40, 5120, 96),    # 2 column tiles, nb 160: split 4
+    (33, 5152, 70),    # nb 161: split 4, uneven
+    (45, 384, 100),    # nb 12: split cut to 2
+    (20, 224, 96),     # nb 7: split cut to 1
 ]
 
 
