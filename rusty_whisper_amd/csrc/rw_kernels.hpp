@@ -32,6 +32,33 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 
+// Loads and stores through pointers read out of a launch table: the
+// compiler cannot tell their address space, and flat accesses also count
+// against the LDS wait counter, so every LDS wait would hold for them.
+// Address space 1 makes them global_load / global_store (vector-memory
+// counter only).  16-byte values go through native vector types, which keep
+// the address space where HIP's vector classes do not.
+#define RW_GLOBAL_AS __attribute__((address_space(1)))
+typedef uint32_t rw_u32x4 __attribute__((ext_vector_type(4)));
+typedef float rw_f32x4 __attribute__((ext_vector_type(4)));
+__device__ inline uint4 ldg_u4(const void *p) {
+  const rw_u32x4 v = *(const rw_u32x4 RW_GLOBAL_AS *)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+typedef uint32_t rw_u32x2 __attribute__((ext_vector_type(2)));
+__device__ inline uint2 ldg_u2(const void *p) {
+  const rw_u32x2 v = *(const rw_u32x2 RW_GLOBAL_AS *)p;
+  return make_uint2(v.x, v.y);
+}
+__device__ inline float4 ldg_f4(const void *p) {
+  const rw_f32x4 v = *(const rw_f32x4 RW_GLOBAL_AS *)p;
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ inline float ldg_f(const void *p) { return *(const float RW_GLOBAL_AS *)p; }
+__device__ inline uint32_t ldg_u32(const void *p) { return *(const uint32_t RW_GLOBAL_AS *)p; }
+__device__ inline int32_t ldg_i32(const void *p) { return *(const int32_t RW_GLOBAL_AS *)p; }
+__device__ inline void stg_f(float *p, float v) { *(float RW_GLOBAL_AS *)(void *)p = v; }
+
 // ------------------------------------------------------------ scalar helpers
 
 // IEEE half -> single with the exact bit rules of model.rs:68-86 (NaN payload
@@ -240,73 +267,116 @@ __global__ __launch_bounds__(256) void k_quantize(const float *__restrict__ a, i
   }
 }
 
-// Activations for the encoder GEMM, one workgroup per row of the padded
-// row groups (rows >= m are written as zeros); 8 lanes per block, 32 blocks
-// per pass.  The quantization is quantize_acts_i8's (src/quant.rs:691-716)
-// bit for bit; each element is stored as f16(d_a * q_a * 2^-e), at its
-// a16_index position, with e chosen from the row's largest |x| so that the
-// largest value lands in [2^14, 2^15): no value overflows, and every value
-// keeps f16's full precision unless it is below 2^-28 of the row's largest.
-// rs[row] = 2^e undoes the scaling exactly in the GEMM's epilogue.
+// quantize_acts_i8's q for v = x * inv as a float: round half away from
+// zero, clamp to +-127 (an infinite v, from an infinite inv, included),
+// NaN -> 0, and +0 (never -0) for zero
+__device__ inline float quant_q(float v) {
+  const float r = roundf(fminf(fabsf(v), 127.0f));
+  if (v != v) return 0.0f;
+  return v <= -0.5f ? -r : r;
+}
+
+// Activations for the encoder GEMM: one wavefront per row (4 rows per
+// workgroup; rows >= m of the padded row groups are written as zeros), lanes
+// 8b + t holding elements 4t..4t+3 of blocks 8p + b.  The quantization is
+// quantize_acts_i8's (src/quant.rs:691-716) bit for bit: the block maxima
+// come from 8-lane shuffles, and the correctly rounded d = amax / 127 and
+// inv = 1 / d of pass p are computed once, by lane p % 8 of each 8-lane
+// group, and read back by shuffle.  Each element is stored as
+// f16(q_a * (d_a * 2^(15-e))) at its a16_index position, e chosen from the
+// row's largest |x| so that the largest value lands in [2^14, 2^15): no
+// value overflows, and every value keeps f16's full precision unless it is
+// below 2^-28 of the row's largest.  d_a * 2^(15-e) is exact unless it falls
+// below f32's normal range, and then every q_a times it is zero in f16
+// either way.  rs[row] = 2^(e-15) undoes the scaling in the GEMM's epilogue.  NP passes of 8 blocks stay in registers; a longer
+// row is read twice, once for its largest |x| and once to quantize.
+template <int NP>
 __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ a, int m, int k, int nb,
                                                       uint16_t *__restrict__ a16, float *__restrict__ rs) {
-  constexpr int KEEP = 8;  // passes of 32 blocks held in registers (k <= 8192)
-  __shared__ float wmax[4];
-  const int row = blockIdx.x;
-  const int t = threadIdx.x, lb = t >> 3, lt = t & 7;
+  const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lb = lane >> 3, lt = lane & 7;
   const int g = row / RG, r = row % RG;
-  if (row >= m) {  // uniform per workgroup
-    for (int bl = lb; bl < nb; bl += 32)
+  if (row >= m) {  // uniform per wavefront
+    for (int bl = lb; bl < nb; bl += 8)
       *reinterpret_cast<uint2 *>(a16 + a16_index(nb, g, bl, r, 4 * lt)) = make_uint2(0u, 0u);
-    if (t == 0) rs[row] = 0.0f;
+    if (lane == 0) rs[row] = 0.0f;
     return;
   }
   const float *x = a + (size_t)row * k;
-  float4 xv[KEEP];
+  constexpr int CB = 8 * NP;  // blocks per chunk
+  const int nch = (nb + CB - 1) / CB;
+  float4 v[NP];
+  float bam[NP];
+  auto load = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int bl = c * CB + 8 * p + lb;
+      v[p] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (bl < nb) v[p] = ldg_f4(x + (size_t)bl * QK + 4 * lt);
+    }
+  };
+  auto block_max = [&]() __attribute__((always_inline)) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      float b = fmaxf(fmaxf(fabsf(v[p].x), fabsf(v[p].y)), fmaxf(fabsf(v[p].z), fabsf(v[p].w)));
+      b = fmaxf(b, __shfl_xor(b, 1));
+      b = fmaxf(b, __shfl_xor(b, 2));
+      b = fmaxf(b, __shfl_xor(b, 4));
+      bam[p] = b;
+      amax = fmaxf(amax, b);
+    }
+    return amax;
+  };
   float amax = 0.0f;
-#pragma unroll
-  for (int p = 0; p < KEEP; ++p) {
-    const int bl = 32 * p + lb;
-    xv[p] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (bl < nb) xv[p] = *reinterpret_cast<const float4 *>(x + (size_t)bl * QK + 4 * lt);
-    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(xv[p].x), fabsf(xv[p].y)), fmaxf(fabsf(xv[p].z), fabsf(xv[p].w))));
+  for (int c = 0; c < nch; ++c) {
+    load(c);
+    amax = fmaxf(amax, block_max());
   }
-  for (int bl = 32 * KEEP + lb; bl < nb; bl += 32) {
-    const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)bl * QK + 4 * lt);
-    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-  }
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-  if ((t & 63) == 0) wmax[t >> 6] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  amax = fmaxf(amax, __shfl_xor(amax, 8));
+  amax = fmaxf(amax, __shfl_xor(amax, 16));
+  amax = fmaxf(amax, __shfl_xor(amax, 32));
   int e = 15;  // zero, inf or NaN rows: no scaling
   if (amax > 0.0f && amax <= 3.4028235e38f) {
     frexpf(amax, &e);  // amax in [2^(e-1), 2^e)
     e = max(e, -110);
   }
   const float down = ldexpf(1.0f, 15 - e);
-  // whole wavefronts run every pass (the shuffles need all 8 lanes of a
-  // block); lanes past the row's blocks quantize zeros and store nothing
-  auto emit = [&](float4 v, int bl) __attribute__((always_inline)) {
-    const BlockQuant bq = quantize_block8(v);
-    if (bl < nb) {
-      h2v lo2 = {(_Float16)(__fmul_rn(bq.d, (float)bq.q0) * down), (_Float16)(__fmul_rn(bq.d, (float)bq.q1) * down)};
-      h2v hi2 = {(_Float16)(__fmul_rn(bq.d, (float)bq.q2) * down), (_Float16)(__fmul_rn(bq.d, (float)bq.q3) * down)};
-      *reinterpret_cast<uint2 *>(a16 + a16_index(nb, g, bl, r, 4 * lt)) =
-          make_uint2(__builtin_bit_cast(uint32_t, lo2), __builtin_bit_cast(uint32_t, hi2));
+  constexpr int NC = (NP + 7) / 8;
+  for (int c = 0; c < nch; ++c) {
+    if (nch > 1) {
+      load(c);
+      block_max();
     }
-  };
+    // lane t of each 8-lane group divides for the passes p = t (mod 8)
+    float dv[NC], iv[NC];
 #pragma unroll
-  for (int p = 0; p < KEEP; ++p)
-    if (32 * p < nb) emit(xv[p], 32 * p + lb);
-  for (int b0 = 32 * KEEP; b0 < nb; b0 += 32) {
-    const int bl = b0 + lb;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (bl < nb) v = *reinterpret_cast<const float4 *>(x + (size_t)bl * QK + 4 * lt);
-    emit(v, bl);
+    for (int cc = 0; cc < NC; ++cc) {
+      float b = bam[8 * cc];
+#pragma unroll
+      for (int t = 1; t < 8; ++t)
+        if (8 * cc + t < NP) b = lt == t ? bam[8 * cc + t] : b;
+      dv[cc] = __fdiv_rn(b, 127.0f);
+      iv[cc] = dv[cc] > 0.0f ? __fdiv_rn(1.0f, dv[cc]) : 0.0f;
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      if (c * CB + 8 * p >= nb) break;  // uniform
+      const int bl = c * CB + 8 * p + lb;
+      const int src = (lane & ~7) | (p & 7);
+      const float inv = __shfl(iv[p >> 3], src);
+      const float dd = __shfl(dv[p >> 3], src) * down;
+      const float q0 = quant_q(__fmul_rn(v[p].x, inv)), q1 = quant_q(__fmul_rn(v[p].y, inv));
+      const float q2 = quant_q(__fmul_rn(v[p].z, inv)), q3 = quant_q(__fmul_rn(v[p].w, inv));
+      if (bl < nb) {
+        const h2v lo2 = {(_Float16)__fmul_rn(q0, dd), (_Float16)__fmul_rn(q1, dd)};
+        const h2v hi2 = {(_Float16)__fmul_rn(q2, dd), (_Float16)__fmul_rn(q3, dd)};
+        *reinterpret_cast<uint2 *>(a16 + a16_index(nb, g, bl, r, 4 * lt)) =
+            make_uint2(__builtin_bit_cast(uint32_t, lo2), __builtin_bit_cast(uint32_t, hi2));
+      }
+    }
   }
-  if (t == 0) rs[row] = ldexpf(1.0f, e - 15);
+  if (lane == 0) rs[row] = ldexpf(1.0f, e - 15);
 }
 
 // --------------------------------------------------- MFMA operand unpack
@@ -363,32 +433,6 @@ __global__ __launch_bounds__(64) void k_block_dots(WeightView w, ActView a, int 
 
 // ---------------------------------------------------------------- k_gemv2
 
-// Loads and stores through pointers read out of a launch table: the
-// compiler cannot tell their address space, and flat accesses also count
-// against the LDS wait counter, so every LDS wait would hold for them.
-// Address space 1 makes them global_load / global_store (vector-memory
-// counter only).  16-byte values go through native vector types, which keep
-// the address space where HIP's vector classes do not.
-#define RW_GLOBAL_AS __attribute__((address_space(1)))
-typedef uint32_t rw_u32x4 __attribute__((ext_vector_type(4)));
-typedef float rw_f32x4 __attribute__((ext_vector_type(4)));
-__device__ inline uint4 ldg_u4(const void *p) {
-  const rw_u32x4 v = *(const rw_u32x4 RW_GLOBAL_AS *)p;
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-typedef uint32_t rw_u32x2 __attribute__((ext_vector_type(2)));
-__device__ inline uint2 ldg_u2(const void *p) {
-  const rw_u32x2 v = *(const rw_u32x2 RW_GLOBAL_AS *)p;
-  return make_uint2(v.x, v.y);
-}
-__device__ inline float4 ldg_f4(const void *p) {
-  const rw_f32x4 v = *(const rw_f32x4 RW_GLOBAL_AS *)p;
-  return make_float4(v.x, v.y, v.z, v.w);
-}
-__device__ inline float ldg_f(const void *p) { return *(const float RW_GLOBAL_AS *)p; }
-__device__ inline uint32_t ldg_u32(const void *p) { return *(const uint32_t RW_GLOBAL_AS *)p; }
-__device__ inline int32_t ldg_i32(const void *p) { return *(const int32_t RW_GLOBAL_AS *)p; }
-__device__ inline void stg_f(float *p, float v) { *(float RW_GLOBAL_AS *)(void *)p = v; }
 
 // One linear of a decode-shape launch: out[m, n] = a[m, k] W^T (+ bias).
 struct GemvItem {

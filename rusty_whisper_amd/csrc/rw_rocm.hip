@@ -246,9 +246,19 @@ static ActView act_view(const ActLayout &L, void *ws) {
 static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &L, void *ws, hipStream_t s) {
   char *b = (char *)ws;
   if (L.f16) {
-    const size_t rows = (size_t)L.mgroups * RG;
-    hipLaunchKernelGGL(k_quantize_f16, dim3((unsigned)rows), dim3(256), 0, s, a, (int)m, (int)k, L.nb,
-                       (uint16_t *)(b + L.off_a16), (float *)(b + L.off_rs));
+    // one wavefront per row, 4 rows per workgroup; NP passes of 8 blocks in
+    // registers (longer rows are read twice)
+    const unsigned wgs = (unsigned)((size_t)L.mgroups * RG / 4);
+    uint16_t *a16 = (uint16_t *)(b + L.off_a16);
+    float *rs = (float *)(b + L.off_rs);
+#define RW_QF16(NP) hipLaunchKernelGGL(k_quantize_f16<NP>, dim3(wgs), dim3(256), 0, s, a, (int)m, (int)k, L.nb, a16, rs)
+    if (L.nb <= 8) RW_QF16(1);
+    else if (L.nb <= 16) RW_QF16(2);
+    else if (L.nb <= 40) RW_QF16(5);
+    else if (L.nb <= 64) RW_QF16(8);
+    else if (L.nb <= 160) RW_QF16(20);
+    else RW_QF16(32);
+#undef RW_QF16
     LAUNCH_TRY("k_quantize_f16");
     return RW_OK;
   }

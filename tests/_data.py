@@ -48,6 +48,34 @@ def random_blocks(dtype: int, nblocks: int, seed: int, scale_codes=None) -> np.n
     return raw.reshape(-1)
 
 
+def edge_activation_rows(k: int) -> np.ndarray:
+    """Rows that hit every special case of quantize_acts_i8 (quant.rs:691-716)."""
+    rows = []
+    z = np.zeros(k, np.float32)
+    rows.append(z)  # d = 0 -> inv = 0 -> q = 0
+    h = np.zeros(k, np.float32)
+    h[:4] = [127.0, 0.5, -0.5, 1.5]  # amax 127 -> d = 1: exact halves round away from 0
+    rows.append(h)
+    e = np.zeros(k, np.float32)
+    e[0], e[1] = 3.0, -3.0  # +-amax -> +-127
+    rows.append(e)
+    t = np.full(k, 1e-38, np.float32)  # d subnormal, 1/d overflows to inf
+    t[1] = -2e-39
+    rows.append(t)
+    s = np.full(k, 3e-45, np.float32)  # subnormal inputs
+    rows.append(s)
+    n = np.ones(k, np.float32)
+    n[3] = np.nan  # NaN ignored by the amax fold, quantizes to 0
+    rows.append(n)
+    i = np.ones(k, np.float32)
+    i[5] = np.inf  # amax = inf -> inv = 0 -> q = 0 (inf*0 = NaN -> 0)
+    rows.append(i)
+    b = np.full(k, 3.4e38, np.float32)
+    b[2] = -3.4e38
+    rows.append(b)
+    return np.stack(rows)
+
+
 def rel_row_l2(got: np.ndarray, ref: np.ndarray) -> float:
     """max_ij |got-ref| / ||ref_i||_2 -- the north-star output tolerance."""
     ref64 = ref.astype(np.float64)

@@ -1,6 +1,10 @@
 """Device-pointer entry points on the GPU, through the C ABI.
 
 Bars (written in each test):
+  * the encoder GEMM's activation plane (m > 8) holds, bit for bit, the f16
+    values f16(q_a * f32(d_a * 2^(15-e))) of quantize_acts_i8's q_a and d_a,
+    with 2^(e-1) <= the row's largest |x| < 2^e (e >= -110; 15 for zero or
+    non-finite rows), and the row scales 2^(e-15);
   * quantizing inside the decode launch and quantizing separately
     (rw_rocm_quantize_dev + rw_rocm_matmul_prequant_dev) give bitwise the
     same outputs, in both regimes;
@@ -17,7 +21,7 @@ import pytest
 import oracle as O
 from rusty_whisper_amd import _abi as A
 
-from _data import DTYPES, NAMES, activations, rel_row_l2, weights
+from _data import DTYPES, NAMES, activations, edge_activation_rows, rel_row_l2, weights
 
 pytestmark = pytest.mark.gpu
 
@@ -227,3 +231,65 @@ def test_graph_replay_matches_eager(torch, dtype, n, m):
         assert np.array_equal(_bits(out2.cpu().numpy()), _bits(ref2)), rep
         del junk
     del graph
+
+
+def _scale_rows(k):
+    """Rows for the per-row power-of-two scale of the f16 plane."""
+    rows = []
+    big = np.full(k, 1e-20, np.float32)
+    big[:32] = np.linspace(-1e30, 1e30, 32, dtype=np.float32)  # a huge block beside tiny ones
+    rows.append(big)
+    p2 = np.zeros(k, np.float32)
+    p2[:4] = [2.0, -1.0, 0.25, -2.0]  # amax exactly a power of two
+    rows.append(p2)
+    rows.append(np.full(k, -0.0, np.float32))  # -0 inputs quantize to +0
+    tiny = np.full(k, 1e-40, np.float32)  # subnormal row maximum: e clamps at -110
+    tiny[::3] = -3e-41
+    rows.append(tiny)
+    return np.stack(rows)
+
+
+def _a16_expected(a):
+    """The f16 plane's values and row scales, from the oracle's q_a and d_a."""
+    m, k = a.shape
+    with np.errstate(all="ignore"):
+        q, d, _ = O.quantize_acts(a)
+    amax = np.fmax.reduce(np.abs(a), axis=1, initial=np.float32(0))  # NaN skipped, as the Rust fold
+    e = np.full(m, 15, np.int64)
+    ok = (amax > 0) & np.isfinite(amax)
+    e[ok] = np.maximum(np.frexp(amax[ok])[1], -110)
+    down = np.ldexp(np.float32(1), (15 - e)).astype(np.float32)
+    dd = (d * down[:, None]).astype(np.float32)
+    with np.errstate(all="ignore"):
+        vals = (q.astype(np.float32) * np.repeat(dd, 32, axis=1)).astype(np.float16)
+    return vals, np.ldexp(np.float32(1), (e - 15)).astype(np.float32)
+
+
+def _a16_index(m, k):
+    rows = (m + 31) // 32 * 32
+    nb = k // 32
+    i = np.arange(rows)[:, None]
+    kk = np.arange(k)[None, :]
+    g, r, bl, e = i // 32, i % 32, kk // 32, kk % 32
+    return (g * nb + bl) * 1024 + (e >> 4) * 512 + (32 * ((e >> 3) & 1) + r) * 8 + (e & 7)
+
+
+@pytest.mark.parametrize("k", [32, 96, 1280, 5120, 8224, 16384])
+def test_gemm_activation_plane_bit_exact(torch, k):
+    # 8224 and 16384 take the long-row path (the row is read twice)
+    a = np.concatenate([activations(21, k, seed=k, outliers=0.01), edge_activation_rows(k), _scale_rows(k)])
+    m = a.shape[0]
+    assert m > 8  # the encoder (f16) layout
+    wsz = A.workspace_size(m, k)
+    ws = torch.zeros(wsz, dtype=torch.uint8, device="cuda:0")
+    A.quantize_dev(_dev(torch, a), m, k, ws, wsz)
+    torch.cuda.synchronize()
+    raw = ws.cpu().numpy()
+    rows = (m + 31) // 32 * 32
+    plane = raw[:rows * k * 2].view(np.uint16)[_a16_index(m, k)]
+    off_rs = (rows * k * 2 + 255) // 256 * 256
+    rs = raw[off_rs:off_rs + rows * 4].view(np.float32)
+    want, want_rs = _a16_expected(a)
+    assert np.array_equal(plane[:m], want.view(np.uint16)), np.argwhere(plane[:m] != want.view(np.uint16))[:5]
+    assert np.array_equal(rs[:m].view(np.uint32), want_rs.view(np.uint32))
+    assert not plane[m:].any() and not rs[m:].any()  # padding rows of the last row group

@@ -17,7 +17,7 @@ import pytest
 import oracle as O
 from rusty_whisper_amd import _abi as A
 
-from _data import DTYPES, NAMES, activations, random_blocks, rel_row_l2, weights
+from _data import DTYPES, NAMES, activations, edge_activation_rows, random_blocks, rel_row_l2, weights
 
 pytestmark = pytest.mark.gpu
 
@@ -134,37 +134,10 @@ def test_dequant_nonfinite_scales(dtype):
 # ----------------------------------------------------- quantize_acts
 
 
-def _edge_activation_rows(k):
-    rows = []
-    z = np.zeros(k, np.float32)
-    rows.append(z)  # d = 0 -> inv = 0 -> q = 0
-    h = np.zeros(k, np.float32)
-    h[:4] = [127.0, 0.5, -0.5, 1.5]  # amax 127 -> d = 1: exact halves round away from 0
-    rows.append(h)
-    e = np.zeros(k, np.float32)
-    e[0], e[1] = 3.0, -3.0  # +-amax -> +-127
-    rows.append(e)
-    t = np.full(k, 1e-38, np.float32)  # d subnormal, 1/d overflows to inf
-    t[1] = -2e-39
-    rows.append(t)
-    s = np.full(k, 3e-45, np.float32)  # subnormal inputs
-    rows.append(s)
-    n = np.ones(k, np.float32)
-    n[3] = np.nan  # NaN ignored by the amax fold, quantizes to 0
-    rows.append(n)
-    i = np.ones(k, np.float32)
-    i[5] = np.inf  # amax = inf -> inv = 0 -> q = 0 (inf*0 = NaN -> 0)
-    rows.append(i)
-    b = np.full(k, 3.4e38, np.float32)
-    b[2] = -3.4e38
-    rows.append(b)
-    return np.stack(rows)
-
-
 @pytest.mark.parametrize("m,k", [(37, 96), (1, 32), (64, 384), (70, 1280)])
 def test_quantize_acts_bit_exact(m, k):
     a = activations(m, k, seed=m * 7 + k, outliers=0.01)
-    edge = _edge_activation_rows(k)
+    edge = edge_activation_rows(k)
     a = np.concatenate([a, edge])
     with np.errstate(all="ignore"):
         q0, d0, s0 = O.quantize_acts(a)
