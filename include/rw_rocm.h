@@ -130,6 +130,20 @@ int rw_rocm_quantize_dev(const float *a, size_t m, size_t k, void *workspace, si
 int rw_rocm_matmul_prequant_dev(const rw_weight *w, const void *workspace, size_t m, const float *bias,
                                 float *out, void *stream);
 
+/* Several products from one quantized activation in one launch:
+ * out[i][m, n_i] = a W_i^T (+ bias[i]) for i < count, 1 <= count <= 4, with
+ * `workspace` filled by rw_rocm_quantize_dev (same m and k).  The weights
+ * share dtype, k and device; `bias` may be NULL (no biases) or hold NULL
+ * entries.  Replaces the linear_w calls on one input of src/encoder.rs:130-141
+ * (Q, K and V of the self-attention; Q/K/V of src/decoder.rs:148-158 in the
+ * decode shape).  For m > 8 the weights' column tiles share one GEMM launch
+ * whose k split is chosen from all of them, so a result can differ from
+ * rw_rocm_matmul_prequant_dev's in the last bits of the f32 sums (within
+ * the same error bound); it never depends on m.  For m <= 8 each weight
+ * runs its own decode launch, bitwise rw_rocm_matmul_prequant_dev. */
+int rw_rocm_matmul_prequant_multi_dev(const rw_weight *const *w, size_t count, const void *workspace, size_t m,
+                                      const float *const *bias, float *const *out, void *stream);
+
 /* One entry of a grouped launch: out_g[m_g, n_g] = a_g W_g^T (+ bias_g). */
 typedef struct rw_linear {
     const rw_weight *w;

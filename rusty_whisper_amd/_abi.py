@@ -61,6 +61,8 @@ _SIGNATURES = {
                                        C.c_void_p]),
     "rw_rocm_matmul_prequant_dev": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p,
                                               C.c_void_p]),
+    "rw_rocm_matmul_prequant_multi_dev": (C.c_int, [C.POINTER(C.c_void_p), C.c_size_t, C.c_void_p, C.c_size_t,
+                                                    C.POINTER(C.c_void_p), C.POINTER(C.c_void_p), C.c_void_p]),
     "rw_rocm_matmul_grouped_dev": (C.c_int, [C.POINTER(rw_linear), C.c_size_t, C.c_void_p, C.c_size_t,
                                              C.c_void_p]),
     "rw_rocm_grouped_workspace_size": (C.c_size_t, [C.POINTER(rw_linear), C.c_size_t]),
@@ -194,6 +196,16 @@ class DeviceWeight:
             self.free()
         except Exception:
             pass
+
+
+def matmul_prequant_multi_dev(weights, workspace, m: int, outs, biases=None, stream: int | None = None) -> None:
+    """out[i] = (activations quantized into `workspace`) W_i^T (+ biases[i]) for
+    up to 4 weights of one dtype and k, in one launch for m > 8."""
+    cnt = len(weights)
+    warr = (C.c_void_p * max(cnt, 1))(*[w.handle for w in weights])
+    oarr = (C.c_void_p * max(cnt, 1))(*[_ptr(o) for o in outs])
+    barr = None if biases is None else (C.c_void_p * max(cnt, 1))(*[_ptr(b) for b in biases])
+    check(lib().rw_rocm_matmul_prequant_multi_dev(warr, cnt, _ptr(workspace), m, barr, oarr, stream))
 
 
 def workspace_size(m: int, k: int) -> int:

@@ -730,13 +730,30 @@ __device__ inline void weight_f16(uint4 qb, uint32_t dmw, v8h &b0, v8h &b1) {
 
 constexpr int GEMM_TM = 4, GEMM_TN = 2, GEMM_P = 2;
 
+// The weights of one k_gemm launch (all of one dtype and k, against one
+// quantized activation): column tiles [tile0, tile0 + cdiv(ngroups, TN)) of
+// the launch belong to item i.
+constexpr int GEMM_MAX_SET = 4;
+struct GemmItem {
+  GemmPlanes gp;
+  const float *bias;
+  float *out;
+  int n, ngroups, tile0;
+};
+struct GemmSet {
+  GemmItem it[GEMM_MAX_SET];
+  int count, nb, nb_pad;
+};
+
 // Encoder-shape GEMM (m > 8): out = rs * (A' W'^T) (+ bias), with A' the f16
 // values of the quantized activations (k_quantize_f16) and W' = f16(d_b*q_b
 // + m_b) formed in registers from the byte plane with one packed f16 fma per
 // two weights (a single rounding).  Products of f16 operands are exact and
 // accumulate in f32 inside v_mfma_f32_32x32x16_f16, so |y - exact| <=
 // 2^-10 sum|a||w| plus the f32 accumulation error.
-// A workgroup owns one tile of TM activation row groups x TN weight row
+// A launch covers up to GEMM_MAX_SET weights that share the activation (the
+// column tiles of the launch run through the weights in turn).  A
+// workgroup owns one tile of TM activation row groups x TN weight row
 // groups (128 x 64) and has KW wavefronts, each taking every KW-th block
 // (block kw, kw + KW, ...).  A wavefront loads its operands straight into
 // registers, P blocks ahead, and needs no other wavefront until the end: no
@@ -744,11 +761,10 @@ constexpr int GEMM_TM = 4, GEMM_TN = 2, GEMM_P = 2;
 // s + P, then runs the 16 MFMAs of block s while the VALU dequantizes the
 // weights of block s + 1 (one MFMA, then three VALU instructions).  At the
 // end the KW partial tiles meet in LDS and are summed in kw order, each
-// wavefront finishing TM / KW row groups.  KW comes from the weight's shape
-// alone, so a row's result never depends on m.
+// wavefront finishing TM / KW row groups.  KW comes from the weights'
+// shapes alone, so a row's result never depends on m.
 template <int DT, int KW>
-__global__ __launch_bounds__(64 * KW, 1) void k_gemm(WeightView w, GemmPlanes gp, ActView a, int m, int n,
-                                                     const float *__restrict__ bias, float *__restrict__ out) {
+__global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int m) {
   constexpr int TM = GEMM_TM, TN = GEMM_TN, P = GEMM_P, S = P + 1;
   constexpr int RED = KW > 1 ? KW * TM * TN * 16 * 64 * 4 : 16;
   __shared__ __align__(16) uint8_t lds[RED];
@@ -767,7 +783,22 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(WeightView w, GemmPlanes gp
     bx = lin % nx;
     by = lin / nx;
   }
-  const int nb = w.nb;
+  // this tile's weight, selected by uniform compares (no runtime index into
+  // the argument array)
+  int wi = 0;
+#pragma unroll
+  for (int t = 1; t < GEMM_MAX_SET; ++t)
+    if (t < set.count && bx >= set.it[t].tile0) wi = t;
+  GemmItem it = set.it[0];
+#pragma unroll
+  for (int t = 1; t < GEMM_MAX_SET; ++t)
+    if (wi == t) it = set.it[t];
+  bx -= it.tile0;
+  const GemmPlanes gp = it.gp;
+  const float *__restrict__ bias = it.bias;
+  float *__restrict__ out = it.out;
+  const int n = it.n, ngroups = it.ngroups;
+  const int nb = set.nb;
   const int nsw = nb > kw ? (nb - kw + KW - 1) / KW : 0;  // this wavefront's block count
 
   // uniform bases at block kw (row groups past the end repeat the last one)
@@ -780,8 +811,8 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(WeightView w, GemmPlanes gp
   const uint8_t *qbase[TN], *dbase[TN];
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
-    const int g = min(bx * TN + j, w.ngroups - 1);
-    const size_t s0 = qs_slot(w, g, kw, 0);
+    const int g = min(bx * TN + j, ngroups - 1);
+    const size_t s0 = ((size_t)g * set.nb_pad + kw) * RG;
     qbase[j] = gp.q8 + s0 * 32;
     dbase[j] = reinterpret_cast<const uint8_t *>(gp.dm + s0);
   }
@@ -893,7 +924,7 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(WeightView w, GemmPlanes gp
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
       const int cg = bx * TN + j;
-      if (cg >= w.ngroups) continue;
+      if (cg >= ngroups) continue;
       const int col = cg * RG + r;
       float y[16];
 #pragma unroll

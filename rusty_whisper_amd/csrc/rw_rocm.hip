@@ -270,34 +270,62 @@ static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &
   return RW_OK;
 }
 
+#define RW_DISPATCH_DT(dt, FN, ...)                  \
+  switch (dt) {                                      \
+    case RW_Q4_0: FN<RW_Q4_0>(__VA_ARGS__); break;   \
+    case RW_Q4_1: FN<RW_Q4_1>(__VA_ARGS__); break;   \
+    case RW_Q5_0: FN<RW_Q5_0>(__VA_ARGS__); break;   \
+    case RW_Q5_1: FN<RW_Q5_1>(__VA_ARGS__); break;   \
+    default: FN<RW_Q8_0>(__VA_ARGS__); break;        \
+  }
+
 // GEMM: a workgroup tile is 4 activation row groups x 2 weight row groups
-// (128 x 64) with KW wavefronts along k.  KW is chosen from the weight's
+// (128 x 64) with KW wavefronts along k.  KW is chosen from the launch's
 // column tiles so that a 1500-row input (12 row tiles) gives about one
 // wavefront per SIMD or more -- 1 from 48 column tiles up, 2 from 24, else 4
-// -- and every wavefront keeps at least 4 blocks.  It depends on the weight
+// -- and every wavefront keeps at least 4 blocks.  It depends on the weights
 // alone, so a row's result never depends on m.
-static int gemm_kw(const rw_weight *w) {
-  const size_t tiles = cdiv(w->ngroups, GEMM_TN);
+static int gemm_kw(size_t tiles, int nb) {
   int kw = tiles >= 48 ? 1 : tiles >= 24 ? 2 : 4;
-  while (kw > 1 && w->nb < 4 * kw) kw /= 2;
+  while (kw > 1 && nb < 4 * kw) kw /= 2;
   return kw;
 }
 
 template <int DT, int KW>
-static void launch_gemm_kw(const rw_weight *w, const ActView &av, int m, const float *bias, float *out,
-                           hipStream_t s) {
-  dim3 grid((unsigned)cdiv(w->ngroups, GEMM_TN), (unsigned)cdiv(av.mgroups, GEMM_TM));
-  hipLaunchKernelGGL((k_gemm<DT, KW>), grid, dim3(64 * KW), 0, s, w->view, w->gemm, av, m, (int)w->n, bias, out);
+static void launch_gemm_kw(const GemmSet &set, size_t tiles, const ActView &av, int m, hipStream_t s) {
+  dim3 grid((unsigned)tiles, (unsigned)cdiv(av.mgroups, GEMM_TM));
+  hipLaunchKernelGGL((k_gemm<DT, KW>), grid, dim3(64 * KW), 0, s, set, av, m);
 }
 
 template <int DT>
-static void launch_gemm_dt(const rw_weight *w, const ActView &av, int m, const float *bias, float *out,
-                           hipStream_t s) {
-  switch (gemm_kw(w)) {
-    case 4: launch_gemm_kw<DT, 4>(w, av, m, bias, out, s); break;
-    case 2: launch_gemm_kw<DT, 2>(w, av, m, bias, out, s); break;
-    default: launch_gemm_kw<DT, 1>(w, av, m, bias, out, s); break;
+static void launch_gemm_dt(const GemmSet &set, size_t tiles, const ActView &av, int m, hipStream_t s) {
+  switch (gemm_kw(tiles, set.nb)) {
+    case 4: launch_gemm_kw<DT, 4>(set, tiles, av, m, s); break;
+    case 2: launch_gemm_kw<DT, 2>(set, tiles, av, m, s); break;
+    default: launch_gemm_kw<DT, 1>(set, tiles, av, m, s); break;
   }
+}
+
+// one k_gemm launch for `count` (1 .. GEMM_MAX_SET) weights of one dtype and
+// k against the quantized activation `av`
+static void run_gemm(const rw_weight *const *w, const float *const *bias, float *const *out, size_t count,
+                     const ActView &av, int m, hipStream_t s) {
+  GemmSet set{};
+  set.count = (int)count;
+  set.nb = w[0]->nb;
+  set.nb_pad = w[0]->nb_pad;
+  size_t tiles = 0;
+  for (size_t i = 0; i < count; ++i) {
+    GemmItem &it = set.it[i];
+    it.gp = w[i]->gemm;
+    it.bias = bias ? bias[i] : nullptr;
+    it.out = out[i];
+    it.n = (int)w[i]->n;
+    it.ngroups = w[i]->ngroups;
+    it.tile0 = (int)tiles;
+    tiles += cdiv(w[i]->ngroups, GEMM_TN);
+  }
+  RW_DISPATCH_DT(w[0]->dtype, launch_gemm_dt, set, tiles, av, m, s);
 }
 
 // ------------------------------------------------------ decode GEMV
@@ -360,15 +388,6 @@ static void launch_gemv_dt(int m, const GemvItem *items, const int *wg_item, con
   }
 }
 
-#define RW_DISPATCH_DT(dt, FN, ...)                  \
-  switch (dt) {                                      \
-    case RW_Q4_0: FN<RW_Q4_0>(__VA_ARGS__); break;   \
-    case RW_Q4_1: FN<RW_Q4_1>(__VA_ARGS__); break;   \
-    case RW_Q5_0: FN<RW_Q5_0>(__VA_ARGS__); break;   \
-    case RW_Q5_1: FN<RW_Q5_1>(__VA_ARGS__); break;   \
-    default: FN<RW_Q8_0>(__VA_ARGS__); break;        \
-  }
-
 #define RW_DISPATCH_GEMV(w, m, ...)                                              \
   switch ((w)->dtype) {                                                          \
     case RW_Q4_0: launch_gemv_dt<RW_Q4_0>((int)(m), __VA_ARGS__); break;         \
@@ -392,7 +411,7 @@ static int run_product(const rw_weight *w, size_t m, const float *bias, float *o
     RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, gemv_wgs(w, gemv_ks(w)), gemv_chunk((int)m, w->noct), s);
     LAUNCH_TRY("k_gemv2");
   } else {
-    RW_DISPATCH_DT(w->dtype, launch_gemm_dt, w, av, (int)m, bias, out, s);
+    run_gemm(&w, &bias, &out, 1, av, (int)m, s);
     LAUNCH_TRY("k_gemm");
   }
   return RW_OK;
@@ -716,6 +735,34 @@ int rw_rocm_matmul_prequant_dev(const rw_weight *w, const void *workspace, size_
   if (m > (size_t)INT32_MAX / 2) return fail(RW_EINVAL, "m = %zu is too large", m);
   HIP_TRY(hipSetDevice(w->device));
   return run_product(w, m, bias, out, workspace, (hipStream_t)stream);
+}
+
+int rw_rocm_matmul_prequant_multi_dev(const rw_weight *const *w, size_t count, const void *workspace, size_t m,
+                                      const float *const *bias, float *const *out, void *stream) {
+  if (!w || !out) return fail(RW_EINVAL, "weight or output array is NULL");
+  if (count < 1 || count > (size_t)GEMM_MAX_SET)
+    return fail(RW_EINVAL, "count = %zu: between 1 and %d weights per call", count, GEMM_MAX_SET);
+  for (size_t i = 0; i < count; ++i) {
+    if (!w[i] || !out[i]) return fail(RW_EINVAL, "weight or output %zu is NULL", i);
+    if (w[i]->dtype != w[0]->dtype || w[i]->k != w[0]->k || w[i]->device != w[0]->device)
+      return fail(RW_EINVAL, "weight %zu differs from weight 0 in dtype, k or device", i);
+  }
+  if (m == 0) return RW_OK;
+  if (!workspace) return fail(RW_EINVAL, "workspace is NULL");
+  if (m > (size_t)INT32_MAX / 2) return fail(RW_EINVAL, "m = %zu is too large", m);
+  HIP_TRY(hipSetDevice(w[0]->device));
+  hipStream_t s = (hipStream_t)stream;
+  if (m <= GEMV_MAX_M) {  // the decode shape: one GEMV launch per weight
+    for (size_t i = 0; i < count; ++i) {
+      int rc = run_product(w[i], m, bias ? bias[i] : nullptr, out[i], workspace, s);
+      if (rc) return rc;
+    }
+    return RW_OK;
+  }
+  ActLayout L = act_layout(m, w[0]->k);
+  run_gemm(w, bias, out, count, act_view(L, (void *)workspace), (int)m, s);
+  LAUNCH_TRY("k_gemm");
+  return RW_OK;
 }
 
 int rw_rocm_matmul_t_q(const rw_weight *w, const float *a, size_t m, size_t k, const float *bias, float *out) {

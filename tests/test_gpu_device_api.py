@@ -5,6 +5,10 @@ Bars (written in each test):
     values f16(q_a * f32(d_a * 2^(15-e))) of quantize_acts_i8's q_a and d_a,
     with 2^(e-1) <= the row's largest |x| < 2^e (e >= -110; 15 for zero or
     non-finite rows), and the row scales 2^(e-15);
+  * one launch for several weights on one quantized input matches the
+    oracle (1e-3 row-L2, and the regime's bound against the exact float64
+    combination), its rows do not depend on m, and in the decode shape it
+    is bitwise the single-weight call;
   * quantizing inside the decode launch and quantizing separately
     (rw_rocm_quantize_dev + rw_rocm_matmul_prequant_dev) give bitwise the
     same outputs, in both regimes;
@@ -21,7 +25,7 @@ import pytest
 import oracle as O
 from rusty_whisper_amd import _abi as A
 
-from _data import DTYPES, NAMES, activations, edge_activation_rows, rel_row_l2, weights
+from _data import DTYPES, NAMES, activations, check_combine, edge_activation_rows, rel_row_l2, weights
 
 pytestmark = pytest.mark.gpu
 
@@ -293,3 +297,63 @@ def test_gemm_activation_plane_bit_exact(torch, k):
     assert np.array_equal(plane[:m], want.view(np.uint16)), np.argwhere(plane[:m] != want.view(np.uint16))[:5]
     assert np.array_equal(rs[:m].view(np.uint32), want_rs.view(np.uint32))
     assert not plane[m:].any() and not rs[m:].any()  # padding rows of the last row group
+
+
+# (dtype, m, [n_i], k, [has bias]): q/k/v of the large-v3 encoder, ragged
+# widths, a single weight, four weights with a long row, and the decode shape
+MULTI = [
+    (7, 40, [1280, 1280, 1280], 1280, [True, False, True]),
+    (2, 70, [96, 33, 200], 416, [False, True, True]),
+    (8, 9, [64], 96, [True]),
+    (6, 33, [64, 64, 64, 64], 5120, [True, True, False, True]),
+    (3, 5, [70, 40], 256, [True, False]),
+]
+
+
+@pytest.mark.parametrize("dtype,m,ns,k,hasb", MULTI, ids=lambda x: str(x))
+def test_prequant_multi(torch, dtype, m, ns, k, hasb):
+    rng = np.random.default_rng(m + k)
+    raws = [weights(dtype, n, k, seed=17 * i + n) for i, n in enumerate(ns)]
+    ws_ = [A.DeviceWeight(dtype, n, k, raw) for n, raw in zip(ns, raws)]
+    biases = [rng.standard_normal(n).astype(np.float32) if hb else None for n, hb in zip(ns, hasb)]
+    a = activations(m, k, seed=m * 3 + k, outliers=0.01)
+    wsz = A.workspace_size(m, k)
+    ws = torch.empty(wsz, dtype=torch.uint8, device="cuda:0")
+    A.quantize_dev(_dev(torch, a), m, k, ws, wsz)
+
+    def run(mm):
+        outs = [torch.full((mm, n), float("nan"), device="cuda:0") for n in ns]
+        A.matmul_prequant_multi_dev(ws_, ws, mm, outs, [None if b is None else _dev(torch, b) for b in biases])
+        torch.cuda.synchronize()
+        return [o.cpu().numpy() for o in outs]
+
+    got = run(m)
+    for w, raw, b, y in zip(ws_, raws, biases, got):
+        ref = O.matmul_emul(a, dtype, raw, w.n, bias=b)
+        assert rel_row_l2(y, ref) <= NORTH_STAR_TOL
+        check_combine(y, a, dtype, raw, w.n, b)
+        if m <= A.GEMV_MAX_M:  # decode shape: bitwise the single-weight call
+            single = torch.empty(m, w.n, device="cuda:0")
+            w.matmul_prequant_dev(ws, m, single, None if b is None else _dev(torch, b))
+            torch.cuda.synchronize()
+            assert np.array_equal(_bits(single.cpu().numpy()), _bits(y))
+    if m > 9:  # rows do not depend on m: quantize the first 9 rows alone
+        A.quantize_dev(_dev(torch, a[:9]), 9, k, ws, wsz)
+        for y9, y in zip(run(9), got):
+            assert np.array_equal(_bits(y9), _bits(y[:9]))
+
+
+def test_prequant_multi_rejects_bad_sets(torch):
+    w1 = A.DeviceWeight(7, 64, 128, weights(7, 64, 128, seed=1))
+    w2 = A.DeviceWeight(7, 64, 96, weights(7, 64, 96, seed=2))
+    w3 = A.DeviceWeight(8, 64, 128, weights(8, 64, 128, seed=3))
+    ws = torch.zeros(A.workspace_size(20, 128), dtype=torch.uint8, device="cuda:0")
+    o = [torch.zeros(20, 64, device="cuda:0") for _ in range(5)]
+    with pytest.raises(A.RwError, match="differs"):
+        A.matmul_prequant_multi_dev([w1, w2], ws, 20, o[:2])
+    with pytest.raises(A.RwError, match="differs"):
+        A.matmul_prequant_multi_dev([w1, w3], ws, 20, o[:2])
+    with pytest.raises(A.RwError, match="count"):
+        A.matmul_prequant_multi_dev([w1] * 5, ws, 20, o)
+    with pytest.raises(A.RwError, match="count"):
+        A.matmul_prequant_multi_dev([], ws, 20, [])

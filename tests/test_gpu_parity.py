@@ -17,7 +17,7 @@ import pytest
 import oracle as O
 from rusty_whisper_amd import _abi as A
 
-from _data import DTYPES, NAMES, activations, edge_activation_rows, random_blocks, rel_row_l2, weights
+from _data import DTYPES, NAMES, activations, check_combine, edge_activation_rows, random_blocks, rel_row_l2, weights
 
 pytestmark = pytest.mark.gpu
 
@@ -27,59 +27,6 @@ NORTH_STAR_TOL = 1e-3
 @pytest.fixture(scope="module", autouse=True)
 def _device():
     A.init(0)
-
-
-def _abs_terms(a, dtype, raw, n):
-    """sum_bl |d_a d_b S| + |m_b d_a sum_a| in float64: the scale of the f32
-    combine's rounding error for each output."""
-    k = a.shape[1]
-    qa, da, sa = O.quantize_acts(a)
-    S = O.block_dots(dtype, raw, n, k, qa).astype(np.float64)  # [m, n, nb]
-    _, db, mb, _ = O.unpack_rows(dtype, raw, n, k)
-    t = np.abs(da[:, None, :].astype(np.float64) * db[None, :, :] * S)
-    t += np.abs(mb[None, :, :].astype(np.float64) * (da * sa)[:, None, :])
-    return t.sum(axis=2)
-
-
-def _check_exact_combine(got, a, dtype, raw, n, bias=None):
-    """Decode regime (exact block sums, f32 combine): within a few f32
-    roundings per block of the exact combination."""
-    exact = O.matmul_exact(a, dtype, raw, n, bias=bias)
-    nb = a.shape[1] // 32
-    scale = _abs_terms(a, dtype, raw, n)
-    if bias is not None:
-        scale = scale + np.abs(bias)[None, :]
-    # a few f32 roundings per block on the path (the scale product and the
-    # min term may be formed as short sums of exact products)
-    bound = (4 * nb + 8) * 2.0 ** -24 * scale + 1e-30
-    err = np.abs(got.astype(np.float64) - exact)
-    assert np.all(err <= bound), f"max err/bound {np.max(err / bound):.3g}"
-
-
-def _check_f16_combine(got, a, dtype, raw, n, bias=None):
-    """Encoder regime: f16 operands A' = d_a q_a and W' = d_b q_b + m_b (one
-    rounding each, relative 2^-11), exact products, f32 accumulation.  Per
-    output: |y - exact| <= (2^-10 + (k + 8) 2^-24) sum_j |a_j w_j| plus the
-    f16 subnormal floor, against the exact combination in float64."""
-    exact = O.matmul_exact(a, dtype, raw, n, bias=bias)
-    k = a.shape[1]
-    qa, da, _ = O.quantize_acts(a)
-    av = np.abs(qa.astype(np.float64) * np.repeat(da.astype(np.float64), 32, axis=1))
-    wv = np.abs(O.dequant(dtype, raw, n, k).astype(np.float64))
-    scale = av @ wv.T
-    floor = 2.0 ** -25 * av.sum(axis=1)[:, None] + 2.0 ** -30 * av.max(axis=1)[:, None] * wv.sum(axis=1)[None, :]
-    bound = (2.0 ** -10 + (k + 8) * 2.0 ** -24) * scale + floor + 1e-30
-    if bias is not None:
-        bound = bound + 2.0 ** -24 * np.abs(bias)[None, :]
-    err = np.abs(got.astype(np.float64) - exact)
-    assert np.all(err <= bound), f"max err/bound {np.max(err / bound):.3g}"
-
-
-def _check_combine(got, a, dtype, raw, n, bias=None):
-    if a.shape[0] <= A.GEMV_MAX_M:
-        _check_exact_combine(got, a, dtype, raw, n, bias)
-    else:
-        _check_f16_combine(got, a, dtype, raw, n, bias)
 
 
 # ------------------------------------------------------------ dequant
@@ -195,7 +142,7 @@ def test_matmul_parity(dtype, m, k, n):
     got = w.matmul(a)
     ref = O.matmul_emul(a, dtype, raw, n, tier=O.TIER_VNNI)
     assert rel_row_l2(got, ref) <= NORTH_STAR_TOL
-    _check_combine(got, a, dtype, raw, n)
+    check_combine(got, a, dtype, raw, n)
     got_b = w.matmul(a, bias)
     assert np.array_equal(got_b.view(np.uint32), (got + bias[None, :]).view(np.uint32))
     ref_b = O.matmul_emul(a, dtype, raw, n, bias=bias, tier=O.TIER_AVX2)
@@ -233,7 +180,7 @@ def test_scale_spread_and_outliers(dtype):
     got = A.DeviceWeight(dtype, n, k, raw).matmul(a)
     ref = O.matmul_emul(a, dtype, raw, n)
     assert rel_row_l2(got, ref) <= NORTH_STAR_TOL
-    _check_combine(got, a, dtype, raw, n)
+    check_combine(got, a, dtype, raw, n)
 
 
 # -------------------------------- the reference's own tests, on the GPU
@@ -345,7 +292,7 @@ def test_gemm_k_splits(dtype, m, k, n):
     got = w.matmul(a, bias)
     ref = O.matmul_emul(a, dtype, raw, n, bias=bias)
     assert rel_row_l2(got, ref) <= NORTH_STAR_TOL
-    _check_combine(got, a, dtype, raw, n, bias)
+    check_combine(got, a, dtype, raw, n, bias)
     # a row's result does not depend on m
     assert np.array_equal(w.matmul(a[:9], bias).view(np.uint32), got[:9].view(np.uint32))
 
