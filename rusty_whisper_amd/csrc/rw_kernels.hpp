@@ -697,6 +697,19 @@ __device__ inline void quants_to_f16(const uint32_t (&q)[4], v8h &b0, v8h &b1) {
 // memory operations of this wavefront are outstanding, nothing else
 RW_HD constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
+// A buffer resource over `bytes` bytes at `base` (gfx9 raw buffer: offsets
+// in bytes, loads past the end return zeros)
+__device__ inline __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ inline uint4 ldb_u4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ inline uint32_t ldb_u32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+
 // One lane's operands of one block of k_gemm: A (its 16-byte chunk of each
 // of the two MFMAs, for TM activation row groups) and B raw (its 16 quant
 // bytes and the block's (d, m), for TN weight row groups).
@@ -801,33 +814,33 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int
   const int nb = set.nb;
   const int nsw = nb > kw ? (nb - kw + KW - 1) / KW : 0;  // this wavefront's block count
 
-  // uniform bases at block kw (row groups past the end repeat the last one)
-  const uint8_t *abase[TM];
+  // operands through buffer loads: one resource per plane, a constant lane
+  // offset per row group, and the block's offset in a scalar register (no
+  // per-lane address arithmetic in the loop); row groups past the end repeat
+  // the last one
+  const auto ra = buffer_rsrc(a.a16, (uint32_t)a.mgroups * (uint32_t)nb * 2048u);
+  const auto rq = buffer_rsrc(gp.q8, (uint32_t)ngroups * (uint32_t)set.nb_pad * 1024u);
+  const auto rd = buffer_rsrc(gp.dm, (uint32_t)ngroups * (uint32_t)set.nb_pad * 128u);
+  uint32_t aoff[TM], qoff[TN], doff[TN];
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int g = min(by * TM + i, a.mgroups - 1);
-    abase[i] = reinterpret_cast<const uint8_t *>(a.a16 + a16_index(nb, g, kw, 0, 0));
-  }
-  const uint8_t *qbase[TN], *dbase[TN];
+  for (int i = 0; i < TM; ++i) aoff[i] = (uint32_t)min(by * TM + i, a.mgroups - 1) * (uint32_t)nb * 2048u + l * 16;
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
-    const int g = min(bx * TN + j, ngroups - 1);
-    const size_t s0 = ((size_t)g * set.nb_pad + kw) * RG;
-    qbase[j] = gp.q8 + s0 * 32;
-    dbase[j] = reinterpret_cast<const uint8_t *>(gp.dm + s0);
+    const uint32_t g = (uint32_t)min(bx * TN + j, ngroups - 1);
+    qoff[j] = g * (uint32_t)set.nb_pad * 1024u + r * 32 + 16 * h;
+    doff[j] = g * (uint32_t)set.nb_pad * 128u + r * 4;
   }
-  const int aof = l * 16, qof = r * 32 + 16 * h, dof = r * 4;
   auto load = [&](GemmStage<TM, TN> &st, int s) __attribute__((always_inline)) {
-    const size_t ao = (size_t)s * KW * 2048, qo = (size_t)s * KW * 1024, dmo = (size_t)s * KW * 128;
+    const uint32_t bl = (uint32_t)(kw + s * KW);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      st.a[i][0] = ldg_u4(abase[i] + ao + aof);
-      st.a[i][1] = ldg_u4(abase[i] + ao + 1024 + aof);
+      st.a[i][0] = ldb_u4(ra, aoff[i], bl * 2048u);
+      st.a[i][1] = ldb_u4(ra, aoff[i] + 1024, bl * 2048u);
     }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      st.q[j] = ldg_u4(qbase[j] + qo + qof);
-      st.dm[j] = ldg_u32(dbase[j] + dmo + dof);
+      st.q[j] = ldb_u4(rq, qoff[j], bl * 1024u);
+      st.dm[j] = ldb_u32(rd, doff[j], bl * 128u);
     }
   };
   auto deq = [&](const GemmStage<TM, TN> &st) __attribute__((always_inline)) {

@@ -307,9 +307,16 @@ static void launch_gemm_dt(const GemmSet &set, size_t tiles, const ActView &av, 
 }
 
 // one k_gemm launch for `count` (1 .. GEMM_MAX_SET) weights of one dtype and
-// k against the quantized activation `av`
-static void run_gemm(const rw_weight *const *w, const float *const *bias, float *const *out, size_t count,
-                     const ActView &av, int m, hipStream_t s) {
+// k against the quantized activation `av`.  The kernel addresses each plane
+// with 32-bit byte offsets (buffer loads), so every plane stays below 4 GiB.
+static int run_gemm(const rw_weight *const *w, const float *const *bias, float *const *out, size_t count,
+                    const ActView &av, int m, hipStream_t s) {
+  const size_t lim = (size_t)1 << 32;
+  if ((size_t)av.mgroups * (size_t)w[0]->nb * 2048 >= lim)
+    return fail(RW_EINVAL, "activation [%d, %zu] too large for the GEMM's 32-bit offsets", m, w[0]->k);
+  for (size_t i = 0; i < count; ++i)
+    if ((size_t)w[i]->ngroups * (size_t)w[i]->nb_pad * 1024 >= lim)
+      return fail(RW_EINVAL, "weight [%zu, %zu] too large for the GEMM's 32-bit offsets", w[i]->n, w[i]->k);
   GemmSet set{};
   set.count = (int)count;
   set.nb = w[0]->nb;
@@ -326,6 +333,8 @@ static void run_gemm(const rw_weight *const *w, const float *const *bias, float 
     tiles += cdiv(w[i]->ngroups, GEMM_TN);
   }
   RW_DISPATCH_DT(w[0]->dtype, launch_gemm_dt, set, tiles, av, m, s);
+  LAUNCH_TRY("k_gemm");
+  return RW_OK;
 }
 
 // ------------------------------------------------------ decode GEMV
@@ -411,8 +420,7 @@ static int run_product(const rw_weight *w, size_t m, const float *bias, float *o
     RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, gemv_wgs(w, gemv_ks(w)), gemv_chunk((int)m, w->noct), s);
     LAUNCH_TRY("k_gemv2");
   } else {
-    run_gemm(&w, &bias, &out, 1, av, (int)m, s);
-    LAUNCH_TRY("k_gemm");
+    return run_gemm(&w, &bias, &out, 1, av, (int)m, s);
   }
   return RW_OK;
 }
@@ -760,9 +768,7 @@ int rw_rocm_matmul_prequant_multi_dev(const rw_weight *const *w, size_t count, c
     return RW_OK;
   }
   ActLayout L = act_layout(m, w[0]->k);
-  run_gemm(w, bias, out, count, act_view(L, (void *)workspace), (int)m, s);
-  LAUNCH_TRY("k_gemm");
-  return RW_OK;
+  return run_gemm(w, bias, out, count, act_view(L, (void *)workspace), (int)m, s);
 }
 
 int rw_rocm_matmul_t_q(const rw_weight *w, const float *a, size_t m, size_t k, const float *bias, float *out) {
