@@ -29,7 +29,7 @@ LIB_ROCM = os.path.join(HERE, "librw_rocm.so")
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
-    "-std=c++17",
+    "-std=c++20",
     "-fPIC",
     "-shared",
     "-ffp-contract=off",

@@ -20,6 +20,7 @@
 // of order (k splits, chunking) depends on the weight's shape alone.
 #pragma once
 #include <hip/hip_fp16.h>
+#include <utility>
 #include <hip/hip_runtime.h>
 
 #include "rw_layout.hpp"
@@ -58,6 +59,19 @@ __device__ inline float ldg_f(const void *p) { return *(const float RW_GLOBAL_AS
 __device__ inline uint32_t ldg_u32(const void *p) { return *(const uint32_t RW_GLOBAL_AS *)p; }
 __device__ inline int32_t ldg_i32(const void *p) { return *(const int32_t RW_GLOBAL_AS *)p; }
 __device__ inline void stg_f(float *p, float v) { *(float RW_GLOBAL_AS *)(void *)p = v; }
+
+// A buffer resource over `bytes` bytes at `base` (gfx9 raw buffer: offsets
+// in bytes, loads past the end return zeros)
+__device__ inline __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ inline uint4 ldb_u4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ inline uint32_t ldb_u32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
 
 // ------------------------------------------------------------ scalar helpers
 
@@ -267,6 +281,28 @@ __global__ __launch_bounds__(256) void k_quantize(const float *__restrict__ a, i
   }
 }
 
+// Cross-lane moves within 8-lane groups on the VALU (DPP, gfx9 dpp_ctrl
+// encodings) instead of LDS-pipe shuffles
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+// the maximum over each 8-lane group, in every lane of it
+__device__ inline float max8(float b) {
+  b = fmaxf(b, dpp_f<0xB1>(b));   // quad_perm [1,0,3,2]: lane i ^ 1
+  b = fmaxf(b, dpp_f<0x4E>(b));   // quad_perm [2,3,0,1]: lane i ^ 2
+  b = fmaxf(b, dpp_f<0x141>(b));  // row_half_mirror: lane 7 - i of the 8
+  return b;
+}
+// lane T's value of each 8-lane group, in every lane of it (lt = lane % 8)
+template <int T>
+__device__ inline float bcast8(float v, int lt) {
+  constexpr int Q = T & 3;
+  const float x1 = dpp_f<Q | (Q << 2) | (Q << 4) | (Q << 6)>(v);  // quad_perm [Q,Q,Q,Q]
+  const float x2 = dpp_f<0x141>(x1);                             // the other quad's copy
+  return (lt >> 2) == (T >> 2) ? x1 : x2;
+}
+
 // quantize_acts_i8's q for v = x * inv as a float: round half away from
 // zero, clamp to +-127 (an infinite v, from an infinite inv, included),
 // NaN -> 0, and +0 (never -0) for zero
@@ -293,9 +329,15 @@ __device__ inline float quant_q(float v) {
 template <int NP>
 __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ a, int m, int k, int nb,
                                                       uint16_t *__restrict__ a16, float *__restrict__ rs) {
-  const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lb = lane >> 3, lt = lane & 7;
   const int g = row / RG, r = row % RG;
+  // stores: the plane as a buffer, this lane's place in a block as the
+  // vector offset, the block's place as the scalar offset
+  const auto ro = buffer_rsrc(a16, (uint32_t)((size_t)(m + RG - 1) / RG * RG * (size_t)k * 2));
+  const uint32_t voff = (uint32_t)(a16_index(nb, g, 0, r, 4 * lt) - a16_index(nb, g, 0, 0, 0)) * 2 +
+                        (uint32_t)lb * 2048u;
+  const uint32_t gbase = (uint32_t)a16_index(nb, g, 0, 0, 0) * 2;
   if (row >= m) {  // uniform per wavefront
     for (int bl = lb; bl < nb; bl += 8)
       *reinterpret_cast<uint2 *>(a16 + a16_index(nb, g, bl, r, 4 * lt)) = make_uint2(0u, 0u);
@@ -319,12 +361,8 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
     float amax = 0.0f;
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-      float b = fmaxf(fmaxf(fabsf(v[p].x), fabsf(v[p].y)), fmaxf(fabsf(v[p].z), fabsf(v[p].w)));
-      b = fmaxf(b, __shfl_xor(b, 1));
-      b = fmaxf(b, __shfl_xor(b, 2));
-      b = fmaxf(b, __shfl_xor(b, 4));
-      bam[p] = b;
-      amax = fmaxf(amax, b);
+      bam[p] = max8(fmaxf(fmaxf(fabsf(v[p].x), fabsf(v[p].y)), fmaxf(fabsf(v[p].z), fabsf(v[p].w))));
+      amax = fmaxf(amax, bam[p]);
     }
     return amax;
   };
@@ -359,22 +397,25 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
       dv[cc] = __fdiv_rn(b, 127.0f);
       iv[cc] = dv[cc] > 0.0f ? __fdiv_rn(1.0f, dv[cc]) : 0.0f;
     }
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      if (c * CB + 8 * p >= nb) break;  // uniform
-      const int bl = c * CB + 8 * p + lb;
-      const int src = (lane & ~7) | (p & 7);
-      const float inv = __shfl(iv[p >> 3], src);
-      const float dd = __shfl(dv[p >> 3], src) * down;
+    auto pass = [&](auto pc) __attribute__((always_inline)) {
+      constexpr int p = decltype(pc)::value;
+      const int b0 = c * CB + 8 * p;
+      if (b0 >= nb) return;  // uniform
+      const float inv = bcast8<p & 7>(iv[p >> 3], lt);
+      const float dd = bcast8<p & 7>(dv[p >> 3], lt) * down;
       const float q0 = quant_q(__fmul_rn(v[p].x, inv)), q1 = quant_q(__fmul_rn(v[p].y, inv));
       const float q2 = quant_q(__fmul_rn(v[p].z, inv)), q3 = quant_q(__fmul_rn(v[p].w, inv));
-      if (bl < nb) {
-        const h2v lo2 = {(_Float16)__fmul_rn(q0, dd), (_Float16)__fmul_rn(q1, dd)};
-        const h2v hi2 = {(_Float16)__fmul_rn(q2, dd), (_Float16)__fmul_rn(q3, dd)};
-        *reinterpret_cast<uint2 *>(a16 + a16_index(nb, g, bl, r, 4 * lt)) =
-            make_uint2(__builtin_bit_cast(uint32_t, lo2), __builtin_bit_cast(uint32_t, hi2));
+      const h2v lo2 = {(_Float16)__fmul_rn(q0, dd), (_Float16)__fmul_rn(q1, dd)};
+      const h2v hi2 = {(_Float16)__fmul_rn(q2, dd), (_Float16)__fmul_rn(q3, dd)};
+      if (b0 + lb < nb) {
+        __builtin_amdgcn_raw_buffer_store_b64(
+            (rw_u32x2){__builtin_bit_cast(uint32_t, lo2), __builtin_bit_cast(uint32_t, hi2)}, ro, voff,
+            gbase + (uint32_t)b0 * 2048u, 0);
       }
-    }
+    };
+    [&]<int... P>(std::integer_sequence<int, P...>) {
+      (pass(std::integral_constant<int, P>{}), ...);
+    }(std::make_integer_sequence<int, NP>{});
   }
   if (lane == 0) rs[row] = ldexpf(1.0f, e - 15);
 }
@@ -697,18 +738,6 @@ __device__ inline void quants_to_f16(const uint32_t (&q)[4], v8h &b0, v8h &b1) {
 // memory operations of this wavefront are outstanding, nothing else
 RW_HD constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
-// A buffer resource over `bytes` bytes at `base` (gfx9 raw buffer: offsets
-// in bytes, loads past the end return zeros)
-__device__ inline __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
-}
-__device__ inline uint4 ldb_u4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-  return make_uint4(v[0], v[1], v[2], v[3]);
-}
-__device__ inline uint32_t ldb_u32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
-}
 
 // One lane's operands of one block of k_gemm: A (its 16-byte chunk of each
 // of the two MFMAs, for TM activation row groups) and B raw (its 16 quant

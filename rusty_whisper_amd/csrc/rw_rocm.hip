@@ -246,6 +246,8 @@ static ActView act_view(const ActLayout &L, void *ws) {
 static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &L, void *ws, hipStream_t s) {
   char *b = (char *)ws;
   if (L.f16) {
+    if ((size_t)L.mgroups * RG * k * 2 >= ((size_t)1 << 32))
+      return fail(RW_EINVAL, "activation [%zu, %zu] too large for the GEMM layout's 32-bit offsets", m, k);
     // one wavefront per row, 4 rows per workgroup; NP passes of 8 blocks in
     // registers (longer rows are read twice)
     const unsigned wgs = (unsigned)((size_t)L.mgroups * RG / 4);
