@@ -111,6 +111,35 @@ __device__ inline uint32_t sub_bytes(uint32_t x, uint32_t c) {
 
 __device__ inline uint32_t rotl(uint32_t x, int t) { return t == 0 ? x : (x << t) | (x >> (32 - t)); }
 
+// Cross-lane moves within 8-lane groups on the VALU (DPP, gfx9 dpp_ctrl
+// encodings) instead of LDS-pipe shuffles
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+// the maximum over each 8-lane group, in every lane of it
+__device__ inline float max8(float b) {
+  b = fmaxf(b, dpp_f<0xB1>(b));   // quad_perm [1,0,3,2]: lane i ^ 1
+  b = fmaxf(b, dpp_f<0x4E>(b));   // quad_perm [2,3,0,1]: lane i ^ 2
+  b = fmaxf(b, dpp_f<0x141>(b));  // row_half_mirror: lane 7 - i of the 8
+  return b;
+}
+// the sum over each 8-lane group, in every lane of it
+__device__ inline int sum8(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false);
+  return v;
+}
+// lane T's value of each 8-lane group, in every lane of it (lt = lane % 8)
+template <int T>
+__device__ inline float bcast8(float v, int lt) {
+  constexpr int Q = T & 3;
+  const float x1 = dpp_f<Q | (Q << 2) | (Q << 4) | (Q << 6)>(v);  // quad_perm [Q,Q,Q,Q]
+  const float x2 = dpp_f<0x141>(x1);                             // the other quad's copy
+  return (lt >> 2) == (T >> 2) ? x1 : x2;
+}
+
 // --------------------------------------------------------------- k_repack
 
 template <int DT>
@@ -221,8 +250,8 @@ __global__ __launch_bounds__(256) void k_dequant(WeightView w, int row0, int nro
 // ------------------------------------------------------------- k_quantize
 
 // quantize_acts_i8 (src/quant.rs:691-716) for one 32-element block held by
-// 8 consecutive lanes, 4 elements each: amax over the block by lane
-// shuffles, d = amax / 127 and inv = 1 / d correctly rounded, q = round half
+// 8 consecutive lanes (aligned to 8), 4 elements each: amax over the block by
+// DPP moves, d = amax / 127 and inv = 1 / d correctly rounded, q = round half
 // away from zero of x * inv, clamped to +-127 (NaN -> 0), and sum(q).
 struct BlockQuant {
   int q0, q1, q2, q3, sum;
@@ -230,10 +259,7 @@ struct BlockQuant {
 };
 
 __device__ inline BlockQuant quantize_block8(float4 x) {
-  float amax = fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w)));
-  amax = fmaxf(amax, __shfl_xor(amax, 1));
-  amax = fmaxf(amax, __shfl_xor(amax, 2));
-  amax = fmaxf(amax, __shfl_xor(amax, 4));
+  const float amax = max8(fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
   BlockQuant b;
   b.d = __fdiv_rn(amax, 127.0f);
   const float inv = b.d > 0.0f ? __fdiv_rn(1.0f, b.d) : 0.0f;
@@ -241,11 +267,7 @@ __device__ inline BlockQuant quantize_block8(float4 x) {
   b.q1 = round_clamp_i8(__fmul_rn(x.y, inv));
   b.q2 = round_clamp_i8(__fmul_rn(x.z, inv));
   b.q3 = round_clamp_i8(__fmul_rn(x.w, inv));
-  int s = b.q0 + b.q1 + b.q2 + b.q3;
-  s += __shfl_xor(s, 1);
-  s += __shfl_xor(s, 2);
-  s += __shfl_xor(s, 4);
-  b.sum = s;
+  b.sum = sum8(b.q0 + b.q1 + b.q2 + b.q3);
   return b;
 }
 
@@ -281,28 +303,6 @@ __global__ __launch_bounds__(256) void k_quantize(const float *__restrict__ a, i
   }
 }
 
-// Cross-lane moves within 8-lane groups on the VALU (DPP, gfx9 dpp_ctrl
-// encodings) instead of LDS-pipe shuffles
-template <int CTRL>
-__device__ inline float dpp_f(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
-}
-// the maximum over each 8-lane group, in every lane of it
-__device__ inline float max8(float b) {
-  b = fmaxf(b, dpp_f<0xB1>(b));   // quad_perm [1,0,3,2]: lane i ^ 1
-  b = fmaxf(b, dpp_f<0x4E>(b));   // quad_perm [2,3,0,1]: lane i ^ 2
-  b = fmaxf(b, dpp_f<0x141>(b));  // row_half_mirror: lane 7 - i of the 8
-  return b;
-}
-// lane T's value of each 8-lane group, in every lane of it (lt = lane % 8)
-template <int T>
-__device__ inline float bcast8(float v, int lt) {
-  constexpr int Q = T & 3;
-  const float x1 = dpp_f<Q | (Q << 2) | (Q << 4) | (Q << 6)>(v);  // quad_perm [Q,Q,Q,Q]
-  const float x2 = dpp_f<0x141>(x1);                             // the other quad's copy
-  return (lt >> 2) == (T >> 2) ? x1 : x2;
-}
-
 // quantize_acts_i8's q for v = x * inv as a float: round half away from
 // zero, clamp to +-127 (an infinite v, from an infinite inv, included),
 // NaN -> 0, and +0 (never -0) for zero
@@ -316,9 +316,9 @@ __device__ inline float quant_q(float v) {
 // workgroup; rows >= m of the padded row groups are written as zeros), lanes
 // 8b + t holding elements 4t..4t+3 of blocks 8p + b.  The quantization is
 // quantize_acts_i8's (src/quant.rs:691-716) bit for bit: the block maxima
-// come from 8-lane shuffles, and the correctly rounded d = amax / 127 and
+// come from 8-lane DPP moves, and the correctly rounded d = amax / 127 and
 // inv = 1 / d of pass p are computed once, by lane p % 8 of each 8-lane
-// group, and read back by shuffle.  Each element is stored as
+// group, and read back by DPP broadcast.  Each element is stored as
 // f16(q_a * (d_a * 2^(15-e))) at its a16_index position, e chosen from the
 // row's largest |x| so that the largest value lands in [2^14, 2^15): no
 // value overflows, and every value keeps f16's full precision unless it is
