@@ -12,9 +12,10 @@
 //   k_gemm          encoder shape (m > 8): f16 MFMA GEMM of the quantized
 //                   activations' values against weights dequantized in
 //                   registers (d_b*q_b + m_b, one rounding to f16)
-//   k_gemv2         decoder shape (m <= 8): any number of linears in one
-//                   launch, activations quantized into LDS, one lane per
-//                   weight row, v_dot4_i32_i8 exact block sums
+//   k_gemv          decoder shape (m <= 8): any number of linears in one
+//                   launch, activations quantized into LDS, exact block
+//                   sums of 32 weight rows x all activation rows per
+//                   v_mfma_i32_32x32x32_i8
 //
 // Within a kernel family a row's result never depends on m: every choice
 // of order (k splits, chunking) depends on the weight's shape alone.
@@ -68,6 +69,10 @@ __device__ inline __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t 
 __device__ inline uint4 ldb_u4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
   return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ inline uint2 ldb_u2(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+  return make_uint2(v[0], v[1]);
 }
 __device__ inline uint32_t ldb_u32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
@@ -472,7 +477,7 @@ __global__ __launch_bounds__(64) void k_block_dots(WeightView w, ActView a, int 
   }
 }
 
-// ---------------------------------------------------------------- k_gemv2
+// ----------------------------------------------------------------- k_gemv
 
 
 // One linear of a decode-shape launch: out[m, n] = a[m, k] W^T (+ bias).
@@ -490,87 +495,90 @@ struct GemvItem {
   int pad;
 };
 
-// One octet (8 blocks) of one weight row, as loaded: quants, scales, mins and
-// (Q5) high-bit words.
-template <int DT>
-struct OctRegs {
-  uint4 q[DT == 8 ? 16 : 8];
-  uint4 d, m, h0, h1;
-};
-
-template <int DT>
-__device__ inline void load_oct(const WeightView &w, int g, int r, int o, OctRegs<DT> &x) {
-  const size_t sbase = (((size_t)g * w.noct + o) * RG + r) * OCT;
-  x.d = ldg_u4(w.d + sbase);
-  if (has_min(DT)) x.m = ldg_u4(w.m + sbase);
-  if (has_high(DT)) {
-    x.h0 = ldg_u4(w.qh + sbase);
-    x.h1 = ldg_u4(w.qh + sbase + 4);
-  }
-#pragma unroll
-  for (int b8 = 0; b8 < OCT; ++b8) {
-    const size_t slot = qs_slot(w, g, o * OCT + b8, r);
-    if (DT == 8) {
-      x.q[2 * b8] = ldg_u4(w.qs + slot * 32);
-      x.q[2 * b8 + 1] = ldg_u4(w.qs + slot * 32 + 16);
-    } else {
-      x.q[b8] = ldg_u4(w.qs + slot * 16);
-    }
-  }
-}
-
-// LDS record of one activation block for the decode kernel: MR x 32 int8
-// quants (natural order), MR x {d (f32), c (i32)}, MR x p (f32), padded to
-// 16 bytes.  c = -offset * sum(q) seeds the integer dot of the centered
-// formats (Q4_0: 8, Q5_0: 16) and is 0 otherwise; p = d * sum(q).
-RW_HD constexpr int gemv_rec_bytes(int mr) { return (mr * 44 + 15) & ~15; }
+// LDS record of one activation block for the decode kernel (m = MR rows):
+//   [0, 32 MR)         the rows' int8 quants, MFMA order (the A operand)
+//   [32 MR, +16)       zeros: the A operand of lanes whose row is >= MR
+//   SEED: i32[8]       -c * sum(q_a), c the centering offset of the format
+//                      (Q4_0: 8, Q5_0: 16, else 0)
+//   DA:   f32[8]       d_a
+//   PA:   f32[8]       d_a * sum(q_a) (min term)
+// Entries of rows >= MR in the three arrays are zero.
+RW_HD constexpr int gemv_rec_bytes(int mr) { return 32 * mr + 16 + 96; }
 
 // Decode shape (m = MR <= 8).  One launch covers any number of linears that
 // share (dtype, m); workgroup -> item through `wg_item` (GROUPED), or the
 // single item `one`.  The activation rows are quantized into LDS with the
 // arithmetic of k_quantize (so fused and separate quantization agree bit for
-// bit), `ch_oct` octets of blocks at a time, and weight rows stream past them
-// one per lane through v_dot4_i32_i8, a whole octet of loads in flight per
-// lane (four wavefronts per SIMD hide the latency; a second octet in
-// registers would cost one of them).  2^lks of the 4 wavefronts split a
-// row's octets (the split depends on the weight only); each walks its blocks
-// in increasing order whatever the chunking, and the parts meet in LDS in
-// wavefront order: a row's result depends on its weight row and activation
-// row alone.  Blocks past nb in the last octet meet zero weight planes (the
-// upload writes the padding as zeros) and zero activation records: they add
-// exactly +0.
+// bit), `ch_oct` octets of blocks at a time.  Each wavefront owns two row
+// groups (64 weight rows) and, per block, forms the exact integer sums of
+// all its rows against all activation rows with one
+// v_mfma_i32_32x32x32_i8 per row group: A = the activation block (rows
+// >= MR zero), B = the weight block unpacked to int8 in registers (the
+// centered formats' offset enters as the seed -c*sum(q_a)).  Lane (r, h) then holds the sums of weight row r against
+// activation rows 4h..4h+3 and folds them into f32 accumulators exactly as
+// a scalar loop would: acc += (d_a*d_b) * S, accm += m_b * (d_a*sum(q_a)).
+// 2^lks of the 4 wavefronts split a row's octets (the split depends on the
+// weight only); each walks its blocks in increasing order whatever the
+// chunking, and the parts meet in LDS in wavefront order: a row's result
+// depends on its weight row and activation row alone.  Blocks past nb in the
+// last octet meet zero weight planes (the upload writes the padding as
+// zeros) and zero activation records: they add exactly +0.
 template <int DT, int MR, bool GROUPED>
-__global__ __launch_bounds__(256) void k_gemv2(const GemvItem *__restrict__ items, const int *__restrict__ wg_item,
-                                               GemvItem one, int ch_oct) {
+__global__ __launch_bounds__(256, 4) void k_gemv(const GemvItem *__restrict__ items, const int *__restrict__ wg_item,
+                                              GemvItem one, int ch_oct) {
   extern __shared__ __align__(16) uint8_t lds[];
-  constexpr int REC = gemv_rec_bytes(MR), SC = MR * QK, PO = MR * (QK + 8);
+  constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR, SO = ZO + 16, DO = SO + 32, PO = DO + 32;
   constexpr int OFF = DT == 2 ? 8 : DT == 6 ? 16 : 0;  // centering offset
+  constexpr int QB = DT == 8 ? 32 : 16;                // qs bytes per row-block
   // the descriptor is wave-uniform: scalar loads from the table or kernarg
   const GemvItem I = GROUPED ? items[wg_item[blockIdx.x]] : one;
   const WeightView &w = I.w;
   const int nb = w.nb;
   const int lks = I.lks, KS = 1 << lks;
-  const int t = threadIdx.x, l = t & 63, wv = t >> 6;
+  const int t = threadIdx.x, l = t & 63, h = l >> 5, r = l & 31;
+  const int wv = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: scalar offsets, uniform loops
   const int set = wv >> lks, part = wv & (KS - 1);
-  const int g_raw = (((int)blockIdx.x - (GROUPED ? I.wg0 : 0)) * (4 >> lks) + set) * 2 + (l >> 5);
-  const int g = g_raw < w.ngroups ? g_raw : w.ngroups - 1;
-  const int r = l & 31;
+  const int gw = (((int)blockIdx.x - (GROUPED ? I.wg0 : 0)) * (4 >> lks) + set) * 2;  // first of 2 row groups
   const int o0 = (w.noct * part) >> lks, o1 = (w.noct * (part + 1)) >> lks;
 
-  float acc[MR], accm[MR];
-#pragma unroll
-  for (int i = 0; i < MR; ++i) {
-    acc[i] = 0.0f;
-    accm[i] = 0.0f;
+  // plane buffers (the upload keeps every plane below 4 GiB) and this lane's
+  // offsets in them: qs 8 (Q8_0: 16) bytes of row r's block for half h; d,
+  // m the row's 8 f16 of an octet; qh its 8 words
+  const uint32_t nsc = (uint32_t)w.ngroups * RG * (uint32_t)w.nb_pad;
+  const auto rq = buffer_rsrc(w.qs, nsc * QB);
+  const auto rd = buffer_rsrc(w.d, nsc * 2);
+  const auto rm = buffer_rsrc(w.m, has_min(DT) ? nsc * 2 : 0);
+  const auto rh = buffer_rsrc(w.qh, has_high(DT) ? nsc * 4 : 0);
+  const uint32_t vq = r * QB + (QB / 2) * h, vs = r * 16, vh = r * 32;
+  const int a_off = r < MR ? 32 * r + 16 * h : ZO;
+  const int rot = (32 - 2 * h) & 31;  // rotr by this = rotl by 2h
+
+  // zero the parts of every record slot the chunks never write
+  {
+    constexpr int NZ = 8 - MR > 0 ? 8 - MR : 1, ZW = 4 + 3 * (8 - MR);
+    for (int z = t; z < ch_oct * OCT * ZW; z += 256) {
+      const int s = z / ZW, u = z - s * ZW;
+      const int off = u < 4 ? ZO + 4 * u : SO + 32 * ((u - 4) / NZ) + 4 * (MR + (u - 4) % NZ);
+      *reinterpret_cast<uint32_t *>(lds + s * REC + off) = 0u;
+    }
   }
+
+  float acc[2][4], accm[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      acc[j][v] = 0.0f;
+      accm[j][v] = 0.0f;
+    }
 
   for (int c0 = 0; c0 < w.noct; c0 += ch_oct) {
     const int c1 = min(w.noct, c0 + ch_oct);
     const int bb0 = c0 * OCT, cnb = min(nb, c1 * OCT) - bb0;
     if (c0) __syncthreads();  // every wavefront is done with the previous chunk
-    // --- activation records of blocks [bb0, bb0 + cnb) -> LDS; (row, block)
-    // pairs in row-major order, 4 passes of 32 per batch so their global
-    // loads are in flight together
+    // --- activation records of blocks [bb0, bb0 + cnb) -> LDS; (block, row)
+    // pairs block-major, 4 passes of 32 per batch so their global loads are
+    // in flight together
     const int total = MR * cnb;
     if (I.a) {
       for (int rb0 = 0; rb0 < total; rb0 += 128) {
@@ -580,8 +588,8 @@ __global__ __launch_bounds__(256) void k_gemv2(const GemvItem *__restrict__ item
           const int rb = rb0 + 32 * u + (t >> 3), lt = t & 7;
           x[u] = make_float4(0.f, 0.f, 0.f, 0.f);
           if (rb < total) {
-            const int i = rb / cnb, bl = bb0 + rb % cnb;
-            x[u] = ldg_f4(I.a + ((size_t)i * nb + bl) * QK + 4 * lt);
+            const int lb = rb / MR, i = rb - lb * MR;
+            x[u] = ldg_f4(I.a + ((size_t)i * nb + bb0 + lb) * QK + 4 * lt);
           }
         }
 #pragma unroll
@@ -589,27 +597,28 @@ __global__ __launch_bounds__(256) void k_gemv2(const GemvItem *__restrict__ item
           const int rb = rb0 + 32 * u + (t >> 3), lt = t & 7;
           const BlockQuant bq = quantize_block8(x[u]);
           if (rb < total) {
-            const int i = rb / cnb, lb = rb % cnb;
+            const int lb = rb / MR, i = rb - lb * MR;
             uint8_t *rec = lds + lb * REC;
-            *reinterpret_cast<uint32_t *>(rec + i * QK + 4 * lt) = pack_q4(bq);
+            *reinterpret_cast<uint32_t *>(rec + 32 * i + mfma_pos(4 * lt)) = pack_q4(bq);
             if (lt == 0) {
-              *reinterpret_cast<int2 *>(rec + SC + 8 * i) = make_int2(__float_as_int(bq.d), -OFF * bq.sum);
+              *reinterpret_cast<int *>(rec + SO + 4 * i) = -OFF * bq.sum;
+              *reinterpret_cast<float *>(rec + DO + 4 * i) = bq.d;
               *reinterpret_cast<float *>(rec + PO + 4 * i) = __fmul_rn(bq.d, (float)bq.sum);
             }
           }
         }
       }
     } else {
-      // already quantized: row group 0 of the activation layout, MFMA order
+      // already quantized: row group 0 of the activation layout (MFMA order)
       for (int idx = t; idx < total * 8; idx += 256) {
         const int rb = idx >> 3, lt = idx & 7;
-        const int i = rb / cnb, lb = rb % cnb;
+        const int lb = rb / MR, i = rb - lb * MR;
         const size_t slot = act_slot(nb, 0, bb0 + lb, i);
         uint8_t *rec = lds + lb * REC;
-        *reinterpret_cast<uint32_t *>(rec + i * QK + 4 * lt) = ldg_u32(I.qa + slot * QK + mfma_pos(4 * lt));
+        *reinterpret_cast<uint32_t *>(rec + 32 * i + 4 * lt) = ldg_u32(I.qa + slot * QK + 4 * lt);
         if (lt == 0) {
-          *reinterpret_cast<int2 *>(rec + SC + 8 * i) =
-              make_int2(__float_as_int(ldg_f(I.qda + slot)), -OFF * ldg_i32(I.qsa + slot));
+          *reinterpret_cast<int *>(rec + SO + 4 * i) = -OFF * ldg_i32(I.qsa + slot);
+          *reinterpret_cast<float *>(rec + DO + 4 * i) = ldg_f(I.qda + slot);
           *reinterpret_cast<float *>(rec + PO + 4 * i) = ldg_f(I.qpa + slot);
         }
       }
@@ -620,97 +629,130 @@ __global__ __launch_bounds__(256) void k_gemv2(const GemvItem *__restrict__ item
       reinterpret_cast<uint4 *>(lds + cnb * REC)[z] = make_uint4(0, 0, 0, 0);
     __syncthreads();
 
-    // --- weights: one row per lane, this part's octets inside the chunk,
-    // each loaded whole (the planes are padded to whole octets)
+    // --- weights: this part's octets inside the chunk, each loaded whole
+    // for both row groups (the planes are padded to whole octets)
     const int p0 = max(o0, c0), p1 = min(o1, c1);
-    if (p0 < p1) {
-      for (int o = p0; o < p1; ++o) {
-        OctRegs<DT> cur;
-        load_oct<DT>(w, g, r, o, cur);
-        const uint32_t dw[4] = {cur.d.x, cur.d.y, cur.d.z, cur.d.w};
-        const uint32_t mw[4] = {cur.m.x, cur.m.y, cur.m.z, cur.m.w};
-        const uint32_t hw[8] = {cur.h0.x, cur.h0.y, cur.h0.z, cur.h0.w, cur.h1.x, cur.h1.y, cur.h1.z, cur.h1.w};
-        const uint8_t *orec = lds + (o - c0) * OCT * REC;
+    for (int o = p0; o < p1; ++o) {
+      v4i q[2][8];
+      uint4 dd[2], mm[2], h0[2], h1[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int g = min(gw + j, w.ngroups - 1);
+        const uint32_t sq = (uint32_t)(g * w.nb_pad + o * OCT) * (RG * QB);
+        const uint32_t ss = (uint32_t)(g * w.noct + o) * (RG * 16);
+        dd[j] = ldb_u4(rd, vs, ss);
+        if (has_min(DT)) mm[j] = ldb_u4(rm, vs, ss);
+        if (has_high(DT)) {
+          h0[j] = ldb_u4(rh, vh, 2 * ss);
+          h1[j] = ldb_u4(rh, vh + 16, 2 * ss);
+        }
 #pragma unroll
         for (int b8 = 0; b8 < OCT; ++b8) {
-          const float db = h2f((uint16_t)(dw[b8 >> 1] >> (16 * (b8 & 1))));
-          const float mb = has_min(DT) ? h2f((uint16_t)(mw[b8 >> 1] >> (16 * (b8 & 1)))) : 0.0f;
-          // the block's 32 quants as 8 natural dwords: dword u = elements 4u..4u+3
-          uint32_t wd[8];
           if (DT == 8) {
-            // stored in MFMA order: stored dwords 0..7 hold natural dwords 0,1,4,5,2,3,6,7
-            const uint4 q0 = cur.q[2 * b8], q1 = cur.q[2 * b8 + 1];
-            wd[0] = q0.x; wd[1] = q0.y; wd[4] = q0.z; wd[5] = q0.w;
-            wd[2] = q1.x; wd[3] = q1.y; wd[6] = q1.z; wd[7] = q1.w;
+            const uint4 x = ldb_u4(rq, vq, sq + b8 * (RG * QB));
+            q[j][b8] = v4i{(int)x.x, (int)x.y, (int)x.z, (int)x.w};
           } else {
-            const uint4 q = cur.q[b8];
-            const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              wd[u] = qq[u] & 0x0f0f0f0fu;
-              wd[u + 4] = (qq[u] >> 4) & 0x0f0f0f0fu;
-            }
-            if (has_high(DT)) {
-              const uint32_t x = hw[b8];
-#pragma unroll
-              for (int u = 0; u < 8; ++u) wd[u] |= rotl(x, u) & 0x10101010u;
-            }
+            const uint2 x = ldb_u2(rq, vq, sq + b8 * (RG * QB));
+            q[j][b8] = v4i{(int)x.x, (int)x.y, 0, 0};
           }
-          const uint8_t *rec = orec + b8 * REC;
+        }
+      }
+      const uint8_t *orec = lds + (o - c0) * OCT * REC;
 #pragma unroll
-          for (int i = 0; i < MR; ++i) {
-            const int4 a0 = *reinterpret_cast<const int4 *>(rec + i * QK);
-            const int4 a1 = *reinterpret_cast<const int4 *>(rec + i * QK + 16);
-            const int2 sc = *reinterpret_cast<const int2 *>(rec + SC + 8 * i);
-            // centered formats: sum(q_a*(q-c)) = sum(q_a*q) - c*sum(q_a)
-            int s = sc.y;
-            s = __builtin_amdgcn_sdot4((int)wd[0], a0.x, s, false);
-            s = __builtin_amdgcn_sdot4((int)wd[1], a0.y, s, false);
-            s = __builtin_amdgcn_sdot4((int)wd[2], a0.z, s, false);
-            s = __builtin_amdgcn_sdot4((int)wd[3], a0.w, s, false);
-            s = __builtin_amdgcn_sdot4((int)wd[4], a1.x, s, false);
-            s = __builtin_amdgcn_sdot4((int)wd[5], a1.y, s, false);
-            s = __builtin_amdgcn_sdot4((int)wd[6], a1.z, s, false);
-            s = __builtin_amdgcn_sdot4((int)wd[7], a1.w, s, false);
-            acc[i] = __builtin_fmaf(__int_as_float(sc.x) * db, (float)s, acc[i]);
-            if (has_min(DT)) accm[i] = __builtin_fmaf(mb, *reinterpret_cast<const float *>(rec + PO + 4 * i), accm[i]);
+      for (int b8 = 0; b8 < OCT; ++b8) {
+        const uint8_t *rec = orec + b8 * REC;
+        const v4i aop = *reinterpret_cast<const v4i *>(rec + a_off);
+        const float4 da = *reinterpret_cast<const float4 *>(rec + DO + 16 * h);
+        int4 sd = make_int4(0, 0, 0, 0);
+        if (OFF) sd = *reinterpret_cast<const int4 *>(rec + SO + 16 * h);
+        const int sdv[4] = {sd.x, sd.y, sd.z, sd.w};
+        float4 pa = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (has_min(DT)) pa = *reinterpret_cast<const float4 *>(rec + PO + 16 * h);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          v4i bop;
+          if (DT == 8) {
+            bop = q[j][b8];
+          } else {
+            // low nibbles: elements 8h..8h+7, high nibbles: 16+8h..16+8h+7
+            const uint32_t x0 = (uint32_t)q[j][b8].x, x1 = (uint32_t)q[j][b8].y;
+            uint32_t w0 = x0 & 0x0f0f0f0fu, w1 = x1 & 0x0f0f0f0fu;
+            uint32_t w2 = (x0 >> 4) & 0x0f0f0f0fu, w3 = (x1 >> 4) & 0x0f0f0f0fu;
+            if (has_high(DT)) {
+              const uint32_t hw[8] = {h0[j].x, h0[j].y, h0[j].z, h0[j].w, h1[j].x, h1[j].y, h1[j].z, h1[j].w};
+              // natural dwords 2h, 2h+1, 4+2h, 5+2h of the block
+              const uint32_t xh = __builtin_amdgcn_alignbit(hw[b8], hw[b8], rot);
+              w0 |= xh & 0x10101010u;
+              w1 |= rotl(xh, 1) & 0x10101010u;
+              w2 |= rotl(xh, 4) & 0x10101010u;
+              w3 |= rotl(xh, 5) & 0x10101010u;
+            }
+            bop = v4i{(int)w0, (int)w1, (int)w2, (int)w3};
+          }
+          const v16i s = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, v16i{}, 0, 0, 0);
+          const uint32_t dw = (b8 >> 1) == 0 ? dd[j].x : (b8 >> 1) == 1 ? dd[j].y : (b8 >> 1) == 2 ? dd[j].z : dd[j].w;
+          const float db = h2f((uint16_t)(dw >> (16 * (b8 & 1))));
+          const float dav[4] = {da.x, da.y, da.z, da.w};
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[j][v] = __builtin_fmaf(dav[v] * db, (float)(s[v] + sdv[v]), acc[j][v]);
+          if (has_min(DT)) {
+            const uint32_t mw = (b8 >> 1) == 0 ? mm[j].x : (b8 >> 1) == 1 ? mm[j].y : (b8 >> 1) == 2 ? mm[j].z : mm[j].w;
+            const float mb = h2f((uint16_t)(mw >> (16 * (b8 & 1))));
+            const float pav[4] = {pa.x, pa.y, pa.z, pa.w};
+#pragma unroll
+            for (int v = 0; v < 4; ++v) accm[j][v] = __builtin_fmaf(mb, pav[v], accm[j][v]);
           }
         }
       }
     }
   }
 
-  float y[MR];
+  float y[2][4];
 #pragma unroll
-  for (int i = 0; i < MR; ++i) y[i] = has_min(DT) ? acc[i] + accm[i] : acc[i];
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) y[j][v] = has_min(DT) ? acc[j][v] + accm[j][v] : acc[j][v];
 
   const int n = I.n;
-  const int col = g_raw * RG + r;
   if (KS == 1) {
-    if (g_raw < w.ngroups && col < n)
 #pragma unroll
-      for (int i = 0; i < MR; ++i) stg_f(I.out + (size_t)i * n + col, I.bias ? y[i] + ldg_f(I.bias + col) : y[i]);
+    for (int j = 0; j < 2; ++j) {
+      const int g = gw + j, col = g * RG + r;
+      if (g < w.ngroups && col < n)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (4 * h + v < MR)
+            stg_f(I.out + (size_t)(4 * h + v) * n + col, I.bias ? y[j][v] + ldg_f(I.bias + col) : y[j][v]);
+    }
     return;
   }
   __syncthreads();  // the activation LDS is reused for the partial sums
-  float *red = reinterpret_cast<float *>(lds);  // [4 wavefronts][MR][64]
+  float *red = reinterpret_cast<float *>(lds);  // [4 wavefronts][2 groups x 4][64]
 #pragma unroll
-  for (int i = 0; i < MR; ++i) red[(wv * MR + i) * 64 + l] = y[i];
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[(wv * 8 + 4 * j + v) * 64 + l] = y[j][v];
   __syncthreads();
-  if (part == 0 && g_raw < w.ngroups && col < n) {
+  if (part == 0) {
 #pragma unroll
-    for (int i = 0; i < MR; ++i) {
-      float tt = red[(wv * MR + i) * 64 + l];
-      for (int p = 1; p < KS; ++p) tt = tt + red[((wv + p) * MR + i) * 64 + l];
-      stg_f(I.out + (size_t)i * n + col, I.bias ? tt + ldg_f(I.bias + col) : tt);
+    for (int j = 0; j < 2; ++j) {
+      const int g = gw + j, col = g * RG + r;
+      if (g < w.ngroups && col < n)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (4 * h + v < MR) {
+            float tt = red[(wv * 8 + 4 * j + v) * 64 + l];
+            for (int p = 1; p < KS; ++p) tt = tt + red[((wv + p) * 8 + 4 * j + v) * 64 + l];
+            stg_f(I.out + (size_t)(4 * h + v) * n + col, I.bias ? tt + ldg_f(I.bias + col) : tt);
+          }
     }
   }
 }
 
-// LDS bytes k_gemv2 needs for m rows and chunks of ch_oct octets
+// LDS bytes k_gemv needs for m rows and chunks of ch_oct octets
 RW_HD inline size_t gemv_lds_bytes(int m, int ch_oct) {
   const size_t act = (size_t)ch_oct * OCT * gemv_rec_bytes(m);
-  const size_t red = (size_t)4 * m * 64 * 4;
+  const size_t red = (size_t)4 * 8 * 64 * 4;
   return act > red ? act : red;
 }
 

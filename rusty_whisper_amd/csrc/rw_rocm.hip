@@ -9,7 +9,7 @@
 //   - one-time upload + repack of a weight (QTensor::new plus the packed int8
 //     cache, src/quant.rs:553-563, 589-639);
 //   - regime dispatch (src/quant.rs:754-1051 picks tiers by CPU; here m
-//     picks the kernel: m <= 8 -> k_gemv2, else k_quantize + k_gemm2);
+//     picks the kernel: m <= 8 -> k_gemv, else k_quantize_f16 + k_gemm);
 //   - thread safety: host-pointer calls borrow a (stream, buffers) context
 //     from a per-device pool, so concurrent callers never share buffers.
 #include <hip/hip_fp16.h>
@@ -375,14 +375,14 @@ template <int DT, int MR>
 static void launch_gemv_mr(const GemvItem *items, const int *wg_item, const GemvItem &one, int wgs, int ch_oct,
                            hipStream_t s) {
   if (items)
-    hipLaunchKernelGGL((k_gemv2<DT, MR, true>), dim3((unsigned)wgs), dim3(256), gemv_lds_bytes(MR, ch_oct), s,
+    hipLaunchKernelGGL((k_gemv<DT, MR, true>), dim3((unsigned)wgs), dim3(256), gemv_lds_bytes(MR, ch_oct), s,
                        items, wg_item, one, ch_oct);
   else
-    hipLaunchKernelGGL((k_gemv2<DT, MR, false>), dim3((unsigned)wgs), dim3(256), gemv_lds_bytes(MR, ch_oct), s,
+    hipLaunchKernelGGL((k_gemv<DT, MR, false>), dim3((unsigned)wgs), dim3(256), gemv_lds_bytes(MR, ch_oct), s,
                        items, wg_item, one, ch_oct);
 }
 
-// one k_gemv2 launch: `items` (device) + `wg_item` (device) for a group, or
+// one k_gemv launch: `items` (device) + `wg_item` (device) for a group, or
 // items == NULL and the single item `one`
 template <int DT>
 static void launch_gemv_dt(int m, const GemvItem *items, const int *wg_item, const GemvItem &one, int wgs,
@@ -420,7 +420,7 @@ static int run_product(const rw_weight *w, size_t m, const float *bias, float *o
     one.qpa = av.pa;
     one.qsa = av.sa;
     RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, gemv_wgs(w, gemv_ks(w)), gemv_chunk((int)m, w->noct), s);
-    LAUNCH_TRY("k_gemv2");
+    LAUNCH_TRY("k_gemv");
   } else {
     return run_gemm(&w, &bias, &out, 1, av, (int)m, s);
   }
@@ -435,7 +435,7 @@ static int run_matmul(const rw_weight *w, const float *a, size_t m, const float 
   if (m <= GEMV_MAX_M) {
     GemvItem one = gemv_item(w, a, bias, out);
     RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, gemv_wgs(w, gemv_ks(w)), gemv_chunk((int)m, w->noct), s);
-    LAUNCH_TRY("k_gemv2");
+    LAUNCH_TRY("k_gemv");
     return RW_OK;
   }
   ActLayout L = act_layout(m, w->k);
@@ -446,7 +446,7 @@ static int run_matmul(const rw_weight *w, const float *a, size_t m, const float 
 
 // ------------------------------------------------- grouped decode GEMV
 
-// A grouped call becomes one k_gemv2 launch per distinct (dtype, m);
+// A grouped call becomes one k_gemv launch per distinct (dtype, m);
 // the item table and the workgroup -> item map go to the device in one copy.
 struct GroupLaunch {
   int dt, m, wgs, ch_oct, wg_first;
@@ -547,7 +547,7 @@ static int launch_group(const std::vector<GroupLaunch> &launches, const void *ta
       case RW_Q5_1: launch_gemv_dt<RW_Q5_1>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.ch_oct, s); break;
       default: launch_gemv_dt<RW_Q8_0>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.ch_oct, s); break;
     }
-    LAUNCH_TRY("k_gemv2 (grouped)");
+    LAUNCH_TRY("k_gemv (grouped)");
   }
   return RW_OK;
 }
@@ -639,6 +639,11 @@ int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, siz
   size_t off_dm = align_up(off_m + (has_min(dtype) ? nsc * 2 : 0), 256);
   size_t off_q8 = align_up(off_dm + nsc * 4, 256);  // the GEMM's byte plane (Q8_0 reads qs)
   w->bytes = align_up(off_q8 + (dtype == RW_Q8_0 ? 0 : nsc * 32), 256);
+  // the kernels address each plane with 32-bit byte offsets
+  if (nsc * 32 >= ((size_t)1 << 32)) {
+    delete w;
+    return fail(RW_EINVAL, "shape [%zu, %zu]: a resident plane would exceed 4 GiB", n, k);
+  }
   if (hipMalloc(&w->base, w->bytes) != hipSuccess) {
     (void)hipGetLastError();
     delete w;
