@@ -60,6 +60,9 @@ __device__ inline float ldg_f(const void *p) { return *(const float RW_GLOBAL_AS
 __device__ inline uint32_t ldg_u32(const void *p) { return *(const uint32_t RW_GLOBAL_AS *)p; }
 __device__ inline int32_t ldg_i32(const void *p) { return *(const int32_t RW_GLOBAL_AS *)p; }
 __device__ inline void stg_f(float *p, float v) { *(float RW_GLOBAL_AS *)(void *)p = v; }
+__device__ inline void stg_u4(void *p, uint4 v) {
+  *(rw_u32x4 RW_GLOBAL_AS *)p = rw_u32x4{v.x, v.y, v.z, v.w};
+}
 
 // A buffer resource over `bytes` bytes at `base` (gfx9 raw buffer: offsets
 // in bytes, loads past the end return zeros)
@@ -489,10 +492,12 @@ struct GemvItem {
   const int32_t *qsa;
   const float *bias;
   float *out;
+  uint8_t *rec;  // activation records [noct*8][gemv_rec_bytes(m)] written by
+                 // k_gemv_records (grouped launches), or NULL
   int n;
-  int wg0;  // first workgroup of this item in the launch
-  int lks;  // log2 of the number of wavefronts that split a row's octets
-  int pad;
+  int wg0;   // first workgroup of this item in the launch
+  int qwg0;  // first workgroup of this item in its k_gemv_records launch
+  int lks;   // log2 of the number of wavefronts that split a row's octets
 };
 
 // LDS record of one activation block for the decode kernel (m = MR rows):
@@ -505,18 +510,112 @@ struct GemvItem {
 // Entries of rows >= MR in the three arrays are zero.
 RW_HD constexpr int gemv_rec_bytes(int mr) { return 32 * mr + 16 + 96; }
 
+// Zero the parts of record slots [0, nslots) that gemv_fill never writes:
+// the 16-byte zero A operand and the SEED / DA / PA entries of rows >= MR.
+template <int MR>
+__device__ inline void gemv_zero_slots(uint8_t *lds, int nslots, int t) {
+  constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR, SO = ZO + 16;
+  constexpr int NZ = 8 - MR > 0 ? 8 - MR : 1, ZW = 4 + 3 * (8 - MR);
+  for (int z = t; z < nslots * ZW; z += 256) {
+    const int s = z / ZW, u = z - s * ZW;
+    const int off = u < 4 ? ZO + 4 * u : SO + 32 * ((u - 4) / NZ) + 4 * (MR + (u - 4) % NZ);
+    *reinterpret_cast<uint32_t *>(lds + s * REC + off) = 0u;
+  }
+}
+
+// Activation records of octets [c0, c1) (blocks [8 c0, min(nb, 8 c1))) into
+// LDS at `base`: quantized here from f32 (I.a, the arithmetic of k_quantize,
+// so fused and separate quantization agree bit for bit)
+// or copied from an already quantized workspace (I.qa).  (block, row) pairs
+// block-major, 4 passes of 32 per batch so their global loads are in flight
+// together.  Records of the tail blocks past nb are zeroed.
+template <int DT, int MR>
+__device__ inline void gemv_fill(const GemvItem &I, int nb, int c0, int c1, uint8_t *base, int t) {
+  constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR, SO = ZO + 16, DO = SO + 32, PO = DO + 32;
+  constexpr int OFF = DT == 2 ? 8 : DT == 6 ? 16 : 0;
+  const int bb0 = c0 * OCT, cnb = min(nb, c1 * OCT) - bb0;
+  const int total = MR * cnb;
+  if (I.a) {
+    for (int rb0 = 0; rb0 < total; rb0 += 128) {
+      float4 x[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int rb = rb0 + 32 * u + (t >> 3), lt = t & 7;
+        x[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (rb < total) {
+          const int lb = rb / MR, i = rb - lb * MR;
+          x[u] = ldg_f4(I.a + ((size_t)i * nb + bb0 + lb) * QK + 4 * lt);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int rb = rb0 + 32 * u + (t >> 3), lt = t & 7;
+        const BlockQuant bq = quantize_block8(x[u]);
+        if (rb < total) {
+          const int lb = rb / MR, i = rb - lb * MR;
+          uint8_t *rec = base + lb * REC;
+          *reinterpret_cast<uint32_t *>(rec + 32 * i + mfma_pos(4 * lt)) = pack_q4(bq);
+          if (lt == 0) {
+            *reinterpret_cast<int *>(rec + SO + 4 * i) = -OFF * bq.sum;
+            *reinterpret_cast<float *>(rec + DO + 4 * i) = bq.d;
+            *reinterpret_cast<float *>(rec + PO + 4 * i) = __fmul_rn(bq.d, (float)bq.sum);
+          }
+        }
+      }
+    }
+  } else {
+    // already quantized: row group 0 of the activation layout (MFMA order)
+    for (int idx = t; idx < total * 8; idx += 256) {
+      const int rb = idx >> 3, lt = idx & 7;
+      const int lb = rb / MR, i = rb - lb * MR;
+      const size_t slot = act_slot(nb, 0, bb0 + lb, i);
+      uint8_t *rec = base + lb * REC;
+      *reinterpret_cast<uint32_t *>(rec + 32 * i + 4 * lt) = ldg_u32(I.qa + slot * QK + 4 * lt);
+      if (lt == 0) {
+        *reinterpret_cast<int *>(rec + SO + 4 * i) = -OFF * ldg_i32(I.qsa + slot);
+        *reinterpret_cast<float *>(rec + DO + 4 * i) = ldg_f(I.qda + slot);
+        *reinterpret_cast<float *>(rec + PO + 4 * i) = ldg_f(I.qpa + slot);
+      }
+    }
+  }
+  const int dead = (c1 - c0) * OCT - cnb;
+  for (int z = t; z < dead * (REC / 16); z += 256)
+    reinterpret_cast<uint4 *>(base + cnb * REC)[z] = make_uint4(0, 0, 0, 0);
+}
+
+// Activation records of a grouped decode launch, quantized once per linear
+// instead of once per k_gemv workgroup: workgroup -> (item, pair of octets)
+// through `qwg_item`; the records (zero parts included) are built in LDS
+// by gemv_fill, exactly as k_gemv builds them, and copied to the item's
+// record buffer.
+template <int DT, int MR>
+__global__ __launch_bounds__(256) void k_gemv_records(const GemvItem *__restrict__ items,
+                                                      const int *__restrict__ qwg_item) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr int REC = gemv_rec_bytes(MR);
+  const GemvItem I = items[qwg_item[blockIdx.x]];
+  const int t = threadIdx.x;
+  const int c0 = 2 * ((int)blockIdx.x - I.qwg0), c1 = min(I.w.noct, c0 + 2);
+  gemv_zero_slots<MR>(lds, (c1 - c0) * OCT, t);
+  gemv_fill<DT, MR>(I, I.w.nb, c0, c1, lds, t);
+  __syncthreads();
+  uint4 *dst = reinterpret_cast<uint4 *>(I.rec + (size_t)c0 * OCT * REC);
+  for (int z = t; z < (c1 - c0) * OCT * (REC / 16); z += 256) stg_u4(dst + z, reinterpret_cast<const uint4 *>(lds)[z]);
+}
+
 // Decode shape (m = MR <= 8).  One launch covers any number of linears that
 // share (dtype, m); workgroup -> item through `wg_item` (GROUPED), or the
-// single item `one`.  The activation rows are quantized into LDS with the
-// arithmetic of k_quantize (so fused and separate quantization agree bit for
-// bit), `ch_oct` octets of blocks at a time.  Each wavefront owns two row
+// single item `one`.  The activation rows go to LDS as records (gemv_fill,
+// or copies of k_gemv_records' output), at most `cap_oct` octets of blocks
+// at a time.  Each wavefront owns two row
 // groups (64 weight rows) and, per block, forms the exact integer sums of
-// all its rows against all activation rows with one
-// v_mfma_i32_32x32x32_i8 per row group: A = the activation block (rows
-// >= MR zero), B = the weight block unpacked to int8 in registers (the
-// centered formats' offset enters as the seed -c*sum(q_a)).  Lane (r, h) then holds the sums of weight row r against
-// activation rows 4h..4h+3 and folds them into f32 accumulators exactly as
-// a scalar loop would: acc += (d_a*d_b) * S, accm += m_b * (d_a*sum(q_a)).
+// all its rows against all activation rows with one v_mfma_i32_32x32x32_i8
+// per row group: A = the activation block (rows >= MR zero), B = the weight
+// block unpacked to int8 in registers (the centered formats' offset enters
+// as the seed -c*sum(q_a)).  Lane (r, h) then holds the sums of weight row r
+// against activation rows 4h..4h+3 and folds them into f32 accumulators
+// exactly as a scalar loop would: acc += (d_a*d_b) * S,
+// accm += m_b * (d_a*sum(q_a)).
 // 2^lks of the 4 wavefronts split a row's octets (the split depends on the
 // weight only); each walks its blocks in increasing order whatever the
 // chunking, and the parts meet in LDS in wavefront order: a row's result
@@ -525,7 +624,7 @@ RW_HD constexpr int gemv_rec_bytes(int mr) { return 32 * mr + 16 + 96; }
 // zeros) and zero activation records: they add exactly +0.
 template <int DT, int MR, bool GROUPED>
 __global__ __launch_bounds__(256, 4) void k_gemv(const GemvItem *__restrict__ items, const int *__restrict__ wg_item,
-                                              GemvItem one, int ch_oct) {
+                                              GemvItem one, int cap_oct) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR, SO = ZO + 16, DO = SO + 32, PO = DO + 32;
   constexpr int OFF = DT == 2 ? 8 : DT == 6 ? 16 : 0;  // centering offset
@@ -553,15 +652,9 @@ __global__ __launch_bounds__(256, 4) void k_gemv(const GemvItem *__restrict__ it
   const int a_off = r < MR ? 32 * r + 16 * h : ZO;
   const int rot = (32 - 2 * h) & 31;  // rotr by this = rotl by 2h
 
-  // zero the parts of every record slot the chunks never write
-  {
-    constexpr int NZ = 8 - MR > 0 ? 8 - MR : 1, ZW = 4 + 3 * (8 - MR);
-    for (int z = t; z < ch_oct * OCT * ZW; z += 256) {
-      const int s = z / ZW, u = z - s * ZW;
-      const int off = u < 4 ? ZO + 4 * u : SO + 32 * ((u - 4) / NZ) + 4 * (MR + (u - 4) % NZ);
-      *reinterpret_cast<uint32_t *>(lds + s * REC + off) = 0u;
-    }
-  }
+  // zero the parts of every record slot the fills never write (records
+  // copied whole need none)
+  if (!I.rec) gemv_zero_slots<MR>(lds, cap_oct * OCT, t);
 
   float acc[2][4], accm[2][4];
 #pragma unroll
@@ -572,66 +665,30 @@ __global__ __launch_bounds__(256, 4) void k_gemv(const GemvItem *__restrict__ it
       accm[j][v] = 0.0f;
     }
 
-  for (int c0 = 0; c0 < w.noct; c0 += ch_oct) {
-    const int c1 = min(w.noct, c0 + ch_oct);
-    const int bb0 = c0 * OCT, cnb = min(nb, c1 * OCT) - bb0;
-    if (c0) __syncthreads();  // every wavefront is done with the previous chunk
-    // --- activation records of blocks [bb0, bb0 + cnb) -> LDS; (block, row)
-    // pairs block-major, 4 passes of 32 per batch so their global loads are
-    // in flight together
-    const int total = MR * cnb;
-    if (I.a) {
-      for (int rb0 = 0; rb0 < total; rb0 += 128) {
-        float4 x[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int rb = rb0 + 32 * u + (t >> 3), lt = t & 7;
-          x[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-          if (rb < total) {
-            const int lb = rb / MR, i = rb - lb * MR;
-            x[u] = ldg_f4(I.a + ((size_t)i * nb + bb0 + lb) * QK + 4 * lt);
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int rb = rb0 + 32 * u + (t >> 3), lt = t & 7;
-          const BlockQuant bq = quantize_block8(x[u]);
-          if (rb < total) {
-            const int lb = rb / MR, i = rb - lb * MR;
-            uint8_t *rec = lds + lb * REC;
-            *reinterpret_cast<uint32_t *>(rec + 32 * i + mfma_pos(4 * lt)) = pack_q4(bq);
-            if (lt == 0) {
-              *reinterpret_cast<int *>(rec + SO + 4 * i) = -OFF * bq.sum;
-              *reinterpret_cast<float *>(rec + DO + 4 * i) = bq.d;
-              *reinterpret_cast<float *>(rec + PO + 4 * i) = __fmul_rn(bq.d, (float)bq.sum);
-            }
-          }
-        }
-      }
-    } else {
-      // already quantized: row group 0 of the activation layout (MFMA order)
-      for (int idx = t; idx < total * 8; idx += 256) {
-        const int rb = idx >> 3, lt = idx & 7;
-        const int lb = rb / MR, i = rb - lb * MR;
-        const size_t slot = act_slot(nb, 0, bb0 + lb, i);
-        uint8_t *rec = lds + lb * REC;
-        *reinterpret_cast<uint32_t *>(rec + 32 * i + 4 * lt) = ldg_u32(I.qa + slot * QK + 4 * lt);
-        if (lt == 0) {
-          *reinterpret_cast<int *>(rec + SO + 4 * i) = -OFF * ldg_i32(I.qsa + slot);
-          *reinterpret_cast<float *>(rec + DO + 4 * i) = ldg_f(I.qda + slot);
-          *reinterpret_cast<float *>(rec + PO + 4 * i) = ldg_f(I.qpa + slot);
-        }
+  // chunks: step cc covers octets [s_p + cc, s_p + cc + ch) of every part
+  // p (s_p its first octet), in LDS slots [p*ch, (p+1)*ch), so that every
+  // part advances through every chunk
+  const int span = (w.noct + KS - 1) >> lks;  // the longest part
+  const int ch = min(span, max(1, cap_oct >> lks));
+  for (int cc = 0; cc < span; cc += ch) {
+    if (cc) __syncthreads();  // every wavefront is done with the previous chunk
+    for (int pp = 0; pp < KS; ++pp) {
+      const int c0 = ((w.noct * pp) >> lks) + cc, c1 = min((w.noct * (pp + 1)) >> lks, c0 + ch);
+      if (c0 >= c1) continue;
+      uint8_t *base = lds + pp * ch * OCT * REC;
+      if (I.rec) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(I.rec + (size_t)c0 * OCT * REC);
+        for (int z = t; z < (c1 - c0) * OCT * (REC / 16); z += 256)
+          reinterpret_cast<uint4 *>(base)[z] = ldg_u4(src + z);
+      } else {
+        gemv_fill<DT, MR>(I, nb, c0, c1, base, t);
       }
     }
-    // records of the tail blocks of the last octet: zeros
-    const int dead = (c1 - c0) * OCT - cnb;
-    for (int z = t; z < dead * (REC / 16); z += 256)
-      reinterpret_cast<uint4 *>(lds + cnb * REC)[z] = make_uint4(0, 0, 0, 0);
     __syncthreads();
 
     // --- weights: this part's octets inside the chunk, each loaded whole
     // for both row groups (the planes are padded to whole octets)
-    const int p0 = max(o0, c0), p1 = min(o1, c1);
+    const int p0 = o0 + cc, p1 = min(o1, p0 + ch);
     for (int o = p0; o < p1; ++o) {
       v4i q[2][8];
       uint4 dd[2], mm[2], h0[2], h1[2];
@@ -657,7 +714,7 @@ __global__ __launch_bounds__(256, 4) void k_gemv(const GemvItem *__restrict__ it
           }
         }
       }
-      const uint8_t *orec = lds + (o - c0) * OCT * REC;
+      const uint8_t *orec = lds + (part * ch + o - p0) * OCT * REC;
 #pragma unroll
       for (int b8 = 0; b8 < OCT; ++b8) {
         const uint8_t *rec = orec + b8 * REC;
@@ -749,9 +806,9 @@ __global__ __launch_bounds__(256, 4) void k_gemv(const GemvItem *__restrict__ it
   }
 }
 
-// LDS bytes k_gemv needs for m rows and chunks of ch_oct octets
-RW_HD inline size_t gemv_lds_bytes(int m, int ch_oct) {
-  const size_t act = (size_t)ch_oct * OCT * gemv_rec_bytes(m);
+// LDS bytes k_gemv needs for m rows and cap_oct octets of records
+RW_HD inline size_t gemv_lds_bytes(int m, int cap_oct) {
+  const size_t act = (size_t)cap_oct * OCT * gemv_rec_bytes(m);
   const size_t red = (size_t)4 * 8 * 64 * 4;
   return act > red ? act : red;
 }

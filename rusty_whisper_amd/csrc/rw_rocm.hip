@@ -350,13 +350,20 @@ static int gemv_ks(const rw_weight *w) {
 }
 static int gemv_wgs(const rw_weight *w, int ks) { return (int)cdiv(w->ngroups, 2 * (4 / ks)); }
 
-// LDS per workgroup is held to GEMV_LDS_CAP bytes: activations go through
-// LDS in chunks of this many octets (the arithmetic does not depend on it).
+// LDS per workgroup is held to GEMV_LDS_CAP bytes: activation records go
+// through LDS in chunks (the arithmetic does not depend on them).  A weight
+// split over ks wavefront sets needs ks * ceil(noct / ks) octet slots to hold
+// its whole k at once; a launch gets the most any of its weights needs, up
+// to the cap.
 constexpr size_t GEMV_LDS_CAP = 32768;
-static int gemv_chunk(int m, int noct_max) {
+static int gemv_need(const rw_weight *w) {
+  const int ks = gemv_ks(w);
+  return ks * (int)cdiv(w->noct, ks);
+}
+static int gemv_cap(int m, int need) {
   int cap = (int)(GEMV_LDS_CAP / ((size_t)OCT * gemv_rec_bytes(m)));
-  if (cap < 1) cap = 1;
-  return noct_max < cap ? noct_max : cap;
+  if (cap < 4) cap = 4;
+  return need < cap ? need : cap;
 }
 
 static GemvItem gemv_item(const rw_weight *w, const float *a, const float *bias, float *out) {
@@ -372,30 +379,30 @@ static GemvItem gemv_item(const rw_weight *w, const float *a, const float *bias,
 }
 
 template <int DT, int MR>
-static void launch_gemv_mr(const GemvItem *items, const int *wg_item, const GemvItem &one, int wgs, int ch_oct,
+static void launch_gemv_mr(const GemvItem *items, const int *wg_item, const GemvItem &one, int wgs, int cap_oct,
                            hipStream_t s) {
   if (items)
-    hipLaunchKernelGGL((k_gemv<DT, MR, true>), dim3((unsigned)wgs), dim3(256), gemv_lds_bytes(MR, ch_oct), s,
-                       items, wg_item, one, ch_oct);
+    hipLaunchKernelGGL((k_gemv<DT, MR, true>), dim3((unsigned)wgs), dim3(256), gemv_lds_bytes(MR, cap_oct), s,
+                       items, wg_item, one, cap_oct);
   else
-    hipLaunchKernelGGL((k_gemv<DT, MR, false>), dim3((unsigned)wgs), dim3(256), gemv_lds_bytes(MR, ch_oct), s,
-                       items, wg_item, one, ch_oct);
+    hipLaunchKernelGGL((k_gemv<DT, MR, false>), dim3((unsigned)wgs), dim3(256), gemv_lds_bytes(MR, cap_oct), s,
+                       items, wg_item, one, cap_oct);
 }
 
 // one k_gemv launch: `items` (device) + `wg_item` (device) for a group, or
 // items == NULL and the single item `one`
 template <int DT>
 static void launch_gemv_dt(int m, const GemvItem *items, const int *wg_item, const GemvItem &one, int wgs,
-                           int ch_oct, hipStream_t s) {
+                           int cap_oct, hipStream_t s) {
   switch (m) {
-    case 1: launch_gemv_mr<DT, 1>(items, wg_item, one, wgs, ch_oct, s); break;
-    case 2: launch_gemv_mr<DT, 2>(items, wg_item, one, wgs, ch_oct, s); break;
-    case 3: launch_gemv_mr<DT, 3>(items, wg_item, one, wgs, ch_oct, s); break;
-    case 4: launch_gemv_mr<DT, 4>(items, wg_item, one, wgs, ch_oct, s); break;
-    case 5: launch_gemv_mr<DT, 5>(items, wg_item, one, wgs, ch_oct, s); break;
-    case 6: launch_gemv_mr<DT, 6>(items, wg_item, one, wgs, ch_oct, s); break;
-    case 7: launch_gemv_mr<DT, 7>(items, wg_item, one, wgs, ch_oct, s); break;
-    default: launch_gemv_mr<DT, 8>(items, wg_item, one, wgs, ch_oct, s); break;
+    case 1: launch_gemv_mr<DT, 1>(items, wg_item, one, wgs, cap_oct, s); break;
+    case 2: launch_gemv_mr<DT, 2>(items, wg_item, one, wgs, cap_oct, s); break;
+    case 3: launch_gemv_mr<DT, 3>(items, wg_item, one, wgs, cap_oct, s); break;
+    case 4: launch_gemv_mr<DT, 4>(items, wg_item, one, wgs, cap_oct, s); break;
+    case 5: launch_gemv_mr<DT, 5>(items, wg_item, one, wgs, cap_oct, s); break;
+    case 6: launch_gemv_mr<DT, 6>(items, wg_item, one, wgs, cap_oct, s); break;
+    case 7: launch_gemv_mr<DT, 7>(items, wg_item, one, wgs, cap_oct, s); break;
+    default: launch_gemv_mr<DT, 8>(items, wg_item, one, wgs, cap_oct, s); break;
   }
 }
 
@@ -419,7 +426,7 @@ static int run_product(const rw_weight *w, size_t m, const float *bias, float *o
     one.qda = av.da;
     one.qpa = av.pa;
     one.qsa = av.sa;
-    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, gemv_wgs(w, gemv_ks(w)), gemv_chunk((int)m, w->noct), s);
+    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, gemv_wgs(w, gemv_ks(w)), gemv_cap((int)m, gemv_need(w)), s);
     LAUNCH_TRY("k_gemv");
   } else {
     return run_gemm(&w, &bias, &out, 1, av, (int)m, s);
@@ -434,7 +441,7 @@ static int run_matmul(const rw_weight *w, const float *a, size_t m, const float 
   if (m == 0) return RW_OK;
   if (m <= GEMV_MAX_M) {
     GemvItem one = gemv_item(w, a, bias, out);
-    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, gemv_wgs(w, gemv_ks(w)), gemv_chunk((int)m, w->noct), s);
+    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, gemv_wgs(w, gemv_ks(w)), gemv_cap((int)m, gemv_need(w)), s);
     LAUNCH_TRY("k_gemv");
     return RW_OK;
   }
@@ -446,17 +453,23 @@ static int run_matmul(const rw_weight *w, const float *a, size_t m, const float 
 
 // ------------------------------------------------- grouped decode GEMV
 
-// A grouped call becomes one k_gemv launch per distinct (dtype, m);
-// the item table and the workgroup -> item map go to the device in one copy.
+// A grouped call becomes, per distinct (dtype, m), one k_gemv_records launch
+// (each linear's activation quantized once, into records) and one k_gemv
+// launch.  The device buffer holds the item table, the workgroup -> item maps
+// of both launches (these go to the device in one copy) and the records.
 struct GroupLaunch {
-  int dt, m, wgs, ch_oct, wg_first;
+  int dt, m, wgs, cap_oct, wg_first, qwgs, qwg_first;
 };
 
 struct GroupPlan {
-  std::vector<size_t> order;               // non-empty items, in launch order
-  std::vector<int> wg0, wgs, wg_first;     // per ordered item
+  std::vector<size_t> order;                           // non-empty items, in launch order
+  std::vector<int> wg0, wgs, wg_first, qwg0, qwgs, qwg_first;  // per ordered item
+  std::vector<size_t> rec_off;                         // per ordered item, from rec_base
   std::vector<GroupLaunch> launches;
-  size_t map_off = 0, bytes = 0;
+  size_t map_off = 0, qmap_off = 0;
+  size_t bytes = 0;     // item table + maps (copied from the host)
+  size_t rec_base = 0;  // records start
+  size_t total = 0;     // bytes of device memory the group needs
 };
 
 static GroupPlan group_plan(const rw_linear *items, size_t count) {
@@ -468,25 +481,37 @@ static GroupPlan group_plan(const rw_linear *items, size_t count) {
   for (size_t i = 0; i < count; ++i)
     if (items[i].w && items[i].m > 0 && items[i].m <= GEMV_MAX_M) P.order.push_back(i);
   std::stable_sort(P.order.begin(), P.order.end(), [&](size_t x, size_t y) { return key(x) < key(y); });
-  int total = 0;
+  int total = 0, qtotal = 0;
+  size_t rec = 0;
   for (size_t j = 0; j < P.order.size(); ++j) {
     const rw_weight *w = items[P.order[j]].w;
+    const int m = (int)items[P.order[j]].m;
     const int ks = gemv_ks(w);
     if (j == 0 || key(P.order[j]) != key(P.order[j - 1])) {
-      P.launches.push_back(GroupLaunch{w->dtype, (int)items[P.order[j]].m, 0, 0, total});
+      P.launches.push_back(GroupLaunch{w->dtype, m, 0, 0, total, 0, qtotal});
     }
     GroupLaunch &L = P.launches.back();
-    const int n = gemv_wgs(w, ks);
+    const int n = gemv_wgs(w, ks), nq = (int)cdiv(w->noct, 2);
     P.wg0.push_back(L.wgs);
     P.wgs.push_back(n);
     P.wg_first.push_back(total);
+    P.qwg0.push_back(L.qwgs);
+    P.qwgs.push_back(nq);
+    P.qwg_first.push_back(qtotal);
+    P.rec_off.push_back(rec);
     L.wgs += n;
-    L.ch_oct = std::max(L.ch_oct, w->noct);
+    L.qwgs += nq;
+    L.cap_oct = std::max(L.cap_oct, gemv_need(w));
     total += n;
+    qtotal += nq;
+    rec += align_up((size_t)w->noct * OCT * gemv_rec_bytes(m), 256);
   }
-  for (GroupLaunch &L : P.launches) L.ch_oct = gemv_chunk(L.m, L.ch_oct);
+  for (GroupLaunch &L : P.launches) L.cap_oct = gemv_cap(L.m, L.cap_oct);
   P.map_off = align_up(P.order.size() * sizeof(GemvItem), 256);
-  P.bytes = P.order.empty() ? 0 : align_up(P.map_off + (size_t)total * sizeof(int), 256);
+  P.qmap_off = P.map_off + (size_t)total * sizeof(int);
+  P.bytes = P.order.empty() ? 0 : align_up(P.qmap_off + (size_t)qtotal * sizeof(int), 256);
+  P.rec_base = P.bytes;
+  P.total = P.order.empty() ? 0 : P.rec_base + rec;
   return P;
 }
 
@@ -495,7 +520,7 @@ struct rw_group {
   int device;
   std::vector<GroupLaunch> launches;
   void *table;
-  size_t map_off, bytes;
+  size_t map_off, qmap_off, bytes;
 };
 
 // pinned staging for launch tables, one per (device, stream); `ev` marks the
@@ -522,30 +547,62 @@ static int check_group_items(const rw_linear *items, size_t count) {
   return RW_OK;
 }
 
-// item table, then the workgroup -> item map, as the plan lays them out
-static void fill_tables(const GroupPlan &P, const rw_linear *items, void *host) {
+// item table, then the two workgroup -> item maps, as the plan lays them out;
+// `dev` is the device address the tables will have (the records follow them)
+static void fill_tables(const GroupPlan &P, const rw_linear *items, void *host, void *dev) {
   GemvItem *tab = (GemvItem *)host;
   int *map = (int *)((char *)host + P.map_off);
+  int *qmap = (int *)((char *)host + P.qmap_off);
   for (size_t j = 0; j < P.order.size(); ++j) {
     const rw_linear &it = items[P.order[j]];
     tab[j] = gemv_item(it.w, it.a, it.bias, it.out);
     tab[j].wg0 = P.wg0[j];
+    tab[j].qwg0 = P.qwg0[j];
+    tab[j].rec = (uint8_t *)dev + P.rec_base + P.rec_off[j];
     for (int q = 0; q < P.wgs[j]; ++q) map[P.wg_first[j] + q] = (int)j;
+    for (int q = 0; q < P.qwgs[j]; ++q) qmap[P.qwg_first[j] + q] = (int)j;
   }
 }
 
+template <int DT>
+static void launch_records_dt(int m, const GemvItem *items, const int *qmap, int qwgs, hipStream_t s) {
+#define RW_REC(MR)                                                                                          \
+  hipLaunchKernelGGL((k_gemv_records<DT, MR>), dim3((unsigned)qwgs), dim3(256),                               \
+                     (size_t)2 * OCT * gemv_rec_bytes(MR), s, items, qmap)
+  switch (m) {
+    case 1: RW_REC(1); break;
+    case 2: RW_REC(2); break;
+    case 3: RW_REC(3); break;
+    case 4: RW_REC(4); break;
+    case 5: RW_REC(5); break;
+    case 6: RW_REC(6); break;
+    case 7: RW_REC(7); break;
+    default: RW_REC(8); break;
+  }
+#undef RW_REC
+}
+
 static int launch_group(const std::vector<GroupLaunch> &launches, const void *table, size_t map_off,
-                        hipStream_t s) {
+                        size_t qmap_off, hipStream_t s) {
   const GemvItem *dtab = (const GemvItem *)table;
   const int *dmap = (const int *)((const char *)table + map_off);
+  const int *qmap = (const int *)((const char *)table + qmap_off);
   const GemvItem none{};
   for (const GroupLaunch &L : launches) {
     switch (L.dt) {
-      case RW_Q4_0: launch_gemv_dt<RW_Q4_0>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.ch_oct, s); break;
-      case RW_Q4_1: launch_gemv_dt<RW_Q4_1>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.ch_oct, s); break;
-      case RW_Q5_0: launch_gemv_dt<RW_Q5_0>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.ch_oct, s); break;
-      case RW_Q5_1: launch_gemv_dt<RW_Q5_1>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.ch_oct, s); break;
-      default: launch_gemv_dt<RW_Q8_0>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.ch_oct, s); break;
+      case RW_Q4_0: launch_records_dt<RW_Q4_0>(L.m, dtab, qmap + L.qwg_first, L.qwgs, s); break;
+      case RW_Q4_1: launch_records_dt<RW_Q4_1>(L.m, dtab, qmap + L.qwg_first, L.qwgs, s); break;
+      case RW_Q5_0: launch_records_dt<RW_Q5_0>(L.m, dtab, qmap + L.qwg_first, L.qwgs, s); break;
+      case RW_Q5_1: launch_records_dt<RW_Q5_1>(L.m, dtab, qmap + L.qwg_first, L.qwgs, s); break;
+      default: launch_records_dt<RW_Q8_0>(L.m, dtab, qmap + L.qwg_first, L.qwgs, s); break;
+    }
+    LAUNCH_TRY("k_gemv_records (grouped)");
+    switch (L.dt) {
+      case RW_Q4_0: launch_gemv_dt<RW_Q4_0>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.cap_oct, s); break;
+      case RW_Q4_1: launch_gemv_dt<RW_Q4_1>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.cap_oct, s); break;
+      case RW_Q5_0: launch_gemv_dt<RW_Q5_0>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.cap_oct, s); break;
+      case RW_Q5_1: launch_gemv_dt<RW_Q5_1>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.cap_oct, s); break;
+      default: launch_gemv_dt<RW_Q8_0>(L.m, dtab, dmap + L.wg_first, none, L.wgs, L.cap_oct, s); break;
     }
     LAUNCH_TRY("k_gemv (grouped)");
   }
@@ -810,7 +867,7 @@ int rw_rocm_matmul_t_q(const rw_weight *w, const float *a, size_t m, size_t k, c
 
 size_t rw_rocm_grouped_workspace_size(const rw_linear *items, size_t count) {
   if (!items) return 0;
-  return group_plan(items, count).bytes;
+  return group_plan(items, count).total;
 }
 
 int rw_rocm_matmul_grouped_dev(const rw_linear *items, size_t count, void *workspace, size_t workspace_len,
@@ -825,9 +882,9 @@ int rw_rocm_matmul_grouped_dev(const rw_linear *items, size_t count, void *works
   HIP_TRY(hipSetDevice(device));
   void *ws = workspace;
   if (ws) {
-    if (workspace_len < P.bytes) return fail(RW_EINVAL, "workspace of %zu bytes < %zu needed", workspace_len, P.bytes);
+    if (workspace_len < P.total) return fail(RW_EINVAL, "workspace of %zu bytes < %zu needed", workspace_len, P.total);
   } else {
-    int rc = stream_workspace(device, stream, P.bytes, &ws);
+    int rc = stream_workspace(device, stream, P.total, &ws);
     if (rc) return rc;
   }
   hipStream_t s = (hipStream_t)stream;
@@ -853,12 +910,12 @@ int rw_rocm_matmul_grouped_dev(const rw_linear *items, size_t count, void *works
       }
       st.cap = want;
     }
-    fill_tables(P, items, st.host);
+    fill_tables(P, items, st.host, ws);
     HIP_TRY(hipMemcpyAsync(ws, st.host, P.bytes, hipMemcpyHostToDevice, s));
     HIP_TRY(hipEventRecord(st.ev, s));
     st.pending = true;
   }
-  return launch_group(P.launches, ws, P.map_off, s);
+  return launch_group(P.launches, ws, P.map_off, P.qmap_off, s);
 }
 
 int rw_rocm_group_create(const rw_linear *items, size_t count, rw_group **out) {
@@ -871,18 +928,19 @@ int rw_rocm_group_create(const rw_linear *items, size_t count, rw_group **out) {
   if (P.order.empty()) return fail(RW_EINVAL, "every item has m = 0");
   const int device = items[0].w->device;
   HIP_TRY(hipSetDevice(device));
-  std::vector<char> host(P.bytes);
-  fill_tables(P, items, host.data());
   rw_group *g = new rw_group;
   g->device = device;
   g->launches = P.launches;
   g->map_off = P.map_off;
-  g->bytes = P.bytes;
-  if (hipMalloc(&g->table, P.bytes) != hipSuccess) {
+  g->qmap_off = P.qmap_off;
+  g->bytes = P.total;
+  if (hipMalloc(&g->table, P.total) != hipSuccess) {
     (void)hipGetLastError();
     delete g;
-    return fail(RW_ENOMEM, "hipMalloc(%zu) for a launch table failed", P.bytes);
+    return fail(RW_ENOMEM, "hipMalloc(%zu) for a launch table failed", P.total);
   }
+  std::vector<char> host(P.bytes);
+  fill_tables(P, items, host.data(), g->table);
   hipError_t e = hipMemcpy(g->table, host.data(), P.bytes, hipMemcpyHostToDevice);
   if (e != hipSuccess) {
     (void)hipFree(g->table);
@@ -896,7 +954,7 @@ int rw_rocm_group_create(const rw_linear *items, size_t count, rw_group **out) {
 int rw_rocm_group_run(const rw_group *g, void *stream) {
   if (!g) return fail(RW_EINVAL, "group is NULL");
   HIP_TRY(hipSetDevice(g->device));
-  return launch_group(g->launches, g->table, g->map_off, (hipStream_t)stream);
+  return launch_group(g->launches, g->table, g->map_off, g->qmap_off, (hipStream_t)stream);
 }
 
 void rw_rocm_group_free(rw_group *g) {
