@@ -154,12 +154,15 @@ typedef struct rw_linear {
 } rw_linear;
 
 /* Run `count` independent linears, each with m <= 8 (the decode-GEMV
- * regime), in one launch per distinct (dtype, m); entries with m == 0 are
- * skipped.  Device pointers, asynchronous on `stream`.  Each
- * result is bitwise identical to the same linear run alone through
+ * regime), in two launches per distinct (dtype, m): every linear's
+ * activation is quantized once, then all products run; entries with m == 0
+ * are skipped.  Device pointers, asynchronous on `stream`.  Each result is
+ * bitwise identical to the same linear run alone through
  * rw_rocm_matmul_t_q_dev.  The launch tables go to `workspace` (>=
  * rw_rocm_grouped_workspace_size bytes; NULL = a buffer of the library's own
- * for this stream) through pinned host memory on `stream`.  Replaces a
+ * for this stream) through pinned host memory on `stream`, and the quantized
+ * activations are kept there; calls that overlap on one workspace race.
+ * Replaces a
  * sequence of independent linear_w calls (src/quant.rs:1054-1063): the
  * Q/K/V projections of src/decoder.rs:148-158 share x, the cross K/V of
  * every layer at src/decoder.rs:44-53 are independent. */
@@ -171,8 +174,10 @@ size_t rw_rocm_grouped_workspace_size(const rw_linear *items, size_t count);
 
 /* A prepared group: the same launches as rw_rocm_matmul_grouped_dev over
  * the same items (so bitwise the same results), with the launch tables
- * uploaded once by rw_rocm_group_create.  rw_rocm_group_run then only
- * launches, queued on `stream`: no copy, no allocation, no host wait.  For
+ * uploaded once by rw_rocm_group_create, which also allocates the group's
+ * buffer for quantized activations.  rw_rocm_group_run then only launches,
+ * queued on `stream`: no copy, no allocation, no host wait; runs of one group
+ * that overlap (two streams) race on that buffer.  For
  * decode loops whose activation and output buffers stay put from token to
  * token (src/decoder.rs:148-196 runs the same linears every step); the
  * pointers in `items` are captured at creation.  Has no reference

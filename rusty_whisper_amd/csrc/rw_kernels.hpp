@@ -60,6 +60,7 @@ __device__ inline float ldg_f(const void *p) { return *(const float RW_GLOBAL_AS
 __device__ inline uint32_t ldg_u32(const void *p) { return *(const uint32_t RW_GLOBAL_AS *)p; }
 __device__ inline int32_t ldg_i32(const void *p) { return *(const int32_t RW_GLOBAL_AS *)p; }
 __device__ inline void stg_f(float *p, float v) { *(float RW_GLOBAL_AS *)(void *)p = v; }
+__device__ inline void stg_u32(void *p, uint32_t v) { *(uint32_t RW_GLOBAL_AS *)p = v; }
 __device__ inline void stg_u4(void *p, uint4 v) {
   *(rw_u32x4 RW_GLOBAL_AS *)p = rw_u32x4{v.x, v.y, v.z, v.w};
 }
@@ -75,6 +76,16 @@ __device__ inline uint4 ldb_u4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t
 }
 __device__ inline uint2 ldb_u2(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+  return make_uint2(v[0], v[1]);
+}
+// Streaming (read-once) loads: the nt cache policy, so data touched once
+// does not displace what the caches should keep
+__device__ inline uint4 ldb_u4_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 2);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ inline uint2 ldb_u2_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 2);
   return make_uint2(v[0], v[1]);
 }
 __device__ inline uint32_t ldb_u32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
@@ -103,13 +114,17 @@ __device__ inline float h2f_exact(uint32_t h) {
 // hardware conversion: identical to h2f_exact for every non-NaN code
 __device__ inline float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
 
-// Rust `(x).round().clamp(-127.0, 127.0) as i32` (NaN -> 0)
+// Rust `(x).round().clamp(-127.0, 127.0) as i32` (NaN -> 0).  In f32
+// round-to-nearest arithmetic, x + copysign(0.49999997, x) truncated toward
+// zero is round-half-away-from-zero(x) for every f32 x (checked over all
+// 2^32 inputs; 0.49999997 rather than 0.5 keeps x = 0.49999997 from
+// rounding up to 1).  v_cvt_i32_f32 truncates, saturates +-inf and maps NaN
+// to 0; v_med3_i32 clamps.
 __device__ inline int round_clamp_i8(float v) {
-  float r = roundf(v);
-  if (r != r) return 0;
-  r = r < -127.0f ? -127.0f : r;
-  r = r > 127.0f ? 127.0f : r;
-  return (int)r;
+  const float y = __fadd_rn(v, __builtin_copysignf(0.49999997f, v));
+  int r;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(y));
+  return min(127, max(-127, r));
 }
 
 // bytes of a packed-nibble word minus `c` (0 <= byte < 128, c <= byte+128)
@@ -495,9 +510,8 @@ struct GemvItem {
   uint8_t *rec;  // activation records [noct*8][gemv_rec_bytes(m)] written by
                  // k_gemv_records (grouped launches), or NULL
   int n;
-  int wg0;   // first workgroup of this item in the launch
-  int qwg0;  // first workgroup of this item in its k_gemv_records launch
   int lks;   // log2 of the number of wavefronts that split a row's octets
+  int pad;
 };
 
 // LDS record of one activation block for the decode kernel (m = MR rows):
@@ -583,31 +597,189 @@ __device__ inline void gemv_fill(const GemvItem &I, int nb, int c0, int c1, uint
     reinterpret_cast<uint4 *>(base + cnb * REC)[z] = make_uint4(0, 0, 0, 0);
 }
 
+// quantize_acts_i8 for one 32-element block held by one lane: the values
+// of quantize_block8 (max and sum are exact in any order): quants as 8
+// natural dwords, sum(q) and d.
+__device__ inline void quantize_block_lane(const float4 (&x)[8], uint32_t (&qd)[8], int &sum, float &d) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(x[u].x), fabsf(x[u].y)), fmaxf(fabsf(x[u].z), fabsf(x[u].w))));
+  d = __fdiv_rn(amax, 127.0f);
+  const float inv = d > 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+  sum = 0;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int q0 = round_clamp_i8(__fmul_rn(x[u].x, inv)), q1 = round_clamp_i8(__fmul_rn(x[u].y, inv));
+    const int q2 = round_clamp_i8(__fmul_rn(x[u].z, inv)), q3 = round_clamp_i8(__fmul_rn(x[u].w, inv));
+    sum += q0 + q1 + q2 + q3;
+    qd[u] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+            ((uint32_t)(q3 & 0xff) << 24);
+  }
+}
+
 // Activation records of a grouped decode launch, quantized once per linear
-// instead of once per k_gemv workgroup: workgroup -> (item, pair of octets)
-// through `qwg_item`; the records (zero parts included) are built in LDS
-// by gemv_fill, exactly as k_gemv builds them, and copied to the item's
-// record buffer.
+// instead of once per k_gemv workgroup.  One lane per (row i, block bl) of
+// an item, rows fastest; workgroup -> (item, part of 256 lanes) through
+// `qwg_item` (item -1 = unused slot).  Each lane
+// writes its row's quants (MFMA order) and SEED / DA / PA entries; the
+// row-0 lane of a block also writes the block's zero parts.  Blocks past nb
+// (the padding of the last octet) get zero records.  The values are those
+// gemv_fill computes, bit for bit.
 template <int DT, int MR>
 __global__ __launch_bounds__(256) void k_gemv_records(const GemvItem *__restrict__ items,
-                                                      const int *__restrict__ qwg_item) {
-  extern __shared__ __align__(16) uint8_t lds[];
-  constexpr int REC = gemv_rec_bytes(MR);
-  const GemvItem I = items[qwg_item[blockIdx.x]];
-  const int t = threadIdx.x;
-  const int c0 = 2 * ((int)blockIdx.x - I.qwg0), c1 = min(I.w.noct, c0 + 2);
-  gemv_zero_slots<MR>(lds, (c1 - c0) * OCT, t);
-  gemv_fill<DT, MR>(I, I.w.nb, c0, c1, lds, t);
-  __syncthreads();
-  uint4 *dst = reinterpret_cast<uint4 *>(I.rec + (size_t)c0 * OCT * REC);
-  for (int z = t; z < (c1 - c0) * OCT * (REC / 16); z += 256) stg_u4(dst + z, reinterpret_cast<const uint4 *>(lds)[z]);
+                                                      const int2 *__restrict__ qwg_item) {
+  constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR, SO = ZO + 16, DO = SO + 32, PO = DO + 32;
+  constexpr int OFF = DT == 2 ? 8 : DT == 6 ? 16 : 0;
+  const int2 wt = qwg_item[blockIdx.x];  // (item, part)
+  if (wt.x < 0) return;  // a slot no item uses
+  const GemvItem I = items[wt.x];
+  const int nb = I.w.nb, nbp = I.w.noct * OCT;
+  const int z = wt.y * 256 + (int)threadIdx.x;
+  if (z >= MR * nbp) return;
+  const int bl = z / MR, i = z - bl * MR;
+  float4 x[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) x[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (bl < nb) {
+    const float *src = I.a + ((size_t)i * nb + bl) * QK;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = ldg_f4(src + 4 * u);
+  }
+  uint32_t qd[8];
+  int sum;
+  float d;
+  quantize_block_lane(x, qd, sum, d);
+  uint8_t *rec = I.rec + (size_t)bl * REC;
+  // natural dword u (elements 4u..4u+3) sits at MFMA-order byte mfma_pos(4u)
+  stg_u4(rec + 32 * i, make_uint4(qd[0], qd[1], qd[4], qd[5]));
+  stg_u4(rec + 32 * i + 16, make_uint4(qd[2], qd[3], qd[6], qd[7]));
+  stg_u32(rec + SO + 4 * i, (uint32_t)(-OFF * sum));
+  stg_f(reinterpret_cast<float *>(rec + DO + 4 * i), d);
+  stg_f(reinterpret_cast<float *>(rec + PO + 4 * i), __fmul_rn(d, (float)sum));
+  if (i == 0) {
+    stg_u4(rec + ZO, make_uint4(0, 0, 0, 0));
+#pragma unroll
+    for (int r = MR; r < 8; ++r) {
+      stg_u32(rec + SO + 4 * r, 0u);
+      stg_u32(rec + DO + 4 * r, 0u);
+      stg_u32(rec + PO + 4 * r, 0u);
+    }
+  }
+}
+
+// row groups (of 32 weight rows) per k_gemv wavefront
+#ifndef GEMV_NG
+#define GEMV_NG 2
+#endif
+#ifndef GEMV_WPE
+#define GEMV_WPE 4
+#endif
+
+// One octet of a wavefront's GEMV_NG row groups, as loaded: quants (8
+// bytes, Q8_0 16, per lane and block), scales, mins and (Q5) high-bit words.
+template <int DT>
+struct GemvOct {
+  std::conditional_t<DT == 8, uint4, uint2> q[GEMV_NG][8];
+  uint4 d[GEMV_NG], m[GEMV_NG], h0[GEMV_NG], h1[GEMV_NG];
+};
+
+// (every weight byte is read once per launch: streaming loads)
+template <int DT>
+__device__ inline void gemv_load_oct(const WeightView &w, int gw, int o, __amdgpu_buffer_rsrc_t rq,
+                                     __amdgpu_buffer_rsrc_t rd, __amdgpu_buffer_rsrc_t rm,
+                                     __amdgpu_buffer_rsrc_t rh, uint32_t vq, uint32_t vs, uint32_t vh,
+                                     GemvOct<DT> &x) {
+  constexpr int QB = DT == 8 ? 32 : 16;
+#pragma unroll
+  for (int j = 0; j < GEMV_NG; ++j) {
+    const int g = min(gw + j, w.ngroups - 1);
+    const uint32_t sq = (uint32_t)(g * w.nb_pad + o * OCT) * (RG * QB);
+    const uint32_t ss = (uint32_t)(g * w.noct + o) * (RG * 16);
+    x.d[j] = ldb_u4_nt(rd, vs, ss);
+    if (has_min(DT)) x.m[j] = ldb_u4_nt(rm, vs, ss);
+    if (has_high(DT)) {
+      x.h0[j] = ldb_u4_nt(rh, vh, 2 * ss);
+      x.h1[j] = ldb_u4_nt(rh, vh + 16, 2 * ss);
+    }
+#pragma unroll
+    for (int b8 = 0; b8 < OCT; ++b8) {
+      if constexpr (DT == 8)
+        x.q[j][b8] = ldb_u4_nt(rq, vq, sq + b8 * (RG * QB));
+      else
+        x.q[j][b8] = ldb_u2_nt(rq, vq, sq + b8 * (RG * QB));
+    }
+  }
+}
+
+// Fold one octet into the accumulators: per block and row group one
+// v_mfma_i32_32x32x32_i8 (exact sums S of weight rows x activation rows),
+// then acc += (d_a*d_b) * S and accm += m_b * (d_a*sum(q_a)) for the
+// activation rows 4h..4h+3 this lane holds.  `orec` = the octet's records.
+template <int DT, int MR>
+__device__ inline void gemv_fold_oct(const uint8_t *orec, int a_off, int h, int rot, const GemvOct<DT> &x,
+                                     float (&acc)[GEMV_NG][4], float (&accm)[GEMV_NG][4]) {
+  constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR, SO = ZO + 16, DO = SO + 32, PO = DO + 32;
+  constexpr int OFF = DT == 2 ? 8 : DT == 6 ? 16 : 0;
+#pragma unroll
+  for (int b8 = 0; b8 < OCT; ++b8) {
+    const uint8_t *rec = orec + b8 * REC;
+    const v4i aop = *reinterpret_cast<const v4i *>(rec + a_off);
+    const float4 da = *reinterpret_cast<const float4 *>(rec + DO + 16 * h);
+    int4 sd = make_int4(0, 0, 0, 0);
+    if (OFF) sd = *reinterpret_cast<const int4 *>(rec + SO + 16 * h);
+    const int sdv[4] = {sd.x, sd.y, sd.z, sd.w};
+    float4 pa = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (has_min(DT)) pa = *reinterpret_cast<const float4 *>(rec + PO + 16 * h);
+#pragma unroll
+    for (int j = 0; j < GEMV_NG; ++j) {
+      v4i bop;
+      if constexpr (DT == 8) {
+        const uint4 v = x.q[j][b8];
+        bop = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+      } else {
+        // low nibbles: elements 8h..8h+7, high nibbles: 16+8h..16+8h+7
+        const uint32_t x0 = x.q[j][b8].x, x1 = x.q[j][b8].y;
+        uint32_t w0 = x0 & 0x0f0f0f0fu, w1 = x1 & 0x0f0f0f0fu;
+        uint32_t w2 = (x0 >> 4) & 0x0f0f0f0fu, w3 = (x1 >> 4) & 0x0f0f0f0fu;
+        if (has_high(DT)) {
+          const uint32_t hw[8] = {x.h0[j].x, x.h0[j].y, x.h0[j].z, x.h0[j].w,
+                                  x.h1[j].x, x.h1[j].y, x.h1[j].z, x.h1[j].w};
+          // natural dwords 2h, 2h+1, 4+2h, 5+2h of the block
+          const uint32_t xh = __builtin_amdgcn_alignbit(hw[b8], hw[b8], rot);
+          w0 |= xh & 0x10101010u;
+          w1 |= rotl(xh, 1) & 0x10101010u;
+          w2 |= rotl(xh, 4) & 0x10101010u;
+          w3 |= rotl(xh, 5) & 0x10101010u;
+        }
+        bop = v4i{(int)w0, (int)w1, (int)w2, (int)w3};
+      }
+      const v16i s = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, v16i{}, 0, 0, 0);
+      const uint32_t dw = (b8 >> 1) == 0 ? x.d[j].x : (b8 >> 1) == 1 ? x.d[j].y : (b8 >> 1) == 2 ? x.d[j].z : x.d[j].w;
+      const float db = h2f((uint16_t)(dw >> (16 * (b8 & 1))));
+      const float dav[4] = {da.x, da.y, da.z, da.w};
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[j][v] = __builtin_fmaf(dav[v] * db, (float)(s[v] + sdv[v]), acc[j][v]);
+      if (has_min(DT)) {
+        const uint32_t mw = (b8 >> 1) == 0 ? x.m[j].x : (b8 >> 1) == 1 ? x.m[j].y : (b8 >> 1) == 2 ? x.m[j].z : x.m[j].w;
+        const float mb = h2f((uint16_t)(mw >> (16 * (b8 & 1))));
+        const float pav[4] = {pa.x, pa.y, pa.z, pa.w};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) accm[j][v] = __builtin_fmaf(mb, pav[v], accm[j][v]);
+      }
+    }
+  }
 }
 
 // Decode shape (m = MR <= 8).  One launch covers any number of linears that
-// share (dtype, m); workgroup -> item through `wg_item` (GROUPED), or the
-// single item `one`.  The activation rows go to LDS as records (gemv_fill,
-// or copies of k_gemv_records' output), at most `cap_oct` octets of blocks
-// at a time.  Each wavefront owns two row
+// share (dtype, m); workgroup -> (item, tile) through `wg_item` (GROUPED; item
+// -1 = unused slot), or the
+// single item `one`: workgroup -> (item, tile of rows).  The host places a
+// grouped launch's tiles so that runs of an item's tiles share an XCD, for
+// its records to be read through one L2.  The activation rows go to LDS as
+// records, copied from
+// k_gemv_records' output (GROUPED) or built by gemv_fill, at most `cap_oct`
+// octets of blocks at a time.  Each wavefront owns two row
 // groups (64 weight rows) and, per block, forms the exact integer sums of
 // all its rows against all activation rows with one v_mfma_i32_32x32x32_i8
 // per row group: A = the activation block (rows >= MR zero), B = the weight
@@ -623,21 +795,23 @@ __global__ __launch_bounds__(256) void k_gemv_records(const GemvItem *__restrict
 // last octet meet zero weight planes (the upload writes the padding as
 // zeros) and zero activation records: they add exactly +0.
 template <int DT, int MR, bool GROUPED>
-__global__ __launch_bounds__(256, 4) void k_gemv(const GemvItem *__restrict__ items, const int *__restrict__ wg_item,
+__global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restrict__ items, const int2 *__restrict__ wg_item,
                                               GemvItem one, int cap_oct) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR, SO = ZO + 16, DO = SO + 32, PO = DO + 32;
   constexpr int OFF = DT == 2 ? 8 : DT == 6 ? 16 : 0;  // centering offset
   constexpr int QB = DT == 8 ? 32 : 16;                // qs bytes per row-block
   // the descriptor is wave-uniform: scalar loads from the table or kernarg
-  const GemvItem I = GROUPED ? items[wg_item[blockIdx.x]] : one;
+  const int2 wt = GROUPED ? wg_item[blockIdx.x] : make_int2(0, (int)blockIdx.x);  // (item, tile)
+  if (wt.x < 0) return;  // a slot no item uses (the whole workgroup)
+  const GemvItem I = GROUPED ? items[wt.x] : one;
   const WeightView &w = I.w;
   const int nb = w.nb;
   const int lks = I.lks, KS = 1 << lks;
   const int t = threadIdx.x, l = t & 63, h = l >> 5, r = l & 31;
   const int wv = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: scalar offsets, uniform loops
   const int set = wv >> lks, part = wv & (KS - 1);
-  const int gw = (((int)blockIdx.x - (GROUPED ? I.wg0 : 0)) * (4 >> lks) + set) * 2;  // first of 2 row groups
+  const int gw = (wt.y * (4 >> lks) + set) * GEMV_NG;  // first row group
   const int o0 = (w.noct * part) >> lks, o1 = (w.noct * (part + 1)) >> lks;
 
   // plane buffers (the upload keeps every plane below 4 GiB) and this lane's
@@ -654,11 +828,11 @@ __global__ __launch_bounds__(256, 4) void k_gemv(const GemvItem *__restrict__ it
 
   // zero the parts of every record slot the fills never write (records
   // copied whole need none)
-  if (!I.rec) gemv_zero_slots<MR>(lds, cap_oct * OCT, t);
+  if (!GROUPED) gemv_zero_slots<MR>(lds, cap_oct * OCT, t);
 
-  float acc[2][4], accm[2][4];
+  float acc[GEMV_NG][4], accm[GEMV_NG][4];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < GEMV_NG; ++j)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       acc[j][v] = 0.0f;
@@ -671,12 +845,17 @@ __global__ __launch_bounds__(256, 4) void k_gemv(const GemvItem *__restrict__ it
   const int span = (w.noct + KS - 1) >> lks;  // the longest part
   const int ch = min(span, max(1, cap_oct >> lks));
   for (int cc = 0; cc < span; cc += ch) {
+    // this part's octets in the chunk; the first one's weights are requested
+    // before the records, so the two memory latencies overlap
+    const int p0 = o0 + cc, p1 = min(o1, p0 + ch);
+    GemvOct<DT> cur;
+    if (GROUPED && p0 < p1) gemv_load_oct<DT>(w, gw, p0, rq, rd, rm, rh, vq, vs, vh, cur);
     if (cc) __syncthreads();  // every wavefront is done with the previous chunk
     for (int pp = 0; pp < KS; ++pp) {
       const int c0 = ((w.noct * pp) >> lks) + cc, c1 = min((w.noct * (pp + 1)) >> lks, c0 + ch);
       if (c0 >= c1) continue;
       uint8_t *base = lds + pp * ch * OCT * REC;
-      if (I.rec) {
+      if constexpr (GROUPED) {
         const uint4 *src = reinterpret_cast<const uint4 *>(I.rec + (size_t)c0 * OCT * REC);
         for (int z = t; z < (c1 - c0) * OCT * (REC / 16); z += 256)
           reinterpret_cast<uint4 *>(base)[z] = ldg_u4(src + z);
@@ -686,94 +865,28 @@ __global__ __launch_bounds__(256, 4) void k_gemv(const GemvItem *__restrict__ it
     }
     __syncthreads();
 
-    // --- weights: this part's octets inside the chunk, each loaded whole
-    // for both row groups (the planes are padded to whole octets)
-    const int p0 = o0 + cc, p1 = min(o1, p0 + ch);
-    for (int o = p0; o < p1; ++o) {
-      v4i q[2][8];
-      uint4 dd[2], mm[2], h0[2], h1[2];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int g = min(gw + j, w.ngroups - 1);
-        const uint32_t sq = (uint32_t)(g * w.nb_pad + o * OCT) * (RG * QB);
-        const uint32_t ss = (uint32_t)(g * w.noct + o) * (RG * 16);
-        dd[j] = ldb_u4(rd, vs, ss);
-        if (has_min(DT)) mm[j] = ldb_u4(rm, vs, ss);
-        if (has_high(DT)) {
-          h0[j] = ldb_u4(rh, vh, 2 * ss);
-          h1[j] = ldb_u4(rh, vh + 16, 2 * ss);
-        }
-#pragma unroll
-        for (int b8 = 0; b8 < OCT; ++b8) {
-          if (DT == 8) {
-            const uint4 x = ldb_u4(rq, vq, sq + b8 * (RG * QB));
-            q[j][b8] = v4i{(int)x.x, (int)x.y, (int)x.z, (int)x.w};
-          } else {
-            const uint2 x = ldb_u2(rq, vq, sq + b8 * (RG * QB));
-            q[j][b8] = v4i{(int)x.x, (int)x.y, 0, 0};
-          }
-        }
-      }
-      const uint8_t *orec = lds + (part * ch + o - p0) * OCT * REC;
-#pragma unroll
-      for (int b8 = 0; b8 < OCT; ++b8) {
-        const uint8_t *rec = orec + b8 * REC;
-        const v4i aop = *reinterpret_cast<const v4i *>(rec + a_off);
-        const float4 da = *reinterpret_cast<const float4 *>(rec + DO + 16 * h);
-        int4 sd = make_int4(0, 0, 0, 0);
-        if (OFF) sd = *reinterpret_cast<const int4 *>(rec + SO + 16 * h);
-        const int sdv[4] = {sd.x, sd.y, sd.z, sd.w};
-        float4 pa = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (has_min(DT)) pa = *reinterpret_cast<const float4 *>(rec + PO + 16 * h);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          v4i bop;
-          if (DT == 8) {
-            bop = q[j][b8];
-          } else {
-            // low nibbles: elements 8h..8h+7, high nibbles: 16+8h..16+8h+7
-            const uint32_t x0 = (uint32_t)q[j][b8].x, x1 = (uint32_t)q[j][b8].y;
-            uint32_t w0 = x0 & 0x0f0f0f0fu, w1 = x1 & 0x0f0f0f0fu;
-            uint32_t w2 = (x0 >> 4) & 0x0f0f0f0fu, w3 = (x1 >> 4) & 0x0f0f0f0fu;
-            if (has_high(DT)) {
-              const uint32_t hw[8] = {h0[j].x, h0[j].y, h0[j].z, h0[j].w, h1[j].x, h1[j].y, h1[j].z, h1[j].w};
-              // natural dwords 2h, 2h+1, 4+2h, 5+2h of the block
-              const uint32_t xh = __builtin_amdgcn_alignbit(hw[b8], hw[b8], rot);
-              w0 |= xh & 0x10101010u;
-              w1 |= rotl(xh, 1) & 0x10101010u;
-              w2 |= rotl(xh, 4) & 0x10101010u;
-              w3 |= rotl(xh, 5) & 0x10101010u;
-            }
-            bop = v4i{(int)w0, (int)w1, (int)w2, (int)w3};
-          }
-          const v16i s = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, v16i{}, 0, 0, 0);
-          const uint32_t dw = (b8 >> 1) == 0 ? dd[j].x : (b8 >> 1) == 1 ? dd[j].y : (b8 >> 1) == 2 ? dd[j].z : dd[j].w;
-          const float db = h2f((uint16_t)(dw >> (16 * (b8 & 1))));
-          const float dav[4] = {da.x, da.y, da.z, da.w};
-#pragma unroll
-          for (int v = 0; v < 4; ++v) acc[j][v] = __builtin_fmaf(dav[v] * db, (float)(s[v] + sdv[v]), acc[j][v]);
-          if (has_min(DT)) {
-            const uint32_t mw = (b8 >> 1) == 0 ? mm[j].x : (b8 >> 1) == 1 ? mm[j].y : (b8 >> 1) == 2 ? mm[j].z : mm[j].w;
-            const float mb = h2f((uint16_t)(mw >> (16 * (b8 & 1))));
-            const float pav[4] = {pa.x, pa.y, pa.z, pa.w};
-#pragma unroll
-            for (int v = 0; v < 4; ++v) accm[j][v] = __builtin_fmaf(mb, pav[v], accm[j][v]);
-          }
-        }
+    // --- weights: each octet loaded whole for all row groups (the planes
+    // are padded to whole octets), then folded in
+    if (p0 < p1) {
+      if (!GROUPED) gemv_load_oct<DT>(w, gw, p0, rq, rd, rm, rh, vq, vs, vh, cur);
+      gemv_fold_oct<DT, MR>(lds + part * ch * OCT * REC, a_off, h, rot, cur, acc, accm);
+      for (int o = p0 + 1; o < p1; ++o) {
+        gemv_load_oct<DT>(w, gw, o, rq, rd, rm, rh, vq, vs, vh, cur);
+        gemv_fold_oct<DT, MR>(lds + (part * ch + o - p0) * OCT * REC, a_off, h, rot, cur, acc, accm);
       }
     }
   }
 
-  float y[2][4];
+  float y[GEMV_NG][4];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < GEMV_NG; ++j)
 #pragma unroll
     for (int v = 0; v < 4; ++v) y[j][v] = has_min(DT) ? acc[j][v] + accm[j][v] : acc[j][v];
 
   const int n = I.n;
   if (KS == 1) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < GEMV_NG; ++j) {
       const int g = gw + j, col = g * RG + r;
       if (g < w.ngroups && col < n)
 #pragma unroll
@@ -784,22 +897,22 @@ __global__ __launch_bounds__(256, 4) void k_gemv(const GemvItem *__restrict__ it
     return;
   }
   __syncthreads();  // the activation LDS is reused for the partial sums
-  float *red = reinterpret_cast<float *>(lds);  // [4 wavefronts][2 groups x 4][64]
+  float *red = reinterpret_cast<float *>(lds);  // [4 wavefronts][GEMV_NG groups x 4][64]
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < GEMV_NG; ++j)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) red[(wv * 8 + 4 * j + v) * 64 + l] = y[j][v];
+    for (int v = 0; v < 4; ++v) red[(wv * 4 * GEMV_NG + 4 * j + v) * 64 + l] = y[j][v];
   __syncthreads();
   if (part == 0) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < GEMV_NG; ++j) {
       const int g = gw + j, col = g * RG + r;
       if (g < w.ngroups && col < n)
 #pragma unroll
         for (int v = 0; v < 4; ++v)
           if (4 * h + v < MR) {
-            float tt = red[(wv * 8 + 4 * j + v) * 64 + l];
-            for (int p = 1; p < KS; ++p) tt = tt + red[((wv + p) * 8 + 4 * j + v) * 64 + l];
+            float tt = red[(wv * 4 * GEMV_NG + 4 * j + v) * 64 + l];
+            for (int p = 1; p < KS; ++p) tt = tt + red[((wv + p) * 4 * GEMV_NG + 4 * j + v) * 64 + l];
             stg_f(I.out + (size_t)(4 * h + v) * n + col, I.bias ? tt + ldg_f(I.bias + col) : tt);
           }
     }
@@ -809,7 +922,7 @@ __global__ __launch_bounds__(256, 4) void k_gemv(const GemvItem *__restrict__ it
 // LDS bytes k_gemv needs for m rows and cap_oct octets of records
 RW_HD inline size_t gemv_lds_bytes(int m, int cap_oct) {
   const size_t act = (size_t)cap_oct * OCT * gemv_rec_bytes(m);
-  const size_t red = (size_t)4 * 8 * 64 * 4;
+  const size_t red = (size_t)4 * 4 * GEMV_NG * 64 * 4;
   return act > red ? act : red;
 }
 

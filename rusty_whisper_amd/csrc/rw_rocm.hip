@@ -348,20 +348,22 @@ static int gemv_ks(const rw_weight *w) {
   while (ks < 4 && w->noct / (2 * ks) >= 4) ks *= 2;
   return ks;
 }
-static int gemv_wgs(const rw_weight *w, int ks) { return (int)cdiv(w->ngroups, 2 * (4 / ks)); }
+static int gemv_wgs(const rw_weight *w, int ks) { return (int)cdiv(w->ngroups, GEMV_NG * (4 / ks)); }
 
 // LDS per workgroup is held to GEMV_LDS_CAP bytes: activation records go
 // through LDS in chunks (the arithmetic does not depend on them).  A weight
 // split over ks wavefront sets needs ks * ceil(noct / ks) octet slots to hold
 // its whole k at once; a launch gets the most any of its weights needs, up
 // to the cap.
-constexpr size_t GEMV_LDS_CAP = 32768;
+#ifndef GEMV_LDS_CAP
+#define GEMV_LDS_CAP 32768
+#endif
 static int gemv_need(const rw_weight *w) {
   const int ks = gemv_ks(w);
   return ks * (int)cdiv(w->noct, ks);
 }
 static int gemv_cap(int m, int need) {
-  int cap = (int)(GEMV_LDS_CAP / ((size_t)OCT * gemv_rec_bytes(m)));
+  int cap = (int)((size_t)GEMV_LDS_CAP / ((size_t)OCT * gemv_rec_bytes(m)));
   if (cap < 4) cap = 4;
   return need < cap ? need : cap;
 }
@@ -379,7 +381,7 @@ static GemvItem gemv_item(const rw_weight *w, const float *a, const float *bias,
 }
 
 template <int DT, int MR>
-static void launch_gemv_mr(const GemvItem *items, const int *wg_item, const GemvItem &one, int wgs, int cap_oct,
+static void launch_gemv_mr(const GemvItem *items, const int2 *wg_item, const GemvItem &one, int wgs, int cap_oct,
                            hipStream_t s) {
   if (items)
     hipLaunchKernelGGL((k_gemv<DT, MR, true>), dim3((unsigned)wgs), dim3(256), gemv_lds_bytes(MR, cap_oct), s,
@@ -392,7 +394,7 @@ static void launch_gemv_mr(const GemvItem *items, const int *wg_item, const Gemv
 // one k_gemv launch: `items` (device) + `wg_item` (device) for a group, or
 // items == NULL and the single item `one`
 template <int DT>
-static void launch_gemv_dt(int m, const GemvItem *items, const int *wg_item, const GemvItem &one, int wgs,
+static void launch_gemv_dt(int m, const GemvItem *items, const int2 *wg_item, const GemvItem &one, int wgs,
                            int cap_oct, hipStream_t s) {
   switch (m) {
     case 1: launch_gemv_mr<DT, 1>(items, wg_item, one, wgs, cap_oct, s); break;
@@ -462,15 +464,39 @@ struct GroupLaunch {
 };
 
 struct GroupPlan {
-  std::vector<size_t> order;                           // non-empty items, in launch order
-  std::vector<int> wg0, wgs, wg_first, qwg0, qwgs, qwg_first;  // per ordered item
-  std::vector<size_t> rec_off;                         // per ordered item, from rec_base
+  std::vector<size_t> order;    // non-empty items, in launch order
+  std::vector<size_t> rec_off;  // per ordered item, from rec_base
   std::vector<GroupLaunch> launches;
+  std::vector<size_t> first;    // per launch: its first ordered item
+  std::vector<int2> map, qmap;  // slot -> (ordered item, tile / part), all launches
   size_t map_off = 0, qmap_off = 0;
   size_t bytes = 0;     // item table + maps (copied from the host)
   size_t rec_base = 0;  // records start
   size_t total = 0;     // bytes of device memory the group needs
 };
+
+// Workgroup slots of a grouped launch.  XCDs take workgroups round-robin
+// (slot 8 p + x runs on XCD x), and each XCD's L2 serves its workgroups.
+// An item's tiles go in runs of up to GEMV_RUN consecutive slots of one XCD,
+// so a run reads the item's activation records through one L2; each run goes
+// to the XCD with the fewest slots so far.  The records kernel's parts are
+// placed the same way.  Unused slots map to item -1.
+constexpr int GEMV_RUN = 8;
+
+static void place_runs(int item, int n, int *pos, std::vector<int2> &slots) {
+  for (int t0 = 0; t0 < n; t0 += GEMV_RUN) {
+    int x = 0;
+    for (int c = 1; c < 8; ++c)
+      if (pos[c] < pos[x]) x = c;
+    const int cnt = std::min(GEMV_RUN, n - t0);
+    for (int q = 0; q < cnt; ++q) {
+      const size_t slot = (size_t)8 * (pos[x] + q) + x;
+      if (slots.size() <= slot) slots.resize(slot + 1, make_int2(-1, 0));
+      slots[slot] = make_int2(item, t0 + q);
+    }
+    pos[x] += cnt;
+  }
+}
 
 static GroupPlan group_plan(const rw_linear *items, size_t count) {
   GroupPlan P;
@@ -481,37 +507,41 @@ static GroupPlan group_plan(const rw_linear *items, size_t count) {
   for (size_t i = 0; i < count; ++i)
     if (items[i].w && items[i].m > 0 && items[i].m <= GEMV_MAX_M) P.order.push_back(i);
   std::stable_sort(P.order.begin(), P.order.end(), [&](size_t x, size_t y) { return key(x) < key(y); });
-  int total = 0, qtotal = 0;
+  const size_t no = P.order.size();
+  P.rec_off.assign(no, 0);
   size_t rec = 0;
-  for (size_t j = 0; j < P.order.size(); ++j) {
-    const rw_weight *w = items[P.order[j]].w;
-    const int m = (int)items[P.order[j]].m;
-    const int ks = gemv_ks(w);
-    if (j == 0 || key(P.order[j]) != key(P.order[j - 1])) {
-      P.launches.push_back(GroupLaunch{w->dtype, m, 0, 0, total, 0, qtotal});
+  for (size_t j0 = 0; j0 < no;) {
+    size_t j1 = j0 + 1;
+    while (j1 < no && key(P.order[j1]) == key(P.order[j0])) ++j1;
+    GroupLaunch L{items[P.order[j0]].w->dtype, (int)items[P.order[j0]].m, 0, 0, (int)P.map.size(), 0,
+                  (int)P.qmap.size()};
+    std::vector<int2> slots, qslots;
+    int pos[8] = {}, qpos[8] = {};
+    for (size_t j = j0; j < j1; ++j) {
+      const rw_weight *w = items[P.order[j]].w;
+      const int m = (int)items[P.order[j]].m;
+      place_runs((int)j, gemv_wgs(w, gemv_ks(w)), pos, slots);
+      place_runs((int)j, (int)cdiv((size_t)m * w->noct * OCT, 256), qpos, qslots);
+      P.rec_off[j] = rec;
+      rec += align_up((size_t)w->noct * OCT * gemv_rec_bytes(m), 256);
+      L.cap_oct = std::max(L.cap_oct, gemv_need(w));
     }
-    GroupLaunch &L = P.launches.back();
-    const int n = gemv_wgs(w, ks), nq = (int)cdiv(w->noct, 2);
-    P.wg0.push_back(L.wgs);
-    P.wgs.push_back(n);
-    P.wg_first.push_back(total);
-    P.qwg0.push_back(L.qwgs);
-    P.qwgs.push_back(nq);
-    P.qwg_first.push_back(qtotal);
-    P.rec_off.push_back(rec);
-    L.wgs += n;
-    L.qwgs += nq;
-    L.cap_oct = std::max(L.cap_oct, gemv_need(w));
-    total += n;
-    qtotal += nq;
-    rec += align_up((size_t)w->noct * OCT * gemv_rec_bytes(m), 256);
+    L.wgs = (int)align_up(slots.size(), 8);
+    L.qwgs = (int)align_up(qslots.size(), 8);
+    slots.resize(L.wgs, make_int2(-1, 0));
+    qslots.resize(L.qwgs, make_int2(-1, 0));
+    P.map.insert(P.map.end(), slots.begin(), slots.end());
+    P.qmap.insert(P.qmap.end(), qslots.begin(), qslots.end());
+    L.cap_oct = gemv_cap(L.m, L.cap_oct);
+    P.launches.push_back(L);
+    P.first.push_back(j0);
+    j0 = j1;
   }
-  for (GroupLaunch &L : P.launches) L.cap_oct = gemv_cap(L.m, L.cap_oct);
-  P.map_off = align_up(P.order.size() * sizeof(GemvItem), 256);
-  P.qmap_off = P.map_off + (size_t)total * sizeof(int);
-  P.bytes = P.order.empty() ? 0 : align_up(P.qmap_off + (size_t)qtotal * sizeof(int), 256);
+  P.map_off = align_up(no * sizeof(GemvItem), 256);
+  P.qmap_off = P.map_off + P.map.size() * sizeof(int2);
+  P.bytes = no == 0 ? 0 : align_up(P.qmap_off + P.qmap.size() * sizeof(int2), 256);
   P.rec_base = P.bytes;
-  P.total = P.order.empty() ? 0 : P.rec_base + rec;
+  P.total = no == 0 ? 0 : P.rec_base + rec;
   return P;
 }
 
@@ -551,24 +581,19 @@ static int check_group_items(const rw_linear *items, size_t count) {
 // `dev` is the device address the tables will have (the records follow them)
 static void fill_tables(const GroupPlan &P, const rw_linear *items, void *host, void *dev) {
   GemvItem *tab = (GemvItem *)host;
-  int *map = (int *)((char *)host + P.map_off);
-  int *qmap = (int *)((char *)host + P.qmap_off);
   for (size_t j = 0; j < P.order.size(); ++j) {
     const rw_linear &it = items[P.order[j]];
     tab[j] = gemv_item(it.w, it.a, it.bias, it.out);
-    tab[j].wg0 = P.wg0[j];
-    tab[j].qwg0 = P.qwg0[j];
     tab[j].rec = (uint8_t *)dev + P.rec_base + P.rec_off[j];
-    for (int q = 0; q < P.wgs[j]; ++q) map[P.wg_first[j] + q] = (int)j;
-    for (int q = 0; q < P.qwgs[j]; ++q) qmap[P.qwg_first[j] + q] = (int)j;
   }
+  memcpy((char *)host + P.map_off, P.map.data(), P.map.size() * sizeof(int2));
+  memcpy((char *)host + P.qmap_off, P.qmap.data(), P.qmap.size() * sizeof(int2));
 }
 
 template <int DT>
-static void launch_records_dt(int m, const GemvItem *items, const int *qmap, int qwgs, hipStream_t s) {
+static void launch_records_dt(int m, const GemvItem *items, const int2 *qmap, int qwgs, hipStream_t s) {
 #define RW_REC(MR)                                                                                          \
-  hipLaunchKernelGGL((k_gemv_records<DT, MR>), dim3((unsigned)qwgs), dim3(256),                               \
-                     (size_t)2 * OCT * gemv_rec_bytes(MR), s, items, qmap)
+  hipLaunchKernelGGL((k_gemv_records<DT, MR>), dim3((unsigned)qwgs), dim3(256), 0, s, items, qmap)
   switch (m) {
     case 1: RW_REC(1); break;
     case 2: RW_REC(2); break;
@@ -585,8 +610,8 @@ static void launch_records_dt(int m, const GemvItem *items, const int *qmap, int
 static int launch_group(const std::vector<GroupLaunch> &launches, const void *table, size_t map_off,
                         size_t qmap_off, hipStream_t s) {
   const GemvItem *dtab = (const GemvItem *)table;
-  const int *dmap = (const int *)((const char *)table + map_off);
-  const int *qmap = (const int *)((const char *)table + qmap_off);
+  const int2 *dmap = (const int2 *)((const char *)table + map_off);
+  const int2 *qmap = (const int2 *)((const char *)table + qmap_off);
   const GemvItem none{};
   for (const GroupLaunch &L : launches) {
     switch (L.dt) {
