@@ -597,34 +597,14 @@ __device__ inline void gemv_fill(const GemvItem &I, int nb, int c0, int c1, uint
     reinterpret_cast<uint4 *>(base + cnb * REC)[z] = make_uint4(0, 0, 0, 0);
 }
 
-// quantize_acts_i8 for one 32-element block held by one lane: the values
-// of quantize_block8 (max and sum are exact in any order): quants as 8
-// natural dwords, sum(q) and d.
-__device__ inline void quantize_block_lane(const float4 (&x)[8], uint32_t (&qd)[8], int &sum, float &d) {
-  float amax = 0.0f;
-#pragma unroll
-  for (int u = 0; u < 8; ++u)
-    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(x[u].x), fabsf(x[u].y)), fmaxf(fabsf(x[u].z), fabsf(x[u].w))));
-  d = __fdiv_rn(amax, 127.0f);
-  const float inv = d > 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
-  sum = 0;
-#pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int q0 = round_clamp_i8(__fmul_rn(x[u].x, inv)), q1 = round_clamp_i8(__fmul_rn(x[u].y, inv));
-    const int q2 = round_clamp_i8(__fmul_rn(x[u].z, inv)), q3 = round_clamp_i8(__fmul_rn(x[u].w, inv));
-    sum += q0 + q1 + q2 + q3;
-    qd[u] = (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
-            ((uint32_t)(q3 & 0xff) << 24);
-  }
-}
-
 // Activation records of a grouped decode launch, quantized once per linear
-// instead of once per k_gemv workgroup.  One lane per (row i, block bl) of
-// an item, rows fastest; workgroup -> (item, part of 256 lanes) through
-// `qwg_item` (item -1 = unused slot).  Each lane
-// writes its row's quants (MFMA order) and SEED / DA / PA entries; the
-// row-0 lane of a block also writes the block's zero parts.  Blocks past nb
-// (the padding of the last octet) get zero records.  The values are those
+// instead of once per k_gemv workgroup.  8 lanes per (row i, block bl), 4
+// elements each (quantize_block8); pairs row-major, so each wavefront reads
+// 8 consecutive blocks of a row (1 KB) per load.  Workgroup -> (item, part
+// of 32 pairs) through `qwg_item` (item -1 = unused slot).  Each lane writes
+// its 4 quants (MFMA order), the block's first lane the row's SEED / DA / PA
+// entries, and row 0's first lane also the block's zero parts.  Blocks past
+// nb (the padding of the last octet) get zero records.  The values are those
 // gemv_fill computes, bit for bit.
 template <int DT, int MR>
 __global__ __launch_bounds__(256) void k_gemv_records(const GemvItem *__restrict__ items,
@@ -635,35 +615,28 @@ __global__ __launch_bounds__(256) void k_gemv_records(const GemvItem *__restrict
   if (wt.x < 0) return;  // a slot no item uses
   const GemvItem I = items[wt.x];
   const int nb = I.w.nb, nbp = I.w.noct * OCT;
-  const int z = wt.y * 256 + (int)threadIdx.x;
-  if (z >= MR * nbp) return;
-  const int bl = z / MR, i = z - bl * MR;
-  float4 x[8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u) x[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (bl < nb) {
-    const float *src = I.a + ((size_t)i * nb + bl) * QK;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) x[u] = ldg_f4(src + 4 * u);
-  }
-  uint32_t qd[8];
-  int sum;
-  float d;
-  quantize_block_lane(x, qd, sum, d);
+  const int t = threadIdx.x, lt = t & 7;
+  const int p = wt.y * 32 + (t >> 3);  // (row, block) pair
+  const bool live = p < MR * nbp;      // uniform per 8-lane group
+  const int i = p / nbp, bl = p - i * nbp;
+  float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (live && bl < nb) x = ldg_f4(I.a + ((size_t)i * nb + bl) * QK + 4 * lt);
+  const BlockQuant bq = quantize_block8(x);  // every lane of the wavefront takes part in the DPP moves
+  if (!live) return;
   uint8_t *rec = I.rec + (size_t)bl * REC;
-  // natural dword u (elements 4u..4u+3) sits at MFMA-order byte mfma_pos(4u)
-  stg_u4(rec + 32 * i, make_uint4(qd[0], qd[1], qd[4], qd[5]));
-  stg_u4(rec + 32 * i + 16, make_uint4(qd[2], qd[3], qd[6], qd[7]));
-  stg_u32(rec + SO + 4 * i, (uint32_t)(-OFF * sum));
-  stg_f(reinterpret_cast<float *>(rec + DO + 4 * i), d);
-  stg_f(reinterpret_cast<float *>(rec + PO + 4 * i), __fmul_rn(d, (float)sum));
-  if (i == 0) {
-    stg_u4(rec + ZO, make_uint4(0, 0, 0, 0));
+  stg_u32(rec + 32 * i + mfma_pos(4 * lt), pack_q4(bq));
+  if (lt == 0) {
+    stg_u32(rec + SO + 4 * i, (uint32_t)(-OFF * bq.sum));
+    stg_f(reinterpret_cast<float *>(rec + DO + 4 * i), bq.d);
+    stg_f(reinterpret_cast<float *>(rec + PO + 4 * i), __fmul_rn(bq.d, (float)bq.sum));
+    if (i == 0) {
+      stg_u4(rec + ZO, make_uint4(0, 0, 0, 0));
 #pragma unroll
-    for (int r = MR; r < 8; ++r) {
-      stg_u32(rec + SO + 4 * r, 0u);
-      stg_u32(rec + DO + 4 * r, 0u);
-      stg_u32(rec + PO + 4 * r, 0u);
+      for (int r = MR; r < 8; ++r) {
+        stg_u32(rec + SO + 4 * r, 0u);
+        stg_u32(rec + DO + 4 * r, 0u);
+        stg_u32(rec + PO + 4 * r, 0u);
+      }
     }
   }
 }

@@ -521,7 +521,7 @@ static GroupPlan group_plan(const rw_linear *items, size_t count) {
       const rw_weight *w = items[P.order[j]].w;
       const int m = (int)items[P.order[j]].m;
       place_runs((int)j, gemv_wgs(w, gemv_ks(w)), pos, slots);
-      place_runs((int)j, (int)cdiv((size_t)m * w->noct * OCT, 256), qpos, qslots);
+      place_runs((int)j, (int)cdiv((size_t)m * w->noct * OCT, 32), qpos, qslots);
       P.rec_off[j] = rec;
       rec += align_up((size_t)w->noct * OCT * gemv_rec_bytes(m), 256);
       L.cap_oct = std::max(L.cap_oct, gemv_need(w));
