@@ -390,7 +390,7 @@ def main() -> int:
             "ms_per_step": round(dms, 4),
             "ms_per_step_with_table_upload": round(dms_call, 4),
             "bytes_per_step": D["bytes"],
-            "launch": "prepared group (rw_rocm_group_run): one k_gemv launch for the set",
+            "launch": "prepared group (rw_rocm_group_run): one k_gemv_records launch (each linear's activation quantized once) and one k_gemv launch for the set",
             "peak": HBM_PEAK_GBS,
             "frac": round(gbs / HBM_PEAK_GBS, 4),
         }

@@ -1,7 +1,7 @@
 // rw_layout.hpp -- how quantized weights and quantized activations sit in HBM.
 //
 // Weights ([n, k] ggml matrix, nb = k/32 blocks per row) are repacked once at
-// upload into four planes.  Rows are interleaved in groups of 32 ("row
+// upload into the decode / validation planes below and the GEMM planes.  Rows are interleaved in groups of 32 ("row
 // groups"), so the 32 rows of one group are contiguous for a given block:
 // a wavefront reading one block of 32 consecutive rows touches one
 // contiguous span.  Blocks are padded to a multiple of 8 ("octets") so the
@@ -33,25 +33,26 @@
 // rotl(X, t) & 0x10101010: element 4t+u's bit sits at bit (8u + 4 - t) mod 32
 // of X.  Two VALU ops per 4 elements instead of four.
 //
-// GEMM scale planes (weights): the f16 d_b and m_b of each block split
-// exactly into two bf16 (8 + 3 significant bits) and packed as one dword
-// (low half = high part), the B operand of the scale / min-term MFMAs:
-//   dsp [ngroups][nb_pad][32 rows]    u32  bf16 pair of d_b
-//   msp [ngroups][nb_pad][32 rows]    u32  bf16 pair of m_b (_1 formats)
+// GEMM planes (weights), indexed like qs:
+//   q8  [ngroups][nb_pad][32 rows][32 B]  every quant as one byte in MFMA
+//        order (Q4/Q5 the unsigned value as stored; Q8_0 reads qs itself)
+//   dm  [ngroups][nb_pad][32 rows]        u32: f16 d_b (low), f16 m_b (high)
 //
 // Quantized activations ([m, k] f32 in, quantize_acts_i8 semantics) are
-// written by the quantize kernel in the same row-group form:
-//   qa  [mgroups][nb][32 rows][32 B]  int8, MFMA order
-//   da  [mgroups][nb][32 rows]        f32 block scale d_a
-//   pa  [mgroups][nb][32 rows]        f32 d_a * (float)sum(q_a)  (min term)
-//   sa  [mgroups][nb][32 rows]        i32 sum(q_a)
-//   qh16 [mgroups][nb][32 rows][32 f16]  q_a as f16 (exact), MFMA order
-//   ds16 [mgroups][nb][32 rows][4 u32]   d_a split exactly into three bf16
-//        (hi, mid, lo: 8 + 8 + 8 bits), packed [hi hi][mid mid][lo lo][0 0]
-//   pm16 [mgroups][nb][32 rows][4 u32]   the same split of pa
-// The d_a and d_b splits meet in one bf16 MFMA whose six nonzero k-slots
-// pair (hi, mid, lo) x (hi, lo): the sum of the six exact products is
-// d_a * d_b before the single f32 rounding.
+// written by the quantize kernels in the same row-group form:
+//   int8 layout (decode, validation):
+//     qa  [mgroups][nb][32 rows][32 B]  int8, MFMA order
+//     da  [mgroups][nb][32 rows]        f32 block scale d_a
+//     pa  [mgroups][nb][32 rows]        f32 d_a * (float)sum(q_a)  (min term)
+//     sa  [mgroups][nb][32 rows]        i32 sum(q_a)
+//   f16 layout (encoder GEMM):
+//     a16 f16(d_a * q_a * 2^(15 - e_row)) at a16_index (below), one rounding
+//     rs  [rows] f32 2^(e_row - 15), applied to the GEMM's output rows
+//
+// Decode records (k_gemv, k_gemv_records): per block of an m-row activation,
+// the rows' 32 int8 quants in MFMA order, 16 zero bytes (the A operand of
+// MFMA lanes whose row is >= m), then 8-entry arrays of -c*sum(q_a), d_a and
+// d_a*sum(q_a); see gemv_rec_bytes.
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
