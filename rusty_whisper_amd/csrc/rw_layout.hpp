@@ -1,8 +1,9 @@
 // rw_layout.hpp -- how quantized weights and quantized activations sit in HBM.
 //
 // Weights ([n, k] ggml matrix, nb = k/32 blocks per row) are repacked once at
-// upload into the decode / validation planes below and the GEMM planes.  Rows are interleaved in groups of 32 ("row
-// groups"), so the 32 rows of one group are contiguous for a given block:
+// upload into the decode / validation planes below and the GEMM planes.
+// Rows are interleaved in groups of 32 ("row groups"), so the 32 rows of one
+// group are contiguous for a given block:
 // a wavefront reading one block of 32 consecutive rows touches one
 // contiguous span.  Blocks are padded to a multiple of 8 ("octets") so the
 // per-block scalars of 8 blocks are 16/32 contiguous bytes per row.
