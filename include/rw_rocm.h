@@ -49,6 +49,7 @@ extern "C" {
 #define RW_ENODEV (-2)  /* no usable gfx950 device / bad device index */
 #define RW_EHIP (-3)    /* a HIP runtime call failed */
 #define RW_ENOMEM (-4)  /* device allocation failed */
+#define RW_EIO (-5)     /* a model file cannot be opened, read or mapped */
 
 /* ggml dtype ids (src/quant.rs:43-52) */
 #define RW_Q4_0 2
@@ -205,6 +206,59 @@ int rw_rocm_quantize_acts(const float *a, size_t m, size_t k, int8_t *q, float *
  * int8 matrix cores (v_mfma_i32_32x32x32_i8) from the resident weight
  * planes.  S is host [m, n, k/32]. */
 int rw_rocm_block_dots(const rw_weight *w, const int8_t *qa, size_t m, int32_t *S);
+
+/* ---- Model files straight to resident weights ----
+ *
+ * rw_rocm_model_load reads a whisper model in either container the reference
+ * loads -- the legacy ggml ".bin" (src/model.rs:145-275) or GGUF with the
+ * reference's metadata mapping (src/gguf.rs:156-300) -- chosen by the magic,
+ * from a read-only memory map.  Every 2-D block-quantized matrix goes to the
+ * current device through rw_rocm_weight_upload straight from the mapped bytes
+ * (the reference's Weight::Quant); every other tensor becomes host f32 as the
+ * reference's Weight::Dense (f16 by the exact conversion of
+ * src/model.rs:68-86, quantized tensors of other ranks by d*q + m).  Shapes
+ * are row-major (the file's innermost-first dims flipped).  A malformed file
+ * fails with RW_EINVAL and the reference's message; an unreadable one with
+ * RW_EIO.  RW_MODEL_PARSE_ONLY skips the uploads (no device needed): the
+ * quantized matrices are then reachable only as their blocks
+ * (rw_rocm_model_raw).  Replaces model::load_model and gguf::load.  Pointers
+ * returned by the accessors live until rw_rocm_model_free, which also frees
+ * the uploaded weights. */
+typedef struct rw_model rw_model;
+#define RW_MODEL_PARSE_ONLY 1
+int rw_rocm_model_load(const char *path, int flags, rw_model **out);
+void rw_rocm_model_free(rw_model *m);
+
+/* The 11 hyperparameters in the order of HParams (src/model.rs:24-37):
+ * n_vocab, n_audio_ctx, n_audio_state, n_audio_head, n_audio_layer,
+ * n_text_ctx, n_text_state, n_text_head, n_text_layer, n_mels, ftype. */
+int rw_rocm_model_hparams(const rw_model *m, int32_t *hp);
+
+/* The embedded mel filterbank, n_mel x n_fft row-major f32 (Model::mel_filters). */
+int rw_rocm_model_mel_filters(const rw_model *m, const float **data, size_t *n_mel, size_t *n_fft);
+
+/* Vocabulary (Model::vocab): n_vocab tokens as raw bytes, the ids past the
+ * file's own tokens named "[_extra_token_<id>]" as the reference names them. */
+int rw_rocm_model_vocab_size(const rw_model *m, size_t *n);
+int rw_rocm_model_token(const rw_model *m, size_t id, const uint8_t **bytes, size_t *len);
+
+/* Tensors (Model::tensors): count, name by index (file order; a repeated name
+ * keeps the last tensor, as the reference's map does), and by name the ggml
+ * dtype, rank and row-major shape (unused dims 1).  rw_rocm_model_tensor
+ * returns 1 for a quantized matrix (Weight::Quant), 0 for a dense tensor. */
+int rw_rocm_model_tensor_count(const rw_model *m, size_t *n);
+int rw_rocm_model_tensor_name(const rw_model *m, size_t i, const char **name);
+int rw_rocm_model_tensor(const rw_model *m, const char *name, int *dtype, int *ndims, size_t *shape);
+
+/* A quantized matrix's resident device weight (RW_EINVAL for a dense tensor
+ * or a parse-only load). */
+int rw_rocm_model_weight(const rw_model *m, const char *name, const rw_weight **w);
+
+/* A dense tensor's host f32 data (RW_EINVAL for a quantized matrix). */
+int rw_rocm_model_dense(const rw_model *m, const char *name, const float **data, size_t *len);
+
+/* A tensor's bytes as stored in the file (ggml blocks for quantized ones). */
+int rw_rocm_model_raw(const rw_model *m, const char *name, const uint8_t **raw, size_t *len);
 
 /* Copy the calling thread's last error text (NUL-terminated, truncated to
  * len).  Returns the full text length. */

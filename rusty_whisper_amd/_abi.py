@@ -17,8 +17,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "librw_rocm.so")
 HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "rw_rocm.h")
 
-RW_OK, RW_EINVAL, RW_ENODEV, RW_EHIP, RW_ENOMEM = 0, -1, -2, -3, -4
-CODE_NAMES = {RW_EINVAL: "RW_EINVAL", RW_ENODEV: "RW_ENODEV", RW_EHIP: "RW_EHIP", RW_ENOMEM: "RW_ENOMEM"}
+RW_OK, RW_EINVAL, RW_ENODEV, RW_EHIP, RW_ENOMEM, RW_EIO = 0, -1, -2, -3, -4, -5
+CODE_NAMES = {RW_EINVAL: "RW_EINVAL", RW_ENODEV: "RW_ENODEV", RW_EHIP: "RW_EHIP", RW_ENOMEM: "RW_ENOMEM",
+              RW_EIO: "RW_EIO"}
 Q4_0, Q4_1, Q5_0, Q5_1, Q8_0 = 2, 3, 6, 7, 8
 DTYPES = (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0)
 QK = 32
@@ -74,6 +75,21 @@ _SIGNATURES = {
                                         C.c_void_p]),
     "rw_rocm_block_dots": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     "rw_rocm_last_error": (C.c_int, [C.c_char_p, C.c_size_t]),
+    "rw_rocm_model_load": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(C.c_void_p)]),
+    "rw_rocm_model_free": (None, [C.c_void_p]),
+    "rw_rocm_model_hparams": (C.c_int, [C.c_void_p, C.POINTER(C.c_int32)]),
+    "rw_rocm_model_mel_filters": (C.c_int, [C.c_void_p, C.POINTER(C.POINTER(C.c_float)),
+                                            C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
+    "rw_rocm_model_vocab_size": (C.c_int, [C.c_void_p, C.POINTER(C.c_size_t)]),
+    "rw_rocm_model_token": (C.c_int, [C.c_void_p, C.c_size_t, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]),
+    "rw_rocm_model_tensor_count": (C.c_int, [C.c_void_p, C.POINTER(C.c_size_t)]),
+    "rw_rocm_model_tensor_name": (C.c_int, [C.c_void_p, C.c_size_t, C.POINTER(C.c_char_p)]),
+    "rw_rocm_model_tensor": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_int),
+                                       C.POINTER(C.c_size_t)]),
+    "rw_rocm_model_weight": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_void_p)]),
+    "rw_rocm_model_dense": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.POINTER(C.c_float)),
+                                      C.POINTER(C.c_size_t)]),
+    "rw_rocm_model_raw": (C.c_int, [C.c_void_p, C.c_char_p, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]),
 }
 
 _lib = None
@@ -262,6 +278,104 @@ class Group:
     def free(self) -> None:
         if self.handle:
             lib().rw_rocm_group_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+MODEL_PARSE_ONLY = 1
+HPARAM_NAMES = ("n_vocab", "n_audio_ctx", "n_audio_state", "n_audio_head", "n_audio_layer", "n_text_ctx",
+                "n_text_state", "n_text_head", "n_text_layer", "n_mels", "ftype")
+
+
+class _ModelWeight(DeviceWeight):
+    """A quantized matrix owned by a Model (freed with it)."""
+
+    def __init__(self, handle: int, dtype: int, n: int, k: int, owner: "Model"):
+        self.handle, self.dtype, self.n, self.k = handle, dtype, n, k
+        self._owner = owner
+
+    def free(self) -> None:
+        self.handle = None
+
+    def __del__(self):
+        pass
+
+
+class Model:
+    """A whisper model file (ggml .bin or GGUF) loaded by rw_rocm_model_load:
+    hparams, mel filters, vocab, and named tensors -- quantized matrices as
+    resident device weights, the rest as host f32 arrays."""
+
+    def __init__(self, path: str, parse_only: bool = False):
+        h = C.c_void_p()
+        check(lib().rw_rocm_model_load(os.fsencode(path), MODEL_PARSE_ONLY if parse_only else 0, C.byref(h)))
+        self.handle = h.value
+        hp = (C.c_int32 * 11)()
+        check(lib().rw_rocm_model_hparams(self.handle, hp))
+        self.hparams = dict(zip(HPARAM_NAMES, list(hp)))
+
+    def mel_filters(self) -> np.ndarray:
+        p, nm, nf = C.POINTER(C.c_float)(), C.c_size_t(), C.c_size_t()
+        check(lib().rw_rocm_model_mel_filters(self.handle, C.byref(p), C.byref(nm), C.byref(nf)))
+        n = nm.value * nf.value
+        if n == 0:
+            return np.zeros((nm.value, nf.value), dtype=np.float32)
+        return np.ctypeslib.as_array(p, shape=(n,)).copy().reshape(nm.value, nf.value)
+
+    def vocab(self) -> list[bytes]:
+        n = C.c_size_t()
+        check(lib().rw_rocm_model_vocab_size(self.handle, C.byref(n)))
+        out = []
+        for i in range(n.value):
+            p, ln = C.c_void_p(), C.c_size_t()
+            check(lib().rw_rocm_model_token(self.handle, i, C.byref(p), C.byref(ln)))
+            out.append(C.string_at(p.value, ln.value) if ln.value else b"")
+        return out
+
+    def names(self) -> list[str]:
+        n = C.c_size_t()
+        check(lib().rw_rocm_model_tensor_count(self.handle, C.byref(n)))
+        out = []
+        for i in range(n.value):
+            nm = C.c_char_p()
+            check(lib().rw_rocm_model_tensor_name(self.handle, i, C.byref(nm)))
+            out.append(nm.value.decode(errors="replace"))
+        return out
+
+    def tensor(self, name: str):
+        """(dtype, row-major shape, is_quantized_matrix)."""
+        dt, nd = C.c_int(), C.c_int()
+        sh = (C.c_size_t * 3)()
+        q = check(lib().rw_rocm_model_tensor(self.handle, name.encode(), C.byref(dt), C.byref(nd), sh))
+        return dt.value, tuple(sh[: nd.value]), bool(q)
+
+    def weight(self, name: str) -> DeviceWeight:
+        h = C.c_void_p()
+        check(lib().rw_rocm_model_weight(self.handle, name.encode(), C.byref(h)))
+        dt, shape, _ = self.tensor(name)
+        return _ModelWeight(h.value, dt, shape[0], shape[1], self)
+
+    def dense(self, name: str) -> np.ndarray:
+        p, n = C.POINTER(C.c_float)(), C.c_size_t()
+        check(lib().rw_rocm_model_dense(self.handle, name.encode(), C.byref(p), C.byref(n)))
+        _, shape, _ = self.tensor(name)
+        if n.value == 0:
+            return np.zeros(shape, dtype=np.float32)
+        return np.ctypeslib.as_array(p, shape=(n.value,)).copy().reshape(shape)
+
+    def raw(self, name: str) -> bytes:
+        p, n = C.c_void_p(), C.c_size_t()
+        check(lib().rw_rocm_model_raw(self.handle, name.encode(), C.byref(p), C.byref(n)))
+        return C.string_at(p.value, n.value) if n.value else b""
+
+    def free(self) -> None:
+        if getattr(self, "handle", None):
+            lib().rw_rocm_model_free(self.handle)
             self.handle = None
 
     def __del__(self):

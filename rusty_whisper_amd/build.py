@@ -1,6 +1,7 @@
 """Build recipe for the package's native libraries (run from __graft_entry__.build()).
 
-  librw_rocm.so   hipcc, gfx950 only: csrc/rw_rocm.hip (+ rw_kernels.hpp)
+  librw_rocm.so   hipcc, gfx950 only: csrc/rw_rocm.hip (+ rw_kernels.hpp) and
+                  the host-only model loader csrc/rw_model.cpp
   _rw_quant*.so   g++: the C++ mirror of the reference's quant API
                   (host/rw_quant.cpp) with its pybind11 binding
 
@@ -46,9 +47,9 @@ def _run(cmd: list[str]) -> None:
 
 
 def build_rocm(extra: list[str] | None = None) -> str:
-    src = os.path.join(CSRC, "rw_rocm.hip")
+    srcs = [os.path.join(CSRC, "rw_rocm.hip"), os.path.join(CSRC, "rw_model.cpp")]
     tmp = LIB_ROCM + ".tmp"
-    _run([HIPCC, *HIP_FLAGS, *(extra or []), f"-I{INCLUDE}", f"-I{CSRC}", src, "-o", tmp])
+    _run([HIPCC, *HIP_FLAGS, *(extra or []), f"-I{INCLUDE}", f"-I{CSRC}", *srcs, "-o", tmp])
     os.replace(tmp, LIB_ROCM)
     return LIB_ROCM
 

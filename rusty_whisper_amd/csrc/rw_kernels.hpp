@@ -771,8 +771,7 @@ template <int DT, int MR, bool GROUPED>
 __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restrict__ items, const int2 *__restrict__ wg_item,
                                               GemvItem one, int cap_oct) {
   extern __shared__ __align__(16) uint8_t lds[];
-  constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR, SO = ZO + 16, DO = SO + 32, PO = DO + 32;
-  constexpr int OFF = DT == 2 ? 8 : DT == 6 ? 16 : 0;  // centering offset
+  constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR;
   constexpr int QB = DT == 8 ? 32 : 16;                // qs bytes per row-block
   // the descriptor is wave-uniform: scalar loads from the table or kernarg
   const int2 wt = GROUPED ? wg_item[blockIdx.x] : make_int2(0, (int)blockIdx.x);  // (item, tile)

@@ -35,6 +35,12 @@ using namespace rw;
 
 static thread_local std::string g_err;
 
+// the error text of a failure raised outside this file (rw_model.cpp)
+int rw_internal_fail(int code, const char *msg) {
+  g_err = msg;
+  return code;
+}
+
 static int fail(int code, const char *fmt, ...) {
   char buf[512];
   va_list ap;
