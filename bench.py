@@ -238,6 +238,46 @@ def time_decode(A, torch, D, steps: int, warmup: int, stream):
     return t_group, t_call
 
 
+def time_model_load(A, synth, dtype: int, path: str, reps: int = 2):
+    """rw_rocm_model_load on a ggml .bin holding large-v3's quantized matrices
+    (32 encoder layers x 6 linears, 32 decoder layers x 10, the token
+    embedding [51866, 1280]) as random blocks: parse the map, upload and
+    repack every matrix.  The file is freshly written, so it is read from the
+    page cache; returns (seconds per load, file bytes, matrices)."""
+    import struct
+
+    import numpy as np
+
+    cfg = synth.LARGE_V3
+    d, fc, layers = cfg["d"], cfg["fc"], cfg["layers"]
+    shapes = [(f"encoder.blocks.{i}.{nm}.weight", n, k) for i in range(layers)
+              for nm, n, k in synth.encoder_layer_shapes(d, fc)]
+    shapes += [(f"decoder.blocks.{i}.{nm}.weight", n, k) for i in range(layers)
+               for nm, n, k in synth.decoder_layer_shapes(d, fc)]
+    shapes.append(("decoder.token_embedding.weight", cfg["n_vocab"], d))
+    rng = np.random.default_rng(7)
+    bb = synth.BLOCK_BYTES[dtype]
+    i32 = lambda v: struct.pack("<i", v)  # noqa: E731
+    with open(path, "wb") as f:
+        hp = [cfg["n_vocab"], 1500, d, 20, layers, 448, d, 20, layers, 128, 1]
+        f.write(i32(0x67676D6C) + b"".join(i32(v) for v in hp) + i32(0) + i32(0) + i32(0))
+        for name, n, k in shapes:
+            nm = name.encode()
+            f.write(i32(2) + i32(len(nm)) + i32(dtype) + i32(k) + i32(n) + nm)
+            blocks = rng.integers(0, 256, size=(n * k // 32, bb), dtype=np.uint8)
+            blocks[:, 0:2] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)  # finite scales
+            f.write(blocks.tobytes())
+        size = f.tell()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        M = A.Model(path)
+        times.append(time.perf_counter() - t0)
+        M.free()
+    os.unlink(path)
+    return min(times), size, len(shapes)
+
+
 def cpu_baseline(synth, dtype: int, m: int, budget_s: float):
     """The reference CPU path (oracle/cpu_baseline.c) on one large-v3 encoder
     layer: each of the six linears on its first call (cold path, as the
@@ -293,6 +333,8 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--load-model", default="",
+                    help="also time the model loader on a large-v3-shaped ggml file written to this path")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="first copy this many MiB device to device (a kernel of known traffic, to scale "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -396,6 +438,18 @@ def main() -> int:
         }
         del D
         torch.cuda.empty_cache()
+
+    if args.load_model:
+        lq = synth.BY_NAME[args.decode_quant]
+        secs, size, count = time_model_load(A, synth, lq, args.load_model)
+        log(f"model load {secs:.3f} s for {size / 1e9:.3f} GB ({size / secs / 1e9:.2f} GB/s, {count} matrices)")
+        result["model_load"] = {
+            "workload": f"ggml .bin of large-v3's {count} quantized matrices ({args.decode_quant}, random blocks), "
+                        f"in the page cache: parse, upload and repack every matrix",
+            "seconds": round(secs, 4),
+            "file_bytes": size,
+            "GB_per_s": round(size / secs / 1e9, 3),
+        }
 
     if not args.no_cpu:
         cb = cpu_baseline(synth, dtype, args.m, args.cpu_seconds)
