@@ -335,47 +335,57 @@ __device__ inline float quant_q(float v) {
   return v <= -0.5f ? -r : r;
 }
 
-// Activations for the encoder GEMM: one wavefront per row (4 rows per
-// workgroup; rows >= m of the padded row groups are written as zeros), lanes
-// 8b + t holding elements 4t..4t+3 of blocks 8p + b.  The quantization is
-// quantize_acts_i8's (src/quant.rs:691-716) bit for bit: the block maxima
-// come from 8-lane DPP moves, and the correctly rounded d = amax / 127 and
-// inv = 1 / d of pass p are computed once, by lane p % 8 of each 8-lane
-// group, and read back by DPP broadcast.  Each element is stored as
-// f16(q_a * (d_a * 2^(15-e))) at its a16_index position, e chosen from the
-// row's largest |x| so that the largest value lands in [2^14, 2^15): no
-// value overflows, and every value keeps f16's full precision unless it is
-// below 2^-28 of the row's largest.  d_a * 2^(15-e) is exact unless it falls
-// below f32's normal range, and then every q_a times it is zero in f16
-// either way.  rs[row] = 2^(e-15) undoes the scaling in the GEMM's epilogue.  NP passes of 8 blocks stay in registers; a longer
-// row is read twice, once for its largest |x| and once to quantize.
-template <int NP>
+// Activations for the encoder GEMM: WPR wavefronts per row (4 / WPR rows
+// per workgroup; rows >= m of the padded row groups are written as zeros).
+// A row's blocks go in passes of 8 (1 KB of f32), pass P to wavefront
+// P % WPR, whose lanes 8b + t hold elements 4t..4t+3 of block 8P + b.  The
+// quantization is quantize_acts_i8's (src/quant.rs:691-716) bit for bit: the
+// block maxima come from 8-lane DPP moves, and the correctly rounded
+// d = amax / 127 and inv = 1 / d of a wavefront's pass p are computed once, by
+// lane p % 8 of each 8-lane group, and read back by DPP broadcast.  Each
+// element is stored as f16(q_a * (d_a * 2^(15-e))) at its a16_index position,
+// e chosen from the row's largest |x| (the wavefronts of a row meet in LDS)
+// so that the largest value lands in [2^14, 2^15): no value overflows, and
+// every value keeps f16's full precision unless it is below 2^-28 of the
+// row's largest.  d_a * 2^(15-e) is exact unless it falls below f32's normal
+// range, and then every q_a times it is zero in f16 either way.
+// rs[row] = 2^(e-15) undoes the scaling in the GEMM's epilogue.  NP passes per
+// wavefront stay in registers; a longer row is read twice, once for its
+// largest |x| and once to quantize.
+template <int NP, int WPR>
 __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ a, int m, int k, int nb,
                                                       uint16_t *__restrict__ a16, float *__restrict__ rs) {
-  const int lane = threadIdx.x & 63, row = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  static_assert(WPR == 1 || WPR == 2 || WPR == 4, "a workgroup holds whole rows");
+  __shared__ float part_max[4];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // workgroup 8j + x runs on XCD x; the 8 * WPR workgroups of a row group
+  // all take the same x, so the group's interleaved f16 lines are written
+  // through one L2
+  constexpr int WPG = 8 * WPR;  // workgroups per row group
+  const int x8 = blockIdx.x & 7, j = blockIdx.x >> 3;
+  const int g = 8 * (j / WPG) + x8;
+  if (g * RG >= ((m + RG - 1) / RG) * RG) return;  // a slot past the last row group (whole workgroup)
+  const int r = (j % WPG) * (4 / WPR) + wv / WPR, part = wv % WPR;
+  const int row = g * RG + r;
   const int lb = lane >> 3, lt = lane & 7;
-  const int g = row / RG, r = row % RG;
   // stores: the plane as a buffer, this lane's place in a block as the
   // vector offset, the block's place as the scalar offset
   const auto ro = buffer_rsrc(a16, (uint32_t)((size_t)(m + RG - 1) / RG * RG * (size_t)k * 2));
   const uint32_t voff = (uint32_t)(a16_index(nb, g, 0, r, 4 * lt) - a16_index(nb, g, 0, 0, 0)) * 2 +
                         (uint32_t)lb * 2048u;
   const uint32_t gbase = (uint32_t)a16_index(nb, g, 0, 0, 0) * 2;
-  if (row >= m) {  // uniform per wavefront
-    for (int bl = lb; bl < nb; bl += 8)
-      *reinterpret_cast<uint2 *>(a16 + a16_index(nb, g, bl, r, 4 * lt)) = make_uint2(0u, 0u);
-    if (lane == 0) rs[row] = 0.0f;
-    return;
-  }
+  const bool live = row < m;  // uniform per row
   const float *x = a + (size_t)row * k;
-  constexpr int CB = 8 * NP;  // blocks per chunk
+  constexpr int CB = 8 * NP * WPR;  // blocks per chunk (all wavefronts of the row)
   const int nch = (nb + CB - 1) / CB;
+  // first block of this wavefront's pass p in chunk c
+  auto first = [&](int c, int p) __attribute__((always_inline)) { return c * CB + 8 * (p * WPR + part); };
   float4 v[NP];
   float bam[NP];
   auto load = [&](int c) __attribute__((always_inline)) {
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-      const int bl = c * CB + 8 * p + lb;
+      const int bl = first(c, p) + lb;
       v[p] = make_float4(0.f, 0.f, 0.f, 0.f);
       if (bl < nb) v[p] = ldg_f4(x + (size_t)bl * QK + 4 * lt);
     }
@@ -389,14 +399,32 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
     }
     return amax;
   };
-  float amax = 0.0f;
-  for (int c = 0; c < nch; ++c) {
-    load(c);
-    amax = fmaxf(amax, block_max());
+  float amax = 0.0f;  // fmaxf drops NaN, in any order of combination
+  if (live) {
+    for (int c = 0; c < nch; ++c) {
+      load(c);
+      amax = fmaxf(amax, block_max());
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 8));
+    amax = fmaxf(amax, __shfl_xor(amax, 16));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
   }
-  amax = fmaxf(amax, __shfl_xor(amax, 8));
-  amax = fmaxf(amax, __shfl_xor(amax, 16));
-  amax = fmaxf(amax, __shfl_xor(amax, 32));
+  if (WPR > 1) {  // every wavefront reaches the barrier
+    if (lane == 0) part_max[wv] = amax;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < WPR; ++j) amax = fmaxf(amax, part_max[wv - part + j]);
+  }
+  if (!live) {
+    for (int c = 0; c < nch; ++c)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const int bl = first(c, p) + lb;
+        if (bl < nb) *reinterpret_cast<uint2 *>(a16 + a16_index(nb, g, bl, r, 4 * lt)) = make_uint2(0u, 0u);
+      }
+    if (part == 0 && lane == 0) rs[row] = 0.0f;
+    return;
+  }
   int e = 15;  // zero, inf or NaN rows: no scaling
   if (amax > 0.0f && amax <= 3.4028235e38f) {
     frexpf(amax, &e);  // amax in [2^(e-1), 2^e)
@@ -422,7 +450,7 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
     }
     auto pass = [&](auto pc) __attribute__((always_inline)) {
       constexpr int p = decltype(pc)::value;
-      const int b0 = c * CB + 8 * p;
+      const int b0 = first(c, p);
       if (b0 >= nb) return;  // uniform
       const float inv = bcast8<p & 7>(iv[p >> 3], lt);
       const float dd = bcast8<p & 7>(dv[p >> 3], lt) * down;
@@ -440,7 +468,7 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
       (pass(std::integral_constant<int, P>{}), ...);
     }(std::make_integer_sequence<int, NP>{});
   }
-  if (lane == 0) rs[row] = ldexpf(1.0f, e - 15);
+  if (part == 0 && lane == 0) rs[row] = ldexpf(1.0f, e - 15);
 }
 
 // --------------------------------------------------- MFMA operand unpack

@@ -254,18 +254,21 @@ static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &
   if (L.f16) {
     if ((size_t)L.mgroups * RG * k * 2 >= ((size_t)1 << 32))
       return fail(RW_EINVAL, "activation [%zu, %zu] too large for the GEMM layout's 32-bit offsets", m, k);
-    // one wavefront per row, 4 rows per workgroup; NP passes of 8 blocks in
-    // registers (longer rows are read twice)
-    const unsigned wgs = (unsigned)((size_t)L.mgroups * RG / 4);
+    // WPR wavefronts per row, 4 / WPR rows per workgroup; NP passes of 8
+    // blocks per wavefront in registers (longer rows are read twice)
+    const size_t g8 = align_up((size_t)L.mgroups, 8);  // row groups, padded to whole XCD rounds
     uint16_t *a16 = (uint16_t *)(b + L.off_a16);
     float *rs = (float *)(b + L.off_rs);
-#define RW_QF16(NP) hipLaunchKernelGGL(k_quantize_f16<NP>, dim3(wgs), dim3(256), 0, s, a, (int)m, (int)k, L.nb, a16, rs)
-    if (L.nb <= 8) RW_QF16(1);
-    else if (L.nb <= 16) RW_QF16(2);
-    else if (L.nb <= 40) RW_QF16(5);
-    else if (L.nb <= 64) RW_QF16(8);
-    else if (L.nb <= 160) RW_QF16(20);
-    else RW_QF16(32);
+#define RW_QF16(NP, WPR)                                                                                    \
+  hipLaunchKernelGGL((k_quantize_f16<NP, WPR>), dim3((unsigned)(g8 * RG * WPR / 4)), dim3(256), 0, s, a, (int)m, \
+                     (int)k, L.nb, a16, rs)
+    const int passes = (L.nb + 7) / 8;
+    if (passes <= 1) RW_QF16(1, 1);
+    else if (passes <= 2) RW_QF16(1, 2);
+    else if (passes <= 4) RW_QF16(1, 4);
+    else if (passes <= 8) RW_QF16(2, 4);
+    else if (passes <= 20) RW_QF16(5, 4);
+    else RW_QF16(8, 4);
 #undef RW_QF16
     LAUNCH_TRY("k_quantize_f16");
     return RW_OK;

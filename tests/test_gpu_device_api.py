@@ -250,6 +250,9 @@ def _scale_rows(k):
     tiny = np.full(k, 1e-40, np.float32)  # subnormal row maximum: e clamps at -110
     tiny[::3] = -3e-41
     rows.append(tiny)
+    late = np.full(k, 3e-3, np.float32)  # the row maximum in the last block (the last pass's wavefront)
+    late[-1] = -7e4
+    rows.append(late)
     return np.stack(rows)
 
 
@@ -278,8 +281,9 @@ def _a16_index(m, k):
     return (g * nb + bl) * 1024 + (e >> 4) * 512 + (32 * ((e >> 3) & 1) + r) * 8 + (e & 7)
 
 
-@pytest.mark.parametrize("k", [32, 96, 1280, 5120, 8224, 16384])
+@pytest.mark.parametrize("k", [32, 96, 416, 1024, 1280, 2048, 5120, 8224, 16384])
 def test_gemm_activation_plane_bit_exact(torch, k):
+    # one, two and four wavefronts per row (416: two; 1024 and up: four);
     # 8224 and 16384 take the long-row path (the row is read twice)
     a = np.concatenate([activations(21, k, seed=k, outliers=0.01), edge_activation_rows(k), _scale_rows(k)])
     m = a.shape[0]
