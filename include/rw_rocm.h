@@ -207,6 +207,30 @@ int rw_rocm_quantize_acts(const float *a, size_t m, size_t k, int8_t *q, float *
  * planes.  S is host [m, n, k/32]. */
 int rw_rocm_block_dots(const rw_weight *w, const int8_t *qa, size_t m, int32_t *S);
 
+/* ---- Multi-head attention ----
+ *
+ * out[t_q, n_state] = concat over heads h of softmax(q_h k_h^T / sqrt(dh)
+ * + mask) v_h, with q_h the h-th group of dh = n_state / n_head columns.
+ * Replaces encoder::multi_head_attention / mha_split_kv
+ * (src/encoder.rs:48-80, 109-119): with `causal`, query row i sits at
+ * absolute position t_kv - t_q + i and sees kv rows up to it.  Computed in
+ * f32-equivalent precision (f16 hi/lo pairs on the matrix cores, f32
+ * softmax); within 1e-3 row-L2 of the reference (in practice a few f32
+ * roundings).  Heads of 64 values only (every whisper model); |q|, |k|, |v|
+ * below 65504.  RW_EINVAL for other head sizes, n_state % n_head != 0,
+ * causal with t_q > t_kv, or rows not 16-byte aligned.
+ *
+ * _dev: device pointers, row strides ld* in floats (>= n_state, multiples
+ * of 4 for q, k and out), queued on `stream`; the workspace (NULL: one kept
+ * per (device, stream)) holds rw_rocm_attention_workspace_size bytes.
+ * rw_rocm_attention: host arrays, dense rows, synchronous. */
+size_t rw_rocm_attention_workspace_size(size_t t_q, size_t t_kv, size_t n_state);
+int rw_rocm_attention_dev(const float *q, size_t ldq, const float *k, size_t ldk, const float *v, size_t ldv,
+                          size_t t_q, size_t t_kv, size_t n_state, int n_head, int causal, float *out, size_t ldo,
+                          void *workspace, size_t workspace_len, void *stream);
+int rw_rocm_attention(const float *q, const float *k, const float *v, size_t t_q, size_t t_kv, size_t n_state,
+                      int n_head, int causal, float *out);
+
 /* ---- Model files straight to resident weights ----
  *
  * rw_rocm_model_load reads a whisper model in either container the reference

@@ -75,6 +75,12 @@ _SIGNATURES = {
                                         C.c_void_p]),
     "rw_rocm_block_dots": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     "rw_rocm_last_error": (C.c_int, [C.c_char_p, C.c_size_t]),
+    "rw_rocm_attention_workspace_size": (C.c_size_t, [C.c_size_t, C.c_size_t, C.c_size_t]),
+    "rw_rocm_attention_dev": (C.c_int, [C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t,
+                                        C.c_size_t, C.c_size_t, C.c_size_t, C.c_int, C.c_int, C.c_void_p,
+                                        C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "rw_rocm_attention": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t,
+                                    C.c_int, C.c_int, C.c_void_p]),
     "rw_rocm_model_load": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(C.c_void_p)]),
     "rw_rocm_model_free": (None, [C.c_void_p]),
     "rw_rocm_model_hparams": (C.c_int, [C.c_void_p, C.POINTER(C.c_int32)]),
@@ -285,6 +291,36 @@ class Group:
             self.free()
         except Exception:
             pass
+
+
+# ------------------------------------------------------------ attention
+
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, n_head: int, causal: bool = False) -> np.ndarray:
+    """Host arrays in, host array out (rw_rocm_attention): the reference's
+    multi_head_attention (src/encoder.rs:109-119)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    if q.ndim != 2 or k.ndim != 2 or v.shape != k.shape or (k.size and k.shape[1] != q.shape[1]):
+        raise ValueError("q [t_q, n_state], k and v [t_kv, n_state]")
+    t_q, n_state = q.shape
+    out = np.empty((t_q, n_state), dtype=np.float32)
+    check(lib().rw_rocm_attention(q.ctypes.data, k.ctypes.data, v.ctypes.data, t_q, k.shape[0], n_state, n_head,
+                                  1 if causal else 0, out.ctypes.data))
+    return out
+
+
+def attention_workspace_size(t_q: int, t_kv: int, n_state: int) -> int:
+    return lib().rw_rocm_attention_workspace_size(t_q, t_kv, n_state)
+
+
+def attention_dev(q, k, v, t_q: int, t_kv: int, n_state: int, n_head: int, causal: bool, out,
+                  ldq: int | None = None, ldk: int | None = None, ldv: int | None = None, ldo: int | None = None,
+                  workspace=None, workspace_len: int = 0, stream: int | None = None) -> None:
+    """Device pointers (ints or torch tensors) with row strides in floats."""
+    check(lib().rw_rocm_attention_dev(_ptr(q), ldq or n_state, _ptr(k), ldk or n_state, _ptr(v), ldv or n_state,
+                                      t_q, t_kv, n_state, n_head, 1 if causal else 0, _ptr(out), ldo or n_state,
+                                      _ptr(workspace), workspace_len, stream))
 
 
 MODEL_PARSE_ONLY = 1

@@ -1,0 +1,306 @@
+// rw_attn.hpp -- multi-head attention on gfx950 (device code).
+//
+// out[t_q, n_state] = concat_h softmax(q_h k_h^T / sqrt(64) + mask) v_h, as
+// mha_split_kv (src/encoder.rs:48-80) computes it in f32.  Two launches:
+//
+//   k_attn_split_rows / k_attn_split_vt   q, k and v (f32) -> f16 pairs
+//        x = hi + lo (hi = f16(x), lo = f16(x - hi)), head-major planes:
+//        q, k  [head][t_pad][64]      (q pre-scaled by 1/8, exact)
+//        v^T   [head][64][t_kv_pad]   kv positions permuted in 16-blocks
+//   k_attn    one workgroup per (64 query rows, head), two wavefronts that
+//        split the kv blocks between them and meet in LDS at the end.
+//
+// Precision.  Every product runs on v_mfma_f32_32x32x16_f16 as three f16
+// products, hi*hi + hi*lo + lo*hi, accumulated in f32: each operand keeps
+// 22 of f32's 24 significant bits, and the dropped lo*lo term is below
+// 2^-22 of the product, so scores and outputs stay within a few f32
+// roundings of the reference's f32 arithmetic (values must stay below f16's
+// 65504 in magnitude; whisper's projections are far below it).  The softmax
+// is online (running maximum and sum per query row, rescaled per block) in
+// f32, which is the reference's max / exp / sum / divide reordered.
+//
+// Layouts inside k_attn.  The score block is computed transposed, S^T = K Q^T
+// (32 kv x 32 queries): lane (h, n) then holds 16 kv entries of query n, so a
+// query row's maximum and sum are in-lane plus one exchange with lane n+32.
+// The output is accumulated transposed as well, O^T = V^T P^T, so the
+// per-block rescale of a query column is one multiplier per lane.  P^T's
+// registers feed that MFMA's B operand directly: lane half h holds kv
+// 4h..4h+3 and 8+4h..8+4h+3 of each 16, and the v^T plane stores each
+// 16-block of kv positions in that order (attn_vpos).
+#pragma once
+#include <stdint.h>
+
+#include "rw_layout.hpp"
+
+namespace rw {
+
+constexpr int ATT_DH = 64;   // head size (every whisper model)
+constexpr int ATT_KVB = 32;  // kv rows per block
+constexpr int ATT_QT = 2;    // 32-query tiles per workgroup
+constexpr int ATT_QB = 32 * ATT_QT;
+
+// kv index (within a 16-block) stored at position p of the v^T plane: the
+// middle quads swap (an involution)
+RW_HD inline int attn_vpos(int p) {
+  const int qd = (p >> 2) & 3;
+  return qd == 1 ? p + 4 : qd == 2 ? p - 4 : p;
+}
+
+struct AttnPlanes {
+  const uint16_t *qh, *ql, *kh, *kl, *vh, *vl;
+  int tq_pad, tkv_pad;
+};
+
+#if defined(__HIPCC__)
+
+typedef _Float16 att_v8h __attribute__((ext_vector_type(8)));
+typedef float att_v16f __attribute__((ext_vector_type(16)));
+
+__device__ inline void att_split(float x, uint16_t &hi, uint16_t &lo) {
+  const _Float16 h = (_Float16)x;
+  const _Float16 l = (_Float16)(x - (float)h);
+  hi = __builtin_bit_cast(uint16_t, h);
+  lo = __builtin_bit_cast(uint16_t, l);
+}
+
+// q or k rows -> [head][t_pad][64] f16 pairs; rows >= t are zeros.  One
+// thread per 8 consecutive values of one row and head.
+__global__ __launch_bounds__(256) void k_attn_split_rows(const float *__restrict__ x, int ld, int t, int t_pad,
+                                                         int n_head, float scale, uint16_t *__restrict__ hi,
+                                                         uint16_t *__restrict__ lo) {
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t total = (size_t)n_head * t_pad * 8;
+  if (idx >= total) return;
+  const int c = (int)(idx & 7);
+  const size_t hr = idx >> 3;  // head * t_pad + row
+  const int row = (int)(hr % t_pad), head = (int)(hr / t_pad);
+  float v[8];
+  if (row < t) {
+    const float4 *src = reinterpret_cast<const float4 *>(x + (size_t)row * ld + head * ATT_DH + c * 8);
+    const float4 a = src[0], b = src[1];
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+  }
+  uint16_t h8[8], l8[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) att_split(v[e] * scale, h8[e], l8[e]);
+  const size_t o = hr * ATT_DH + c * 8;
+  *reinterpret_cast<uint4 *>(hi + o) = *reinterpret_cast<const uint4 *>(h8);
+  *reinterpret_cast<uint4 *>(lo + o) = *reinterpret_cast<const uint4 *>(l8);
+}
+
+// v -> v^T [head][64][t_pad] f16 pairs, kv positions permuted by attn_vpos
+// within each 16-block; kv >= t are zeros.  One thread per (head, 8
+// positions, d): a wavefront reads 64 consecutive d of one kv row.
+__global__ __launch_bounds__(256) void k_attn_split_vt(const float *__restrict__ v, int ld, int t, int t_pad,
+                                                       int n_head, uint16_t *__restrict__ hi,
+                                                       uint16_t *__restrict__ lo) {
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const int nc = t_pad / 8;
+  const size_t total = (size_t)n_head * nc * ATT_DH;
+  if (idx >= total) return;
+  const int d = (int)(idx % ATT_DH);
+  const size_t hc = idx / ATT_DH;
+  const int c = (int)(hc % nc), head = (int)(hc / nc);
+  uint16_t h8[8], l8[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int p = c * 8 + e;
+    const int kv = (p & ~15) | attn_vpos(p & 15);
+    const float x = kv < t ? v[(size_t)kv * ld + head * ATT_DH + d] : 0.0f;
+    att_split(x, h8[e], l8[e]);
+  }
+  const size_t o = ((size_t)head * ATT_DH + d) * t_pad + c * 8;
+  *reinterpret_cast<uint4 *>(hi + o) = *reinterpret_cast<const uint4 *>(h8);
+  *reinterpret_cast<uint4 *>(lo + o) = *reinterpret_cast<const uint4 *>(l8);
+}
+
+// out rows [0, t) x columns [0, cols) = 0 (attention over no keys)
+__global__ __launch_bounds__(256) void k_attn_zero(float *__restrict__ out, int ld, int t, int cols) {
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx < (size_t)t * cols) out[(idx / cols) * ld + idx % cols] = 0.0f;
+}
+
+__device__ inline att_v8h att_ld(const uint16_t *p) {
+  return __builtin_bit_cast(att_v8h, *reinterpret_cast<const uint4 *>(p));
+}
+
+__device__ inline att_v16f att_mma3(att_v8h ah, att_v8h al, att_v8h bh, att_v8h bl, att_v16f c) {
+  c = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl, c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, c, 0, 0, 0);
+  return c;
+}
+
+// One kv block's operands for one wavefront: K rows as the A operand of S^T
+// (4 steps of 16 of the head's 64 values), v^T rows as the A operand of O^T
+// (2 row tiles of 32 values x 2 steps of 16 kv).
+struct AttKV {
+  att_v8h kh[4], kl[4];
+  att_v8h vh[2][2], vl[2][2];
+};
+
+__device__ inline void att_load_kv(const AttnPlanes &P, int head, int blk, int h, int n, AttKV &o) {
+  const size_t krow = ((size_t)head * P.tkv_pad + (size_t)blk * ATT_KVB + n) * ATT_DH + 8 * h;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    o.kh[s] = att_ld(P.kh + krow + 16 * s);
+    o.kl[s] = att_ld(P.kl + krow + 16 * s);
+  }
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt) {
+    const size_t vrow = ((size_t)head * ATT_DH + dt * 32 + n) * P.tkv_pad + (size_t)blk * ATT_KVB + 8 * h;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      o.vh[dt][s] = att_ld(P.vh + vrow + 16 * s);
+      o.vl[dt][s] = att_ld(P.vl + vrow + 16 * s);
+    }
+  }
+}
+
+// Workgroup (blockIdx.x, blockIdx.y) = (64 query rows from q0, head).
+// Wavefront w takes kv blocks w, w + 2, ...; a causal query row i (at
+// absolute position t_kv - t_q + i) sees kv rows up to its position.
+__global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, int causal,
+                                              float *__restrict__ out, int ld_out) {
+  constexpr float LOG2E = 1.4426950408889634f;
+  constexpr float NEG_INF = -__builtin_huge_valf();
+  __shared__ __align__(16) float xo[ATT_QB * (ATT_DH + 4)];  // partial O^T exchange, then the output tile
+  __shared__ float xm[ATT_QT * 64], xl[ATT_QT * 64];
+  const int l = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int h = l >> 5, n = l & 31;
+  const int head = blockIdx.y, q0 = blockIdx.x * ATT_QB;
+  const int off = t_kv - t_q;  // absolute position of query row 0
+  const int kv_end = causal ? min(t_kv, off + q0 + ATT_QB) : t_kv;
+  const int nblk = (kv_end + ATT_KVB - 1) / ATT_KVB;
+
+  att_v8h qh[ATT_QT][4], ql[ATT_QT][4];
+#pragma unroll
+  for (int qt = 0; qt < ATT_QT; ++qt) {
+    const size_t qrow = ((size_t)head * P.tq_pad + q0 + qt * 32 + n) * ATT_DH + 8 * h;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      qh[qt][s] = att_ld(P.qh + qrow + 16 * s);
+      ql[qt][s] = att_ld(P.ql + qrow + 16 * s);
+    }
+  }
+  att_v16f o[ATT_QT][2];
+  float m[ATT_QT], lsum[ATT_QT];
+#pragma unroll
+  for (int qt = 0; qt < ATT_QT; ++qt) {
+    o[qt][0] = (att_v16f){};
+    o[qt][1] = (att_v16f){};
+    m[qt] = NEG_INF;
+    lsum[qt] = 0.0f;
+  }
+
+  AttKV cur, nxt;
+  if (wv < nblk) att_load_kv(P, head, wv, h, n, cur);
+  for (int b = wv; b < nblk; b += 2) {
+    if (b + 2 < nblk) att_load_kv(P, head, b + 2, h, n, nxt);  // next block in flight
+#pragma unroll
+    for (int qt = 0; qt < ATT_QT; ++qt) {
+      att_v16f s = (att_v16f){};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) s = att_mma3(cur.kh[k], cur.kl[k], qh[qt][k], ql[qt][k], s);
+      // lane (h, n): s[i] = score of query q0 + 32 qt + n against kv row
+      // 32 b + 8 (i / 4) + 4 h + i % 4
+      const int tq0 = q0 + qt * 32;
+      const bool partial = (b + 1) * ATT_KVB > t_kv || (causal && (b + 1) * ATT_KVB - 1 > off + tq0);
+      if (partial) {
+        const int qpos = off + tq0 + n;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kv = b * ATT_KVB + 8 * (i >> 2) + 4 * h + (i & 3);
+          if (kv >= t_kv || (causal && kv > qpos)) s[i] = NEG_INF;
+        }
+      }
+      float mx = s[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mnew = fmaxf(m[qt], mx);
+      const float mu = mnew == NEG_INF ? 0.0f : mnew;  // a column with nothing visible yet
+      const float alpha = __builtin_amdgcn_exp2f((m[qt] - mu) * LOG2E);
+      m[qt] = mnew;
+      float ps = 0.0f;
+      att_v8h ph[2], pl[2];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float p = __builtin_amdgcn_exp2f((s[i] - mu) * LOG2E);
+        ps += p;
+        const _Float16 ph1 = (_Float16)p;
+        ph[i >> 3][i & 7] = ph1;
+        pl[i >> 3][i & 7] = (_Float16)(p - (float)ph1);
+      }
+      lsum[qt] = lsum[qt] * alpha + ps;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        o[qt][dt] *= alpha;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) o[qt][dt] = att_mma3(cur.vh[dt][k], cur.vl[dt][k], ph[k], pl[k], o[qt][dt]);
+      }
+    }
+    cur = nxt;
+  }
+
+  // wavefront 1 hands its partial state to wavefront 0
+  if (wv == 1) {
+#pragma unroll
+    for (int qt = 0; qt < ATT_QT; ++qt) {
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) xo[((qt * 2 + dt) * 16 + i) * 64 + l] = o[qt][dt][i];
+      xm[qt * 64 + l] = m[qt];
+      xl[qt * 64 + l] = lsum[qt];
+    }
+  }
+  __syncthreads();
+  if (wv == 0) {
+#pragma unroll
+    for (int qt = 0; qt < ATT_QT; ++qt) {
+      const float m1 = xm[qt * 64 + l], l1 = xl[qt * 64 + l];
+      const float mm = fmaxf(m[qt], m1);
+      const float mu = mm == NEG_INF ? 0.0f : mm;
+      const float s0 = __builtin_amdgcn_exp2f((m[qt] - mu) * LOG2E), s1 = __builtin_amdgcn_exp2f((m1 - mu) * LOG2E);
+      float lt = lsum[qt] * s0 + l1 * s1;
+      lt += __shfl_xor(lt, 32);
+      const float inv = 1.0f / lt;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          o[qt][dt][i] = (o[qt][dt][i] * s0 + xo[((qt * 2 + dt) * 16 + i) * 64 + l] * s1) * inv;
+    }
+  }
+  __syncthreads();
+  // the output tile [64 queries][64 d] through LDS, then row-contiguous stores
+  constexpr int LD = ATT_DH + 4;
+  if (wv == 0) {
+#pragma unroll
+    for (int qt = 0; qt < ATT_QT; ++qt)
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<float4 *>(&xo[(qt * 32 + n) * LD + dt * 32 + 8 * g + 4 * h]) =
+              make_float4(o[qt][dt][4 * g], o[qt][dt][4 * g + 1], o[qt][dt][4 * g + 2], o[qt][dt][4 * g + 3]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < ATT_QB * 16 / 128; ++it) {
+    const int c = it * 128 + (int)threadIdx.x;
+    const int row = c >> 4, c4 = c & 15;
+    if (q0 + row < t_q)
+      *reinterpret_cast<float4 *>(out + (size_t)(q0 + row) * ld_out + head * ATT_DH + 4 * c4) =
+          *reinterpret_cast<const float4 *>(&xo[row * LD + 4 * c4]);
+  }
+}
+
+#endif  // __HIPCC__
+
+}  // namespace rw

@@ -26,6 +26,7 @@
 #include <tuple>
 #include <vector>
 
+#include "rw_attn.hpp"
 #include "rw_kernels.hpp"
 #include "rw_rocm.h"
 
@@ -653,6 +654,79 @@ static int check_matmul_args(const rw_weight *w, const void *a, size_t m, size_t
 
 // --------------------------------------------------------------- ABI
 
+// ------------------------------------------------------ attention
+
+// Workspace of one attention call: the f16 pairs of q, k and v^T.
+struct AttnLayout {
+  int n_head, tq_pad, tkv_pad;
+  size_t off_qh, off_ql, off_kh, off_kl, off_vh, off_vl, bytes;
+};
+
+static AttnLayout attn_layout(size_t t_q, size_t t_kv, size_t n_state) {
+  AttnLayout L{};
+  L.n_head = (int)(n_state / ATT_DH);
+  L.tq_pad = (int)align_up(t_q, ATT_QB);
+  L.tkv_pad = (int)align_up(t_kv, ATT_KVB);
+  const size_t qb = (size_t)L.n_head * L.tq_pad * ATT_DH * 2, kb = (size_t)L.n_head * L.tkv_pad * ATT_DH * 2;
+  L.off_qh = 0;
+  L.off_ql = align_up(L.off_qh + qb, 256);
+  L.off_kh = align_up(L.off_ql + qb, 256);
+  L.off_kl = align_up(L.off_kh + kb, 256);
+  L.off_vh = align_up(L.off_kl + kb, 256);
+  L.off_vl = align_up(L.off_vh + kb, 256);
+  L.bytes = align_up(L.off_vl + kb, 256);
+  return L;
+}
+
+// The reference's conditions (src/encoder.rs:48-58, 109-119) plus this
+// kernel's: 64-value heads, 16-byte aligned rows.
+static int check_attn_args(const float *q, size_t ldq, const float *k, size_t ldk, const float *v, size_t ldv,
+                           size_t t_q, size_t t_kv, size_t n_state, int n_head, int causal, const float *out,
+                           size_t ldo) {
+  if (n_head <= 0 || n_state == 0 || n_state % (size_t)n_head)
+    return fail(RW_EINVAL, "n_state %zu is not a positive multiple of n_head %d", n_state, n_head);
+  if (n_state / (size_t)n_head != ATT_DH)
+    return fail(RW_EINVAL, "head size %zu unsupported (the kernel takes %d)", n_state / (size_t)n_head, ATT_DH);
+  if (causal && t_q > t_kv) return fail(RW_EINVAL, "causal attention needs t_q <= t_kv (%zu > %zu)", t_q, t_kv);
+  if (t_q > (1u << 24) || t_kv > (1u << 24)) return fail(RW_EINVAL, "sequence too long");
+  if (t_q == 0) return RW_OK;
+  if (!q || !out || (t_kv && (!k || !v))) return fail(RW_EINVAL, "q, k, v or out is NULL");
+  if (ldq < n_state || ldk < n_state || ldv < n_state || ldo < n_state)
+    return fail(RW_EINVAL, "a row stride is smaller than n_state");
+  if (ldq % 4 || ldk % 4 || ldo % 4 || ((uintptr_t)q | (uintptr_t)k | (uintptr_t)out) % 16)
+    return fail(RW_EINVAL, "q, k and out rows must be 16-byte aligned");
+  return RW_OK;
+}
+
+static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk, const float *v, size_t ldv,
+                         size_t t_q, size_t t_kv, int n_head, int causal, float *out, size_t ldo, const AttnLayout &L,
+                         void *ws, hipStream_t s) {
+  char *b = (char *)ws;
+  uint16_t *qh = (uint16_t *)(b + L.off_qh), *ql = (uint16_t *)(b + L.off_ql);
+  uint16_t *kh = (uint16_t *)(b + L.off_kh), *kl = (uint16_t *)(b + L.off_kl);
+  uint16_t *vh = (uint16_t *)(b + L.off_vh), *vl = (uint16_t *)(b + L.off_vl);
+  if (t_kv == 0) {  // no keys: every output row is the empty sum
+    const size_t nz = t_q * (size_t)n_head * ATT_DH;
+    hipLaunchKernelGGL(k_attn_zero, dim3((unsigned)cdiv(nz, 256)), dim3(256), 0, s, out, (int)ldo, (int)t_q,
+                       n_head * ATT_DH);
+    LAUNCH_TRY("k_attn_zero");
+    return RW_OK;
+  }
+  const size_t nq = (size_t)n_head * L.tq_pad * 8, nk = (size_t)n_head * L.tkv_pad * 8;
+  hipLaunchKernelGGL(k_attn_split_rows, dim3((unsigned)cdiv(nq, 256)), dim3(256), 0, s, q, (int)ldq, (int)t_q,
+                     L.tq_pad, n_head, 0.125f, qh, ql);
+  hipLaunchKernelGGL(k_attn_split_rows, dim3((unsigned)cdiv(nk, 256)), dim3(256), 0, s, k, (int)ldk, (int)t_kv,
+                     L.tkv_pad, n_head, 1.0f, kh, kl);
+  hipLaunchKernelGGL(k_attn_split_vt, dim3((unsigned)cdiv(nk, 256)), dim3(256), 0, s, v, (int)ldv, (int)t_kv,
+                     L.tkv_pad, n_head, vh, vl);
+  LAUNCH_TRY("k_attn_split");
+  const AttnPlanes P{qh, ql, kh, kl, vh, vl, L.tq_pad, L.tkv_pad};
+  hipLaunchKernelGGL(k_attn, dim3((unsigned)(L.tq_pad / ATT_QB), (unsigned)n_head), dim3(128), 0, s, P, (int)t_q,
+                     (int)t_kv, causal ? 1 : 0, out, (int)ldo);
+  LAUNCH_TRY("k_attn");
+  return RW_OK;
+}
+
 extern "C" {
 
 int rw_rocm_version(void) { return 0x000100; }
@@ -1099,6 +1173,66 @@ int rw_rocm_block_dots(const rw_weight *w, const int8_t *qa, size_t m, int32_t *
   LAUNCH_TRY("k_block_dots");
   HIP_TRY(hipMemcpyAsync(S, b + off_s, sbytes, hipMemcpyDeviceToHost, g.c->stream));
   HIP_TRY(hipStreamSynchronize(g.c->stream));
+  return RW_OK;
+}
+
+size_t rw_rocm_attention_workspace_size(size_t t_q, size_t t_kv, size_t n_state) {
+  return attn_layout(t_q, t_kv, n_state).bytes;
+}
+
+int rw_rocm_attention_dev(const float *q, size_t ldq, const float *k, size_t ldk, const float *v, size_t ldv,
+                          size_t t_q, size_t t_kv, size_t n_state, int n_head, int causal, float *out, size_t ldo,
+                          void *workspace, size_t workspace_len, void *stream) {
+  int rc = check_attn_args(q, ldq, k, ldk, v, ldv, t_q, t_kv, n_state, n_head, causal, out, ldo);
+  if (rc) return rc;
+  if (t_q == 0) return RW_OK;
+  int dev;
+  rc = current_device(&dev);
+  if (rc) return rc;
+  const AttnLayout L = attn_layout(t_q, t_kv, n_state);
+  void *ws = workspace;
+  if (ws) {
+    if (workspace_len < L.bytes) return fail(RW_EINVAL, "workspace of %zu bytes < %zu needed", workspace_len, L.bytes);
+  } else {
+    rc = stream_workspace(dev, stream, L.bytes, &ws);
+    if (rc) return rc;
+  }
+  return run_attention(q, ldq, k, ldk, v, ldv, t_q, t_kv, n_head, causal, out, ldo, L, ws, (hipStream_t)stream);
+}
+
+int rw_rocm_attention(const float *q, const float *k, const float *v, size_t t_q, size_t t_kv, size_t n_state,
+                      int n_head, int causal, float *out) {
+  int rc = check_attn_args(q, n_state, k, n_state, v, n_state, t_q, t_kv, n_state, n_head, causal, out, n_state);
+  if (rc) return rc;
+  if (t_q == 0) return RW_OK;
+  int dev;
+  rc = current_device(&dev);
+  if (rc) return rc;
+  CtxGuard g;
+  rc = ctx_acquire(dev, &g.c);
+  if (rc) return rc;
+  Ctx *c = g.c;
+  const AttnLayout L = attn_layout(t_q, t_kv, n_state);
+  const size_t off_q = align_up(L.bytes, 256);
+  const size_t off_k = align_up(off_q + t_q * n_state * 4, 256);
+  const size_t off_v = align_up(off_k + t_kv * n_state * 4, 256);
+  const size_t off_o = align_up(off_v + t_kv * n_state * 4, 256);
+  rc = ctx_reserve(c, align_up(off_o + t_q * n_state * 4, 256));
+  if (rc) return rc;
+  char *b = (char *)c->buf;
+  float *dq = (float *)(b + off_q), *dk = (float *)(b + off_k), *dv = (float *)(b + off_v), *dout = (float *)(b + off_o);
+  HIP_TRY(hipMemcpyAsync(dq, q, t_q * n_state * 4, hipMemcpyHostToDevice, c->stream));
+  if (t_kv) {
+    HIP_TRY(hipMemcpyAsync(dk, k, t_kv * n_state * 4, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(hipMemcpyAsync(dv, v, t_kv * n_state * 4, hipMemcpyHostToDevice, c->stream));
+  }
+  rc = run_attention(dq, n_state, dk, n_state, dv, n_state, t_q, t_kv, n_head, causal, dout, n_state, L, b, c->stream);
+  if (rc) {
+    (void)hipStreamSynchronize(c->stream);
+    return rc;
+  }
+  HIP_TRY(hipMemcpyAsync(out, dout, t_q * n_state * 4, hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
   return RW_OK;
 }
 
