@@ -238,6 +238,36 @@ def time_decode(A, torch, D, steps: int, warmup: int, stream):
     return t_group, t_call
 
 
+def time_attention(A, torch, stream, steps: int, warmup: int, t: int = 1500, n_state: int = 1280, n_head: int = 20):
+    """One encoder layer's self-attention (large-v3: 20 heads of 64 over 1500
+    positions) through rw_rocm_attention_dev on resident q, k, v: ms per
+    call (the three split launches and k_attn) and the algorithmic flops
+    (2 t^2 dh per head for Q K^T, the same for P V)."""
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(11)
+    q, k, v = (torch.randn(t, n_state, device="cuda:0", generator=g) for _ in range(3))
+    out = torch.empty(t, n_state, device="cuda:0")
+    wsz = A.attention_workspace_size(t, t, n_state)
+    ws = torch.empty(wsz, dtype=torch.uint8, device="cuda:0")
+
+    def call():
+        A.attention_dev(q, k, v, t, t, n_state, n_head, False, out, workspace=ws, workspace_len=wsz, stream=stream)
+
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = 4 * t * t * (n_state // n_head) * n_head
+    return ms, flops
+
+
 def time_model_load(A, synth, dtype: int, path: str, reps: int = 2):
     """rw_rocm_model_load on a ggml .bin holding large-v3's quantized matrices
     (32 encoder layers x 6 linears, 32 decoder layers x 10, the token
@@ -332,6 +362,7 @@ def main() -> int:
     ap.add_argument("--decode-m", type=int, default=5)
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-attention", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--load-model", default="",
                     help="also time the model loader on a large-v3-shaped ggml file written to this path")
@@ -438,6 +469,19 @@ def main() -> int:
         }
         del D
         torch.cuda.empty_cache()
+
+    if not args.no_attention:
+        ams, aflops = time_attention(A, torch, stream, max(5, args.steps), 2)
+        atf = aflops / (ams * 1e-3) / 1e12
+        log(f"encoder self-attention {ams * 1e3:.1f} us per layer ({atf:.1f} TFLOP/s algorithmic)")
+        result["attention"] = {
+            "workload": "large-v3 encoder self-attention, one layer: 20 heads x 64, 1500 positions, f32 in/out",
+            "us_per_layer": round(ams * 1e3, 2),
+            "flops": aflops,
+            "TFLOP_per_s": round(atf, 2),
+            "launch": "rw_rocm_attention_dev: three split launches (q, k, v to f16 hi/lo planes) and one k_attn",
+            "note": "algorithmic flops 4*t^2*64 per head; each product runs as three f16 MFMA products",
+        }
 
     if args.load_model:
         lq = synth.BY_NAME[args.decode_quant]

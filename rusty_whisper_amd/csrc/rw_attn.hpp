@@ -3,7 +3,7 @@
 // out[t_q, n_state] = concat_h softmax(q_h k_h^T / sqrt(64) + mask) v_h, as
 // mha_split_kv (src/encoder.rs:48-80) computes it in f32.  Two launches:
 //
-//   k_attn_split_rows / k_attn_split_vt   q, k and v (f32) -> f16 pairs
+//   k_attn_split   q, k and v (f32) -> f16 pairs, one launch
 //        x = hi + lo (hi = f16(x), lo = f16(x - hi)), head-major planes:
 //        q, k  [head][t_pad][64]      (q pre-scaled by 1/8, exact)
 //        v^T   [head][64][t_kv_pad]   kv positions permuted in 16-blocks
@@ -12,12 +12,14 @@
 //
 // Precision.  Every product runs on v_mfma_f32_32x32x16_f16 as three f16
 // products, hi*hi + hi*lo + lo*hi, accumulated in f32: each operand keeps
-// 22 of f32's 24 significant bits, and the dropped lo*lo term is below
-// 2^-22 of the product, so scores and outputs stay within a few f32
-// roundings of the reference's f32 arithmetic (values must stay below f16's
-// 65504 in magnitude; whisper's projections are far below it).  The softmax
-// is online (running maximum and sum per query row, rescaled per block) in
-// f32, which is the reference's max / exp / sum / divide reordered.
+// 22 of f32's 24 significant bits and the dropped lo*lo term is below 2^-22
+// of the product, so outputs stay within about 1e-6 (relative to the row) of
+// the exact result, like the reference's f32 arithmetic.  Probabilities
+// enter as 2^12 p so that small ones keep their f16 bits.  Inputs must stay
+// below f16's 65504 in magnitude (whisper's projections are far below it);
+// inputs below about 1e-3 lose a few bits to f16 subnormal residuals.  The
+// softmax is online (running maximum and sum per query row, rescaled per
+// block) in f32, which is the reference's max / exp / sum / divide reordered.
 //
 // Layouts inside k_attn.  The score block is computed transposed, S^T = K Q^T
 // (32 kv x 32 queries): lane (h, n) then holds 16 kv entries of query n, so a
@@ -56,6 +58,8 @@ struct AttnPlanes {
 typedef _Float16 att_v8h __attribute__((ext_vector_type(8)));
 typedef float att_v16f __attribute__((ext_vector_type(16)));
 
+// x = hi + lo, both f16
+constexpr float ATT_PS = 4096.0f;
 __device__ inline void att_split(float x, uint16_t &hi, uint16_t &lo) {
   const _Float16 h = (_Float16)x;
   const _Float16 l = (_Float16)(x - (float)h);
@@ -63,14 +67,10 @@ __device__ inline void att_split(float x, uint16_t &hi, uint16_t &lo) {
   lo = __builtin_bit_cast(uint16_t, l);
 }
 
-// q or k rows -> [head][t_pad][64] f16 pairs; rows >= t are zeros.  One
-// thread per 8 consecutive values of one row and head.
-__global__ __launch_bounds__(256) void k_attn_split_rows(const float *__restrict__ x, int ld, int t, int t_pad,
-                                                         int n_head, float scale, uint16_t *__restrict__ hi,
-                                                         uint16_t *__restrict__ lo) {
-  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-  const size_t total = (size_t)n_head * t_pad * 8;
-  if (idx >= total) return;
+// q or k rows -> [head][t_pad][64] f16 pairs; rows >= t are zeros.  Item
+// idx covers 8 consecutive values of one row and head.
+__device__ inline void att_split_rows(size_t idx, const float *__restrict__ x, int ld, int t, int t_pad,
+                                      float scale, uint16_t *__restrict__ hi, uint16_t *__restrict__ lo) {
   const int c = (int)(idx & 7);
   const size_t hr = idx >> 3;  // head * t_pad + row
   const int row = (int)(hr % t_pad), head = (int)(hr / t_pad);
@@ -92,15 +92,11 @@ __global__ __launch_bounds__(256) void k_attn_split_rows(const float *__restrict
 }
 
 // v -> v^T [head][64][t_pad] f16 pairs, kv positions permuted by attn_vpos
-// within each 16-block; kv >= t are zeros.  One thread per (head, 8
+// within each 16-block; kv >= t are zeros.  Item idx covers (head, 8
 // positions, d): a wavefront reads 64 consecutive d of one kv row.
-__global__ __launch_bounds__(256) void k_attn_split_vt(const float *__restrict__ v, int ld, int t, int t_pad,
-                                                       int n_head, uint16_t *__restrict__ hi,
-                                                       uint16_t *__restrict__ lo) {
-  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+__device__ inline void att_split_vt(size_t idx, const float *__restrict__ v, int ld, int t, int t_pad,
+                                    uint16_t *__restrict__ hi, uint16_t *__restrict__ lo) {
   const int nc = t_pad / 8;
-  const size_t total = (size_t)n_head * nc * ATT_DH;
-  if (idx >= total) return;
   const int d = (int)(idx % ATT_DH);
   const size_t hc = idx / ATT_DH;
   const int c = (int)(hc % nc), head = (int)(hc / nc);
@@ -117,6 +113,27 @@ __global__ __launch_bounds__(256) void k_attn_split_vt(const float *__restrict__
   *reinterpret_cast<uint4 *>(lo + o) = *reinterpret_cast<const uint4 *>(l8);
 }
 
+// All three splits in one launch: workgroups [0, wq) split q (scaled by
+// 1/8, exact), [wq, wq + wk) split k, the rest split v into v^T.
+__global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ q, int ldq, int t_q,
+                                                    const float *__restrict__ k, int ldk, const float *__restrict__ v,
+                                                    int ldv, int t_kv, AttnPlanes P, int n_head, int wq, int wk) {
+  const int bx = blockIdx.x;
+  if (bx < wq) {
+    const size_t idx = (size_t)bx * 256 + threadIdx.x;
+    if (idx < (size_t)n_head * P.tq_pad * 8)
+      att_split_rows(idx, q, ldq, t_q, P.tq_pad, 0.125f, const_cast<uint16_t *>(P.qh), const_cast<uint16_t *>(P.ql));
+  } else if (bx < wq + wk) {
+    const size_t idx = (size_t)(bx - wq) * 256 + threadIdx.x;
+    if (idx < (size_t)n_head * P.tkv_pad * 8)
+      att_split_rows(idx, k, ldk, t_kv, P.tkv_pad, 1.0f, const_cast<uint16_t *>(P.kh), const_cast<uint16_t *>(P.kl));
+  } else {
+    const size_t idx = (size_t)(bx - wq - wk) * 256 + threadIdx.x;
+    if (idx < (size_t)n_head * (P.tkv_pad / 8) * ATT_DH)
+      att_split_vt(idx, v, ldv, t_kv, P.tkv_pad, const_cast<uint16_t *>(P.vh), const_cast<uint16_t *>(P.vl));
+  }
+}
+
 // out rows [0, t) x columns [0, cols) = 0 (attention over no keys)
 __global__ __launch_bounds__(256) void k_attn_zero(float *__restrict__ out, int ld, int t, int cols) {
   const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -127,28 +144,33 @@ __device__ inline att_v8h att_ld(const uint16_t *p) {
   return __builtin_bit_cast(att_v8h, *reinterpret_cast<const uint4 *>(p));
 }
 
-__device__ inline att_v16f att_mma3(att_v8h ah, att_v8h al, att_v8h bh, att_v8h bl, att_v16f c) {
+// c += ah bh + ah bl + al bh
+__device__ inline void att_mma3(att_v8h ah, att_v8h al, att_v8h bh, att_v8h bl, att_v16f &c) {
   c = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, c, 0, 0, 0);
   c = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl, c, 0, 0, 0);
   c = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, c, 0, 0, 0);
-  return c;
 }
 
 // One kv block's operands for one wavefront: K rows as the A operand of S^T
 // (4 steps of 16 of the head's 64 values), v^T rows as the A operand of O^T
 // (2 row tiles of 32 values x 2 steps of 16 kv).
-struct AttKV {
+struct AttK {
   att_v8h kh[4], kl[4];
+};
+struct AttV {
   att_v8h vh[2][2], vl[2][2];
 };
 
-__device__ inline void att_load_kv(const AttnPlanes &P, int head, int blk, int h, int n, AttKV &o) {
+__device__ inline void att_load_k(const AttnPlanes &P, int head, int blk, int h, int n, AttK &o) {
   const size_t krow = ((size_t)head * P.tkv_pad + (size_t)blk * ATT_KVB + n) * ATT_DH + 8 * h;
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     o.kh[s] = att_ld(P.kh + krow + 16 * s);
     o.kl[s] = att_ld(P.kl + krow + 16 * s);
   }
+}
+
+__device__ inline void att_load_v(const AttnPlanes &P, int head, int blk, int h, int n, AttV &o) {
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt) {
     const size_t vrow = ((size_t)head * ATT_DH + dt * 32 + n) * P.tkv_pad + (size_t)blk * ATT_KVB + 8 * h;
@@ -160,7 +182,7 @@ __device__ inline void att_load_kv(const AttnPlanes &P, int head, int blk, int h
   }
 }
 
-// Workgroup (blockIdx.x, blockIdx.y) = (64 query rows from q0, head).
+// Workgroup (blockIdx.x, blockIdx.y) = (ATT_QB query rows from q0, head).
 // Wavefront w takes kv blocks w, w + 2, ...; a causal query row i (at
 // absolute position t_kv - t_q + i) sees kv rows up to its position.
 __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, int causal,
@@ -187,7 +209,7 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
       ql[qt][s] = att_ld(P.ql + qrow + 16 * s);
     }
   }
-  att_v16f o[ATT_QT][2];
+  att_v16f o[ATT_QT][2];  // O^T
   float m[ATT_QT], lsum[ATT_QT];
 #pragma unroll
   for (int qt = 0; qt < ATT_QT; ++qt) {
@@ -197,17 +219,27 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
     lsum[qt] = 0.0f;
   }
 
-  AttKV cur, nxt;
-  if (wv < nblk) att_load_kv(P, head, wv, h, n, cur);
+  // K one block ahead; V is loaded at the top of its block and first used
+  // after the scores and the softmax
+  AttK cur, nxt;
+  AttV vb;
+  if (wv < nblk) att_load_k(P, head, wv, h, n, cur);
   for (int b = wv; b < nblk; b += 2) {
-    if (b + 2 < nblk) att_load_kv(P, head, b + 2, h, n, nxt);  // next block in flight
+    att_load_v(P, head, b, h, n, vb);
+    if (b + 2 < nblk) att_load_k(P, head, b + 2, h, n, nxt);
+    // both query tiles' scores first, so the softmax of one tile can run on
+    // the VALU while the matrix cores work on the other
+    att_v16f s[ATT_QT];
 #pragma unroll
     for (int qt = 0; qt < ATT_QT; ++qt) {
-      att_v16f s = (att_v16f){};
+      s[qt] = (att_v16f){};
 #pragma unroll
-      for (int k = 0; k < 4; ++k) s = att_mma3(cur.kh[k], cur.kl[k], qh[qt][k], ql[qt][k], s);
-      // lane (h, n): s[i] = score of query q0 + 32 qt + n against kv row
-      // 32 b + 8 (i / 4) + 4 h + i % 4
+      for (int k = 0; k < 4; ++k) att_mma3(cur.kh[k], cur.kl[k], qh[qt][k], ql[qt][k], s[qt]);
+    }
+#pragma unroll
+    for (int qt = 0; qt < ATT_QT; ++qt) {
+      // lane (h, n): s[qt][i] = score of query q0 + 32 qt + n against kv
+      // row 32 b + 8 (i / 4) + 4 h + i % 4
       const int tq0 = q0 + qt * 32;
       const bool partial = (b + 1) * ATT_KVB > t_kv || (causal && (b + 1) * ATT_KVB - 1 > off + tq0);
       if (partial) {
@@ -215,34 +247,42 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int kv = b * ATT_KVB + 8 * (i >> 2) + 4 * h + (i & 3);
-          if (kv >= t_kv || (causal && kv > qpos)) s[i] = NEG_INF;
+          if (kv >= t_kv || (causal && kv > qpos)) s[qt][i] = NEG_INF;
         }
       }
-      float mx = s[0];
+      float mx = s[qt][0];
 #pragma unroll
-      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
+      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[qt][i]);
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float mnew = fmaxf(m[qt], mx);
       const float mu = mnew == NEG_INF ? 0.0f : mnew;  // a column with nothing visible yet
-      const float alpha = __builtin_amdgcn_exp2f((m[qt] - mu) * LOG2E);
-      m[qt] = mnew;
       float ps = 0.0f;
       att_v8h ph[2], pl[2];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float p = __builtin_amdgcn_exp2f((s[i] - mu) * LOG2E);
+        const float p = __builtin_amdgcn_exp2f((s[qt][i] - mu) * LOG2E);
         ps += p;
-        const _Float16 ph1 = (_Float16)p;
+        // P enters the products as 2^12 p, so that small probabilities keep
+        // their f16 bits; the output is divided by 2^12 lsum at the end
+        const float p12 = p * ATT_PS;
+        const _Float16 ph1 = (_Float16)p12;
         ph[i >> 3][i & 7] = ph1;
-        pl[i >> 3][i & 7] = (_Float16)(p - (float)ph1);
+        pl[i >> 3][i & 7] = (_Float16)(p12 - (float)ph1);
       }
-      lsum[qt] = lsum[qt] * alpha + ps;
+      // rescale only when some column's maximum moved (rare after the
+      // first blocks)
+      if (__builtin_amdgcn_ballot_w64(mnew != m[qt])) {
+        const float alpha = __builtin_amdgcn_exp2f((m[qt] - mu) * LOG2E);
+        lsum[qt] *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt) {
-        o[qt][dt] *= alpha;
-#pragma unroll
-        for (int k = 0; k < 2; ++k) o[qt][dt] = att_mma3(cur.vh[dt][k], cur.vl[dt][k], ph[k], pl[k], o[qt][dt]);
+        for (int dt = 0; dt < 2; ++dt) o[qt][dt] *= alpha;
       }
+      m[qt] = mnew;
+      lsum[qt] += ps;
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int k = 0; k < 2; ++k) att_mma3(vb.vh[dt][k], vb.vl[dt][k], ph[k], pl[k], o[qt][dt]);
     }
     cur = nxt;
   }
@@ -269,7 +309,7 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
       const float s0 = __builtin_amdgcn_exp2f((m[qt] - mu) * LOG2E), s1 = __builtin_amdgcn_exp2f((m1 - mu) * LOG2E);
       float lt = lsum[qt] * s0 + l1 * s1;
       lt += __shfl_xor(lt, 32);
-      const float inv = 1.0f / lt;
+      const float inv = 1.0f / (lt * ATT_PS);
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
 #pragma unroll

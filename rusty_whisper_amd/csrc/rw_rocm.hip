@@ -712,15 +712,12 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
     LAUNCH_TRY("k_attn_zero");
     return RW_OK;
   }
-  const size_t nq = (size_t)n_head * L.tq_pad * 8, nk = (size_t)n_head * L.tkv_pad * 8;
-  hipLaunchKernelGGL(k_attn_split_rows, dim3((unsigned)cdiv(nq, 256)), dim3(256), 0, s, q, (int)ldq, (int)t_q,
-                     L.tq_pad, n_head, 0.125f, qh, ql);
-  hipLaunchKernelGGL(k_attn_split_rows, dim3((unsigned)cdiv(nk, 256)), dim3(256), 0, s, k, (int)ldk, (int)t_kv,
-                     L.tkv_pad, n_head, 1.0f, kh, kl);
-  hipLaunchKernelGGL(k_attn_split_vt, dim3((unsigned)cdiv(nk, 256)), dim3(256), 0, s, v, (int)ldv, (int)t_kv,
-                     L.tkv_pad, n_head, vh, vl);
-  LAUNCH_TRY("k_attn_split");
   const AttnPlanes P{qh, ql, kh, kl, vh, vl, L.tq_pad, L.tkv_pad};
+  const size_t nq = (size_t)n_head * L.tq_pad * 8, nk = (size_t)n_head * L.tkv_pad * 8;
+  const int wq = (int)cdiv(nq, 256), wk = (int)cdiv(nk, 256), wv = (int)cdiv(nk, 256);  // v^T: as many items as k
+  hipLaunchKernelGGL(k_attn_split, dim3((unsigned)(wq + wk + wv)), dim3(256), 0, s, q, (int)ldq, (int)t_q, k,
+                     (int)ldk, v, (int)ldv, (int)t_kv, P, n_head, wq, wk);
+  LAUNCH_TRY("k_attn_split");
   hipLaunchKernelGGL(k_attn, dim3((unsigned)(L.tq_pad / ATT_QB), (unsigned)n_head), dim3(128), 0, s, P, (int)t_q,
                      (int)t_kv, causal ? 1 : 0, out, (int)ldo);
   LAUNCH_TRY("k_attn");

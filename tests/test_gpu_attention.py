@@ -3,8 +3,9 @@ the reference's mha_split_kv, src/encoder.rs:48-80).
 
 Bar (written in each test): outputs within 1e-3 of the float32 oracle,
 max error scaled by the oracle row's L2 norm (the matmul path's tolerance),
-and -- what the hi/lo f16 products are built for -- within 2e-5 of the
-float64 oracle on the same scale."""
+and within 1e-5 of the float64 oracle on the same scale (measured: at most
+9e-7 for unit-scale inputs, 4e-6 for inputs of magnitude 1e-3 whose f16
+residuals are subnormal; the float32 oracle itself is at 3e-7)."""
 import numpy as np
 import pytest
 
@@ -14,7 +15,7 @@ from rusty_whisper_amd import _abi as A
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-3
-TIGHT = 2e-5
+TIGHT = 1e-5
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -36,10 +37,12 @@ def rel_row_l2(got, ref):
 
 
 def inputs(t_q, t_kv, n, seed, scale=1.0):
+    """N(0, scale) queries and keys (scale 3 peaks the softmax); values N(0,
+    1), or N(0, scale) when scale < 1."""
     rng = np.random.default_rng(seed)
     q = (rng.standard_normal((t_q, n)) * scale).astype(np.float32)
     k = (rng.standard_normal((t_kv, n)) * scale).astype(np.float32)
-    v = rng.standard_normal((t_kv, n)).astype(np.float32)
+    v = (rng.standard_normal((t_kv, n)) * min(scale, 1.0)).astype(np.float32)
     return q, k, v
 
 
@@ -48,6 +51,7 @@ def check(got, q, k, v, heads, causal):
     ref64 = mha(q, k, v, heads, causal, dtype=np.float64)
     assert np.all(np.isfinite(got))
     e32, e64 = rel_row_l2(got, ref32), rel_row_l2(got, ref64)
+    print(f"  error vs float32 oracle {e32:.3g}, vs float64 {e64:.3g}", flush=True)
     assert e32 <= TOL, e32
     assert e64 <= TIGHT, e64
     return e64
@@ -65,6 +69,7 @@ SHAPES = [
     (1, 77, 384, 6, True, 1.0),          # one decode step
     (1, 1500, 1280, 20, False, 1.0),     # cross-attention, one token
     (130, 130, 192, 3, True, 2.0),
+    (200, 300, 128, 2, False, 1e-3),     # small values: f16 residuals would be subnormal
 ]
 
 
