@@ -231,6 +231,35 @@ int rw_rocm_attention_dev(const float *q, size_t ldq, const float *k, size_t ldk
 int rw_rocm_attention(const float *q, const float *k, const float *v, size_t t_q, size_t t_kv, size_t n_state,
                       int n_head, int causal, float *out);
 
+/* ---- One encoder layer on the device ----
+ *
+ * x[t, n_state] (device, row-major) <- x + attn(ln1(x)), then
+ * x <- x + fc2(gelu(fc1(ln2(x)))): self_attention_block and mlp_block of
+ * src/encoder.rs:121-175 for one non-causal layer, every activation
+ * resident.  The layernorms are fused into the activation quantization of
+ * the product that follows them, GELU and the residual adds into the
+ * products' epilogues, and q, k and v come from one GEMM launch.  Weights
+ * are resident (rw_rocm_weight_upload / rw_rocm_model_weight); q, k, v and
+ * out are [n_state, n_state] of one dtype, fc1 [f, n_state], fc2 [n_state, f];
+ * vectors are device f32 (16-byte aligned), biases may be NULL.
+ * n_state = 64 n_head.  t must exceed 8 (the encoder has t = n_audio_ctx).
+ * The workspace (NULL: one kept per (device, stream)) holds
+ * rw_rocm_encoder_layer_workspace_size bytes; calls that share it must not
+ * overlap.  Outputs within the products' and attention's tolerances of the
+ * reference (1e-3 row-L2 per product). */
+typedef struct rw_encoder_layer {
+  const float *attn_ln_w, *attn_ln_b;
+  const rw_weight *q, *k, *v, *out;
+  const float *q_b, *k_b, *v_b, *out_b; /* whisper's key has no bias: k_b NULL */
+  const float *mlp_ln_w, *mlp_ln_b;
+  const rw_weight *fc1, *fc2;
+  const float *fc1_b, *fc2_b;
+  int n_head;
+} rw_encoder_layer;
+size_t rw_rocm_encoder_layer_workspace_size(const rw_encoder_layer *layer, size_t t);
+int rw_rocm_encoder_layer_dev(const rw_encoder_layer *layer, float *x, size_t t, void *workspace,
+                              size_t workspace_len, void *stream);
+
 /* ---- Model files straight to resident weights ----
  *
  * rw_rocm_model_load reads a whisper model in either container the reference

@@ -81,6 +81,9 @@ _SIGNATURES = {
                                         C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p]),
     "rw_rocm_attention": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t,
                                     C.c_int, C.c_int, C.c_void_p]),
+    "rw_rocm_encoder_layer_workspace_size": (C.c_size_t, [C.c_void_p, C.c_size_t]),
+    "rw_rocm_encoder_layer_dev": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t,
+                                            C.c_void_p]),
     "rw_rocm_model_load": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(C.c_void_p)]),
     "rw_rocm_model_free": (None, [C.c_void_p]),
     "rw_rocm_model_hparams": (C.c_int, [C.c_void_p, C.POINTER(C.c_int32)]),
@@ -321,6 +324,41 @@ def attention_dev(q, k, v, t_q: int, t_kv: int, n_state: int, n_head: int, causa
     check(lib().rw_rocm_attention_dev(_ptr(q), ldq or n_state, _ptr(k), ldk or n_state, _ptr(v), ldv or n_state,
                                       t_q, t_kv, n_state, n_head, 1 if causal else 0, _ptr(out), ldo or n_state,
                                       _ptr(workspace), workspace_len, stream))
+
+
+# ------------------------------------------------------- encoder layer
+
+class RwEncoderLayer(C.Structure):
+    """struct rw_encoder_layer (include/rw_rocm.h)."""
+    _fields_ = [("attn_ln_w", C.c_void_p), ("attn_ln_b", C.c_void_p),
+                ("q", C.c_void_p), ("k", C.c_void_p), ("v", C.c_void_p), ("out", C.c_void_p),
+                ("q_b", C.c_void_p), ("k_b", C.c_void_p), ("v_b", C.c_void_p), ("out_b", C.c_void_p),
+                ("mlp_ln_w", C.c_void_p), ("mlp_ln_b", C.c_void_p),
+                ("fc1", C.c_void_p), ("fc2", C.c_void_p), ("fc1_b", C.c_void_p), ("fc2_b", C.c_void_p),
+                ("n_head", C.c_int)]
+
+
+class EncoderLayer:
+    """One encoder layer's resident parameters: DeviceWeight matrices and
+    device vectors (torch tensors or device pointers), run by
+    rw_rocm_encoder_layer_dev (src/encoder.rs:121-175)."""
+
+    VECS = ("attn_ln_w", "attn_ln_b", "q_b", "k_b", "v_b", "out_b", "mlp_ln_w", "mlp_ln_b", "fc1_b", "fc2_b")
+    MATS = ("q", "k", "v", "out", "fc1", "fc2")
+
+    def __init__(self, n_head: int, **params):
+        self.params = params  # keeps the tensors alive
+        fields = {k: _ptr(params.get(k)) for k in self.VECS}
+        fields.update({k: params[k].handle for k in self.MATS})
+        self.st = RwEncoderLayer(n_head=n_head, **fields)
+
+    def workspace_size(self, t: int) -> int:
+        return lib().rw_rocm_encoder_layer_workspace_size(C.byref(self.st), t)
+
+    def run(self, x, t: int, workspace=None, workspace_len: int = 0, stream: int | None = None) -> None:
+        """x [t, n_state] on the device, updated in place."""
+        check(lib().rw_rocm_encoder_layer_dev(C.byref(self.st), _ptr(x), t, _ptr(workspace), workspace_len,
+                                              stream))
 
 
 MODEL_PARSE_ONLY = 1

@@ -194,7 +194,18 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
   const int l = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = l >> 5, n = l & 31;
-  const int head = blockIdx.y, q0 = blockIdx.x * ATT_QB;
+  // XCD-aware order: workgroup id % 8 is its XCD; each XCD takes one
+  // contiguous range of (head, query block) in head-major order, so a
+  // head's query blocks share their K and v^T planes through one L2
+  int head, q0;
+  {
+    const int nqb = gridDim.x, total = nqb * gridDim.y;
+    const int id = blockIdx.y * nqb + blockIdx.x;
+    const int per = total / 8, rem = total % 8, xcd = id % 8, slot = id / 8;
+    const int lin = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+    head = lin / nqb;
+    q0 = (lin % nqb) * ATT_QB;
+  }
   const int off = t_kv - t_q;  // absolute position of query row 0
   const int kv_end = causal ? min(t_kv, off + q0 + ATT_QB) : t_kv;
   const int nblk = (kv_end + ATT_KVB - 1) / ATT_KVB;

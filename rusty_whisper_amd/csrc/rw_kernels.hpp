@@ -352,11 +352,19 @@ __device__ inline float quant_q(float v) {
 // rs[row] = 2^(e-15) undoes the scaling in the GEMM's epilogue.  NP passes per
 // wavefront stay in registers; a longer row is read twice, once for its
 // largest |x| and once to quantize.
-template <int NP, int WPR>
+//
+// With LN, each row is first layer-normalized as src/tensor.rs:274-287 does
+// (mean, then the mean of squared deviations, inv = 1 / sqrt(var + 1e-5),
+// (x - mean) * inv * w + b; sums over the row in tree order), and the
+// normalized row is what gets quantized.  LN rows fit one chunk (the host
+// checks).
+template <int NP, int WPR, bool LN>
 __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ a, int m, int k, int nb,
-                                                      uint16_t *__restrict__ a16, float *__restrict__ rs) {
+                                                      uint16_t *__restrict__ a16, float *__restrict__ rs,
+                                                      const float *__restrict__ lnw, const float *__restrict__ lnb) {
   static_assert(WPR == 1 || WPR == 2 || WPR == 4, "a workgroup holds whole rows");
   __shared__ float part_max[4];
+  __shared__ float part_sum[2][4];
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // workgroup 8j + x runs on XCD x; the 8 * WPR workgroups of a row group
   // all take the same x, so the group's interleaved f16 lines are written
@@ -399,10 +407,57 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
     }
     return amax;
   };
+  // the row sum over all wavefronts of the row (tree order)
+  auto row_sum = [&](float t, int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) t += __shfl_xor(t, o);
+    if (WPR > 1) {
+      if (lane == 0) part_sum[slot][wv] = t;
+      __syncthreads();
+      t = part_sum[slot][wv - part];
+#pragma unroll
+      for (int jj = 1; jj < WPR; ++jj) t += part_sum[slot][wv - part + jj];
+    }
+    return t;
+  };
+  if constexpr (LN) {
+    // every wavefront takes part in both reductions (their barriers)
+    float t = 0.0f;
+    if (live) {
+      load(0);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) t += (v[p].x + v[p].y) + (v[p].z + v[p].w);
+    }
+    const float mean = __fdiv_rn(row_sum(t, 0), (float)k);
+    t = 0.0f;
+    if (live) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+        if (first(0, p) + lb < nb) {
+          const float d0 = v[p].x - mean, d1 = v[p].y - mean, d2 = v[p].z - mean, d3 = v[p].w - mean;
+          t += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+        }
+    }
+    const float var = __fdiv_rn(row_sum(t, 1), (float)k);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(var + 1e-5f));
+    if (live) {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const int bl = first(0, p) + lb;
+        if (bl < nb) {
+          const float4 w4 = ldg_f4(lnw + (size_t)bl * QK + 4 * lt), b4 = ldg_f4(lnb + (size_t)bl * QK + 4 * lt);
+          v[p].x = (v[p].x - mean) * inv * w4.x + b4.x;
+          v[p].y = (v[p].y - mean) * inv * w4.y + b4.y;
+          v[p].z = (v[p].z - mean) * inv * w4.z + b4.z;
+          v[p].w = (v[p].w - mean) * inv * w4.w + b4.w;
+        }
+      }
+    }
+  }
   float amax = 0.0f;  // fmaxf drops NaN, in any order of combination
   if (live) {
     for (int c = 0; c < nch; ++c) {
-      load(c);
+      if (!LN) load(c);
       amax = fmaxf(amax, block_max());
     }
     amax = fmaxf(amax, __shfl_xor(amax, 8));
@@ -988,12 +1043,23 @@ constexpr int GEMM_TM = 4, GEMM_TN = 2, GEMM_P = 2;
 // quantized activation): column tiles [tile0, tile0 + cdiv(ngroups, TN)) of
 // the launch belong to item i.
 constexpr int GEMM_MAX_SET = 4;
+// epilogue options of a GEMM item: GELU (tanh form, src/tensor.rs:289-305)
+// on y = x W^T + b, and accumulation into the output (out += y, the
+// residual add of src/encoder.rs:146-148, 171-173)
+constexpr int GEMM_GELU = 1, GEMM_ACC = 2;
 struct GemmItem {
   GemmPlanes gp;
   const float *bias;
   float *out;
-  int n, ngroups, tile0;
+  int n, ngroups, tile0, flags;
 };
+
+// gelu(t) = 0.5 t (1 + tanh(sqrt(2/pi) (t + 0.044715 t^3))), evaluated in
+// the reference's order
+__device__ inline float gelu_tanh(float t) {
+  const float inner = 0.7978846f * (t + 0.044715f * t * t * t);
+  return 0.5f * t * (1.0f + tanhf(inner));
+}
 struct GemmSet {
   GemmItem it[GEMM_MAX_SET];
   int count, nb, nb_pad;
@@ -1051,7 +1117,7 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int
   const GemmPlanes gp = it.gp;
   const float *__restrict__ bias = it.bias;
   float *__restrict__ out = it.out;
-  const int n = it.n, ngroups = it.ngroups;
+  const int n = it.n, ngroups = it.ngroups, flags = it.flags;
   const int nb = set.nb;
   const int nsw = nb > kw ? (nb - kw + KW - 1) / KW : 0;  // this wavefront's block count
 
@@ -1207,15 +1273,29 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int
           for (int e = 0; e < 4; ++e) y[4 * q + e] += bv[j];
         }
       }
+      if (flags & GEMM_GELU) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) y[v] = gelu_tanh(y[v]);
+      }
       // lane (h, r) holds rows 8q + 4h + e (e < 4) of column col
       float *o = out + (size_t)(tg * RG + 4 * h) * n + col;
       if (rows_full && (cg + 1) * RG <= n) {
+        if (flags & GEMM_ACC) {
+          float x[16];
+#pragma unroll
+          for (int v = 0; v < 16; ++v) x[v] = o[(size_t)(8 * (v >> 2) + (v & 3)) * n];
+#pragma unroll
+          for (int v = 0; v < 16; ++v) y[v] = x[v] + y[v];
+        }
 #pragma unroll
         for (int v = 0; v < 16; ++v) stg_f(o + (size_t)(8 * (v >> 2) + (v & 3)) * n, y[v]);
       } else if (col < n) {
 #pragma unroll
         for (int v = 0; v < 16; ++v)
-          if (tg * RG + 4 * h + 8 * (v >> 2) + (v & 3) < m) stg_f(o + (size_t)(8 * (v >> 2) + (v & 3)) * n, y[v]);
+          if (tg * RG + 4 * h + 8 * (v >> 2) + (v & 3) < m) {
+            float *p = o + (size_t)(8 * (v >> 2) + (v & 3)) * n;
+            stg_f(p, (flags & GEMM_ACC) ? *p + y[v] : y[v]);
+          }
       }
     }
   }

@@ -250,8 +250,11 @@ static ActView act_view(const ActLayout &L, void *ws) {
 
 // --------------------------------------------------------- launches
 
-static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &L, void *ws, hipStream_t s) {
+static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &L, void *ws, hipStream_t s,
+                           const float *lnw = nullptr, const float *lnb = nullptr) {
   char *b = (char *)ws;
+  if (lnw && (!L.f16 || (L.nb + 7) / 8 > 32))
+    return fail(RW_EINVAL, "layernorm + quantize takes m > %d rows of at most 8192 values", GEMV_MAX_M);
   if (L.f16) {
     if ((size_t)L.mgroups * RG * k * 2 >= ((size_t)1 << 32))
       return fail(RW_EINVAL, "activation [%zu, %zu] too large for the GEMM layout's 32-bit offsets", m, k);
@@ -260,16 +263,25 @@ static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &
     const size_t g8 = align_up((size_t)L.mgroups, 8);  // row groups, padded to whole XCD rounds
     uint16_t *a16 = (uint16_t *)(b + L.off_a16);
     float *rs = (float *)(b + L.off_rs);
-#define RW_QF16(NP, WPR)                                                                                    \
-  hipLaunchKernelGGL((k_quantize_f16<NP, WPR>), dim3((unsigned)(g8 * RG * WPR / 4)), dim3(256), 0, s, a, (int)m, \
-                     (int)k, L.nb, a16, rs)
+#define RW_QF16(NP, WPR, LN)                                                                                \
+  hipLaunchKernelGGL((k_quantize_f16<NP, WPR, LN>), dim3((unsigned)(g8 * RG * WPR / 4)), dim3(256), 0, s, a,     \
+                     (int)m, (int)k, L.nb, a16, rs, lnw, lnb)
     const int passes = (L.nb + 7) / 8;
-    if (passes <= 1) RW_QF16(1, 1);
-    else if (passes <= 2) RW_QF16(1, 2);
-    else if (passes <= 4) RW_QF16(1, 4);
-    else if (passes <= 8) RW_QF16(2, 4);
-    else if (passes <= 20) RW_QF16(5, 4);
-    else RW_QF16(8, 4);
+    if (lnw) {
+      if (passes <= 1) RW_QF16(1, 1, true);
+      else if (passes <= 2) RW_QF16(1, 2, true);
+      else if (passes <= 4) RW_QF16(1, 4, true);
+      else if (passes <= 8) RW_QF16(2, 4, true);
+      else if (passes <= 20) RW_QF16(5, 4, true);
+      else RW_QF16(8, 4, true);
+    } else {
+      if (passes <= 1) RW_QF16(1, 1, false);
+      else if (passes <= 2) RW_QF16(1, 2, false);
+      else if (passes <= 4) RW_QF16(1, 4, false);
+      else if (passes <= 8) RW_QF16(2, 4, false);
+      else if (passes <= 20) RW_QF16(5, 4, false);
+      else RW_QF16(8, 4, false);
+    }
 #undef RW_QF16
     LAUNCH_TRY("k_quantize_f16");
     return RW_OK;
@@ -322,7 +334,7 @@ static void launch_gemm_dt(const GemmSet &set, size_t tiles, const ActView &av, 
 // k against the quantized activation `av`.  The kernel addresses each plane
 // with 32-bit byte offsets (buffer loads), so every plane stays below 4 GiB.
 static int run_gemm(const rw_weight *const *w, const float *const *bias, float *const *out, size_t count,
-                    const ActView &av, int m, hipStream_t s) {
+                    const ActView &av, int m, hipStream_t s, const int *flags = nullptr) {
   const size_t lim = (size_t)1 << 32;
   if ((size_t)av.mgroups * (size_t)w[0]->nb * 2048 >= lim)
     return fail(RW_EINVAL, "activation [%d, %zu] too large for the GEMM's 32-bit offsets", m, w[0]->k);
@@ -341,6 +353,7 @@ static int run_gemm(const rw_weight *const *w, const float *const *bias, float *
     it.out = out[i];
     it.n = (int)w[i]->n;
     it.ngroups = w[i]->ngroups;
+    it.flags = flags ? flags[i] : 0;
     it.tile0 = (int)tiles;
     tiles += cdiv(w[i]->ngroups, GEMM_TN);
   }
@@ -722,6 +735,91 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
                      (int)t_kv, causal ? 1 : 0, out, (int)ldo);
   LAUNCH_TRY("k_attn");
   return RW_OK;
+}
+
+// ------------------------------------------------------ encoder layer
+
+struct LayerLayout {
+  size_t n, f;
+  ActLayout act;  // the quantized activation of the widest product (fc2's)
+  AttnLayout att;
+  size_t off_act, off_q, off_k, off_v, off_a, off_h, off_att, bytes;
+};
+
+static LayerLayout layer_layout(size_t n, size_t f, size_t t) {
+  LayerLayout L{};
+  L.n = n;
+  L.f = f;
+  L.act = act_layout(t, std::max(n, f));
+  L.att = attn_layout(t, t, n);
+  const size_t row = t * n * 4;
+  L.off_act = 0;
+  L.off_q = align_up(L.act.bytes, 256);
+  L.off_k = align_up(L.off_q + row, 256);
+  L.off_v = align_up(L.off_k + row, 256);
+  L.off_a = align_up(L.off_v + row, 256);
+  L.off_h = align_up(L.off_a + row, 256);
+  L.off_att = align_up(L.off_h + t * f * 4, 256);
+  L.bytes = align_up(L.off_att + L.att.bytes, 256);
+  return L;
+}
+
+static bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+static int check_layer(const rw_encoder_layer *E, size_t t) {
+  if (!E) return fail(RW_EINVAL, "layer is NULL");
+  if (!E->q || !E->k || !E->v || !E->out || !E->fc1 || !E->fc2) return fail(RW_EINVAL, "a layer weight is NULL");
+  if (!E->attn_ln_w || !E->attn_ln_b || !E->mlp_ln_w || !E->mlp_ln_b)
+    return fail(RW_EINVAL, "a layernorm vector is NULL");
+  const size_t n = E->q->k, f = E->fc1->n;
+  if (E->n_head <= 0 || n != (size_t)E->n_head * ATT_DH)
+    return fail(RW_EINVAL, "n_state %zu != 64 * n_head (%d)", n, E->n_head);
+  const rw_weight *sq[4] = {E->q, E->k, E->v, E->out};
+  for (const rw_weight *w : sq)
+    if (w->n != n || w->k != n || w->dtype != E->q->dtype)
+      return fail(RW_EINVAL, "q, k, v and out must be [%zu, %zu] of one dtype", n, n);
+  if (E->fc1->k != n || E->fc2->n != n || E->fc2->k != f)
+    return fail(RW_EINVAL, "fc1 must be [f, %zu] and fc2 [%zu, f] (f = %zu)", n, n, f);
+  if (t <= (size_t)GEMV_MAX_M) return fail(RW_EINVAL, "t = %zu: the layer takes more than %d rows", t, GEMV_MAX_M);
+  if (t > (1u << 20)) return fail(RW_EINVAL, "t = %zu is too large", t);
+  if (!al16(E->attn_ln_w) || !al16(E->attn_ln_b) || !al16(E->mlp_ln_w) || !al16(E->mlp_ln_b))
+    return fail(RW_EINVAL, "layernorm vectors must be 16-byte aligned");
+  return RW_OK;
+}
+
+static int run_encoder_layer(const rw_encoder_layer *E, float *x, size_t t, void *ws, hipStream_t s) {
+  const LayerLayout L = layer_layout(E->q->k, E->fc1->n, t);
+  char *b = (char *)ws;
+  float *qb = (float *)(b + L.off_q), *kb = (float *)(b + L.off_k), *vb = (float *)(b + L.off_v);
+  float *ab = (float *)(b + L.off_a), *hb = (float *)(b + L.off_h);
+  const size_t n = L.n, f = L.f;
+  const ActLayout Ln = act_layout(t, n), Lf = act_layout(t, f);
+  const int m = (int)t;
+  // x + out(attn(q, k, v of ln1(x)))
+  int rc = launch_quantize(x, t, n, Ln, b, s, E->attn_ln_w, E->attn_ln_b);
+  if (rc) return rc;
+  {
+    const rw_weight *w3[3] = {E->q, E->k, E->v};
+    const float *b3[3] = {E->q_b, E->k_b, E->v_b};
+    float *o3[3] = {qb, kb, vb};
+    rc = run_gemm(w3, b3, o3, 3, act_view(Ln, b), m, s);
+    if (rc) return rc;
+  }
+  rc = run_attention(qb, n, kb, n, vb, n, t, t, E->n_head, 0, ab, n, L.att, b + L.off_att, s);
+  if (rc) return rc;
+  rc = launch_quantize(ab, t, n, Ln, b, s);
+  if (rc) return rc;
+  const int acc = GEMM_ACC, act = GEMM_GELU;
+  rc = run_gemm(&E->out, &E->out_b, &x, 1, act_view(Ln, b), m, s, &acc);
+  if (rc) return rc;
+  // x + fc2(gelu(fc1(ln2(x))))
+  rc = launch_quantize(x, t, n, Ln, b, s, E->mlp_ln_w, E->mlp_ln_b);
+  if (rc) return rc;
+  rc = run_gemm(&E->fc1, &E->fc1_b, &hb, 1, act_view(Ln, b), m, s, &act);
+  if (rc) return rc;
+  rc = launch_quantize(hb, t, f, Lf, b, s);
+  if (rc) return rc;
+  return run_gemm(&E->fc2, &E->fc2_b, &x, 1, act_view(Lf, b), m, s, &acc);
 }
 
 extern "C" {
@@ -1231,6 +1329,28 @@ int rw_rocm_attention(const float *q, const float *k, const float *v, size_t t_q
   HIP_TRY(hipMemcpyAsync(out, dout, t_q * n_state * 4, hipMemcpyDeviceToHost, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
   return RW_OK;
+}
+
+size_t rw_rocm_encoder_layer_workspace_size(const rw_encoder_layer *layer, size_t t) {
+  if (!layer || !layer->q || !layer->fc1) return 0;
+  return layer_layout(layer->q->k, layer->fc1->n, t).bytes;
+}
+
+int rw_rocm_encoder_layer_dev(const rw_encoder_layer *layer, float *x, size_t t, void *workspace,
+                              size_t workspace_len, void *stream) {
+  int rc = check_layer(layer, t);
+  if (rc) return rc;
+  if (!x || !al16(x)) return fail(RW_EINVAL, "x must be a 16-byte aligned device pointer");
+  HIP_TRY(hipSetDevice(layer->q->device));
+  const size_t need = layer_layout(layer->q->k, layer->fc1->n, t).bytes;
+  void *ws = workspace;
+  if (ws) {
+    if (workspace_len < need) return fail(RW_EINVAL, "workspace of %zu bytes < %zu needed", workspace_len, need);
+  } else {
+    rc = stream_workspace(layer->q->device, stream, need, &ws);
+    if (rc) return rc;
+  }
+  return run_encoder_layer(layer, x, t, ws, (hipStream_t)stream);
 }
 
 }  // extern "C"
