@@ -268,6 +268,47 @@ def time_attention(A, torch, stream, steps: int, warmup: int, t: int = 1500, n_s
     return ms, flops
 
 
+def time_encoder_layers(A, torch, W, stream, steps: int, warmup: int):
+    """All 32 large-v3 encoder layers end to end on the device
+    (rw_rocm_encoder_layer_dev per layer: layernorms, the four products,
+    attention, GELU and the residual adds) on one resident [1500, 1280]
+    activation; the weights are the workload's, the layernorm and bias
+    vectors random.  Returns ms per pass over all layers."""
+    m, d, fc = W["m"], W["d"], W["fc"]
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(21)
+    vec = lambda k, c: (torch.randn(k, device="cuda:0", generator=g) * 0.1 + c)  # noqa: E731
+    layers = []
+    for lw in W["layers"]:
+        layers.append(A.EncoderLayer(d // 64, q=lw["q"], k=lw["k"], v=lw["v"], out=lw["out"], fc1=lw["fc1"],
+                                     fc2=lw["fc2"], attn_ln_w=vec(d, 1.0), attn_ln_b=vec(d, 0.0),
+                                     q_b=W["bias"]["q"], v_b=W["bias"]["v"], out_b=W["bias"]["out"],
+                                     mlp_ln_w=vec(d, 1.0), mlp_ln_b=vec(d, 0.0), fc1_b=W["bias"]["fc1"],
+                                     fc2_b=W["bias"]["fc2"]))
+    x0 = torch.randn(m, d, device="cuda:0", generator=g)
+    x = x0.clone()
+    wsz = layers[0].workspace_size(m)
+    ws = torch.empty(wsz, dtype=torch.uint8, device="cuda:0")
+
+    def run():
+        x.copy_(x0)
+        for L in layers:
+            L.run(x, m, ws, wsz, stream)
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ok = bool(torch.isfinite(x).all().item())
+    return e0.elapsed_time(e1) / steps, ok
+
+
 def time_model_load(A, synth, dtype: int, path: str, reps: int = 2):
     """rw_rocm_model_load on a ggml .bin holding large-v3's quantized matrices
     (32 encoder layers x 6 linears, 32 decoder layers x 10, the token
@@ -363,6 +404,7 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
+    ap.add_argument("--no-layers", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--load-model", default="",
                     help="also time the model loader on a large-v3-shaped ggml file written to this path")
@@ -446,6 +488,18 @@ def main() -> int:
             "frac_of_int8_peak": round(gemm_tops / INT8_PEAK_TOPS, 4),
         },
     }
+    if not args.no_layers:
+        lms, finite = time_encoder_layers(A, torch, W, stream, max(3, args.steps // 2), 1)
+        log(f"32 encoder layers on the device {lms:.3f} ms ({lms * 1e3 / 32:.1f} us per layer, finite={finite})")
+        result["encoder_layers"] = {
+            "workload": f"large-v3 encoder, 32 layers, {args.quant}, M={args.m}: per layer layernorm + q/k/v + "
+                        "attention (20 heads) + out + residual, layernorm + fc1 + GELU + fc2 + residual, all on the "
+                        "device (rw_rocm_encoder_layer_dev)",
+            "ms_per_pass": round(lms, 4),
+            "us_per_layer": round(lms * 1e3 / 32, 2),
+            "finite": finite,
+        }
+
     del W
     torch.cuda.empty_cache()
 
@@ -479,7 +533,7 @@ def main() -> int:
             "us_per_layer": round(ams * 1e3, 2),
             "flops": aflops,
             "TFLOP_per_s": round(atf, 2),
-            "launch": "rw_rocm_attention_dev: three split launches (q, k, v to f16 hi/lo planes) and one k_attn",
+            "launch": "rw_rocm_attention_dev: one split launch (q, k, v to f16 hi/lo planes) and one k_attn",
             "note": "algorithmic flops 4*t^2*64 per head; each product runs as three f16 MFMA products",
         }
 
