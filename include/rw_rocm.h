@@ -260,6 +260,54 @@ size_t rw_rocm_encoder_layer_workspace_size(const rw_encoder_layer *layer, size_
 int rw_rocm_encoder_layer_dev(const rw_encoder_layer *layer, float *x, size_t t, void *workspace,
                               size_t workspace_len, void *stream);
 
+/* ---- The decoder step on the device ----
+ *
+ * rw_decoder is the reference's Decoder (src/decoder.rs:26-213) with its
+ * state resident: per-layer self-attention K/V caches of n_ctx rows, and
+ * cross-attention K/V computed once per audio window (kept as the
+ * attention kernel's f16 hi/lo planes).  forward_hidden runs tokens at
+ * positions n_past .. n_past + n_tok through the embedding, every layer
+ * (causal self-attention over cache + new rows, cross-attention, MLP) and
+ * the final layernorm, extending the caches; the logits are then
+ * rw_rocm_matmul_t_q_dev(token_embedding, hidden) as project_logits does.
+ * Weights are resident rw_weight handles; vectors are device f32, 16-byte
+ * aligned; biases may be NULL.  The token embedding must be quantized (as
+ * in every quantized ggml model).  Replaces Decoder::new (:36-67),
+ * fork (:70-79), reset (:86-95) and forward_hidden (:110-213).  A decoder
+ * is used by one stream at a time. */
+typedef struct rw_decoder_layer {
+  const float *attn_ln_w, *attn_ln_b;
+  const rw_weight *q, *k, *v, *out;
+  const float *q_b, *v_b, *out_b;
+  const float *cross_ln_w, *cross_ln_b;
+  const rw_weight *cq, *ck, *cv, *cout;
+  const float *cq_b, *cv_b, *cout_b;
+  const float *mlp_ln_w, *mlp_ln_b;
+  const rw_weight *fc1, *fc2;
+  const float *fc1_b, *fc2_b;
+} rw_decoder_layer;
+typedef struct rw_decoder_params {
+  int n_layer, n_head, n_ctx;       /* n_text_layer, n_text_head, n_text_ctx */
+  const rw_decoder_layer *layers;   /* n_layer entries, copied at create */
+  const rw_weight *token_embedding; /* [n_vocab, n_state] */
+  const float *positional;          /* [n_ctx, n_state] */
+  const float *ln_w, *ln_b;         /* decoder.ln */
+} rw_decoder_params;
+typedef struct rw_decoder rw_decoder;
+int rw_rocm_decoder_create(const rw_decoder_params *params, size_t n_audio_ctx, rw_decoder **out);
+void rw_rocm_decoder_free(rw_decoder *d);
+/* cross K/V of every layer from the encoder output [n_audio_ctx, n_state]
+ * (device), and n_past = 0 */
+int rw_rocm_decoder_set_audio_dev(rw_decoder *d, const float *enc_out, void *stream);
+int rw_rocm_decoder_reset(rw_decoder *d);
+int rw_rocm_decoder_n_past(const rw_decoder *d, size_t *n_past);
+/* an independent branch: copies the self-attention caches (on `stream`),
+ * shares the cross K/V */
+int rw_rocm_decoder_fork(const rw_decoder *d, void *stream, rw_decoder **out);
+/* tokens: host array of n_tok ids; hidden: device [n_tok, n_state] */
+int rw_rocm_decoder_forward_hidden_dev(rw_decoder *d, const uint32_t *tokens, size_t n_tok, float *hidden,
+                                       void *stream);
+
 /* ---- Model files straight to resident weights ----
  *
  * rw_rocm_model_load reads a whisper model in either container the reference

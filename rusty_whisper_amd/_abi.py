@@ -84,6 +84,14 @@ _SIGNATURES = {
     "rw_rocm_encoder_layer_workspace_size": (C.c_size_t, [C.c_void_p, C.c_size_t]),
     "rw_rocm_encoder_layer_dev": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_size_t,
                                             C.c_void_p]),
+    "rw_rocm_decoder_create": (C.c_int, [C.c_void_p, C.c_size_t, C.POINTER(C.c_void_p)]),
+    "rw_rocm_decoder_free": (None, [C.c_void_p]),
+    "rw_rocm_decoder_set_audio_dev": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
+    "rw_rocm_decoder_reset": (C.c_int, [C.c_void_p]),
+    "rw_rocm_decoder_n_past": (C.c_int, [C.c_void_p, C.POINTER(C.c_size_t)]),
+    "rw_rocm_decoder_fork": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p)]),
+    "rw_rocm_decoder_forward_hidden_dev": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p,
+                                                     C.c_void_p]),
     "rw_rocm_model_load": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(C.c_void_p)]),
     "rw_rocm_model_free": (None, [C.c_void_p]),
     "rw_rocm_model_hparams": (C.c_int, [C.c_void_p, C.POINTER(C.c_int32)]),
@@ -359,6 +367,85 @@ class EncoderLayer:
         """x [t, n_state] on the device, updated in place."""
         check(lib().rw_rocm_encoder_layer_dev(C.byref(self.st), _ptr(x), t, _ptr(workspace), workspace_len,
                                               stream))
+
+
+# ------------------------------------------------------------- decoder
+
+_DEC_LAYER_VECS = ("attn_ln_w", "attn_ln_b", "q_b", "v_b", "out_b", "cross_ln_w", "cross_ln_b", "cq_b", "cv_b",
+                   "cout_b", "mlp_ln_w", "mlp_ln_b", "fc1_b", "fc2_b")
+_DEC_LAYER_MATS = ("q", "k", "v", "out", "cq", "ck", "cv", "cout", "fc1", "fc2")
+
+
+class RwDecoderLayer(C.Structure):
+    """struct rw_decoder_layer (include/rw_rocm.h)."""
+    _fields_ = [(name, C.c_void_p) for name in (
+        "attn_ln_w", "attn_ln_b", "q", "k", "v", "out", "q_b", "v_b", "out_b", "cross_ln_w", "cross_ln_b",
+        "cq", "ck", "cv", "cout", "cq_b", "cv_b", "cout_b", "mlp_ln_w", "mlp_ln_b", "fc1", "fc2", "fc1_b",
+        "fc2_b")]
+
+
+class RwDecoderParams(C.Structure):
+    _fields_ = [("n_layer", C.c_int), ("n_head", C.c_int), ("n_ctx", C.c_int), ("layers", C.c_void_p),
+                ("token_embedding", C.c_void_p), ("positional", C.c_void_p), ("ln_w", C.c_void_p),
+                ("ln_b", C.c_void_p)]
+
+
+class Decoder:
+    """rw_decoder: the reference's Decoder (src/decoder.rs:26-213) with its
+    caches resident.  layers: list of dicts of DeviceWeight matrices and
+    device vectors; token_embedding a DeviceWeight; positional, ln_w, ln_b
+    device vectors."""
+
+    def __init__(self, n_head: int, n_ctx: int, n_audio_ctx: int, layers, token_embedding, positional, ln_w, ln_b,
+                 _handle=None, _keep=None):
+        self._keep = _keep or (layers, token_embedding, positional, ln_w, ln_b)
+        if _handle is not None:
+            self.handle = _handle
+            return
+        arr = (RwDecoderLayer * len(layers))()
+        for i, L in enumerate(layers):
+            for k in _DEC_LAYER_VECS:
+                setattr(arr[i], k, _ptr(L.get(k)))
+            for k in _DEC_LAYER_MATS:
+                setattr(arr[i], k, L[k].handle)
+        prm = RwDecoderParams(len(layers), n_head, n_ctx, C.cast(arr, C.c_void_p), token_embedding.handle,
+                              _ptr(positional), _ptr(ln_w), _ptr(ln_b))
+        h = C.c_void_p()
+        check(lib().rw_rocm_decoder_create(C.byref(prm), n_audio_ctx, C.byref(h)))
+        self.handle = h.value
+
+    def set_audio(self, enc_out, stream: int | None = None) -> None:
+        check(lib().rw_rocm_decoder_set_audio_dev(self.handle, _ptr(enc_out), stream))
+
+    def reset(self) -> None:
+        check(lib().rw_rocm_decoder_reset(self.handle))
+
+    @property
+    def n_past(self) -> int:
+        n = C.c_size_t()
+        check(lib().rw_rocm_decoder_n_past(self.handle, C.byref(n)))
+        return n.value
+
+    def fork(self, stream: int | None = None) -> "Decoder":
+        h = C.c_void_p()
+        check(lib().rw_rocm_decoder_fork(self.handle, stream, C.byref(h)))
+        return Decoder(0, 0, 0, None, None, None, None, None, _handle=h.value, _keep=self._keep)
+
+    def forward_hidden(self, tokens, hidden, stream: int | None = None) -> None:
+        """tokens: host ids; hidden: device [len(tokens), n_state]."""
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        check(lib().rw_rocm_decoder_forward_hidden_dev(self.handle, t.ctypes.data, t.size, _ptr(hidden), stream))
+
+    def free(self) -> None:
+        if getattr(self, "handle", None):
+            lib().rw_rocm_decoder_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 MODEL_PARSE_ONLY = 1

@@ -21,6 +21,7 @@
 
 #include <algorithm>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <tuple>
@@ -28,6 +29,7 @@
 
 #include "rw_attn.hpp"
 #include "rw_kernels.hpp"
+#include "rw_dec.hpp"
 #include "rw_rocm.h"
 
 using namespace rw;
@@ -713,7 +715,7 @@ static int check_attn_args(const float *q, size_t ldq, const float *k, size_t ld
 
 static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk, const float *v, size_t ldv,
                          size_t t_q, size_t t_kv, int n_head, int causal, float *out, size_t ldo, const AttnLayout &L,
-                         void *ws, hipStream_t s) {
+                         void *ws, hipStream_t s, const AttnPlanes *kv_split = nullptr) {
   char *b = (char *)ws;
   uint16_t *qh = (uint16_t *)(b + L.off_qh), *ql = (uint16_t *)(b + L.off_ql);
   uint16_t *kh = (uint16_t *)(b + L.off_kh), *kl = (uint16_t *)(b + L.off_kl);
@@ -725,9 +727,15 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
     LAUNCH_TRY("k_attn_zero");
     return RW_OK;
   }
-  const AttnPlanes P{qh, ql, kh, kl, vh, vl, L.tq_pad, L.tkv_pad};
-  const size_t nq = (size_t)n_head * L.tq_pad * 8, nk = (size_t)n_head * L.tkv_pad * 8;
-  const int wq = (int)cdiv(nq, 256), wk = (int)cdiv(nk, 256), wv = (int)cdiv(nk, 256);  // v^T: as many items as k
+  // kv_split: K and v^T already split (the decoder's cross-attention); only q
+  // is split here
+  AttnPlanes P{qh, ql, kh, kl, vh, vl, L.tq_pad, L.tkv_pad};
+  if (kv_split) {
+    P.kh = kv_split->kh, P.kl = kv_split->kl, P.vh = kv_split->vh, P.vl = kv_split->vl;
+    P.tkv_pad = kv_split->tkv_pad;
+  }
+  const size_t nq = (size_t)n_head * L.tq_pad * 8, nk = kv_split ? 0 : (size_t)n_head * L.tkv_pad * 8;
+  const int wq = (int)cdiv(nq, 256), wk = (int)cdiv(nk, 256), wv = wk;  // v^T: as many items as k
   hipLaunchKernelGGL(k_attn_split, dim3((unsigned)(wq + wk + wv)), dim3(256), 0, s, q, (int)ldq, (int)t_q, k,
                      (int)ldk, v, (int)ldv, (int)t_kv, P, n_head, wq, wk);
   LAUNCH_TRY("k_attn_split");
@@ -735,6 +743,158 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
                      (int)t_kv, causal ? 1 : 0, out, (int)ldo);
   LAUNCH_TRY("k_attn");
   return RW_OK;
+}
+
+// ------------------------------------------------------ decoder step
+
+// Cross-attention K/V of every layer as the attention kernel's split planes,
+// computed once per audio window and shared by forks.
+struct CrossKV {
+  int device = -1;
+  size_t n_audio = 0, n = 0;
+  int n_layer = 0, tkv_pad = 0;
+  void *buf = nullptr;  // per layer: kh, kl, vh, vl planes of (n_head x 64) x tkv_pad f16
+  size_t layer_bytes = 0, plane_bytes = 0;
+  ~CrossKV() {
+    if (buf) (void)hipFree(buf);
+  }
+  AttnPlanes planes(int l) const {
+    const char *b = (const char *)buf + (size_t)l * layer_bytes;
+    return AttnPlanes{nullptr, nullptr, (const uint16_t *)b, (const uint16_t *)(b + plane_bytes),
+                      (const uint16_t *)(b + 2 * plane_bytes), (const uint16_t *)(b + 3 * plane_bytes), 0, tkv_pad};
+  }
+};
+
+struct rw_decoder {
+  rw_decoder_params p{};
+  std::vector<rw_decoder_layer> layers;
+  int device = -1;
+  size_t n = 0, f = 0, n_audio = 0, n_past = 0;
+  float *self_kv = nullptr;  // per layer: k then v, n_ctx x n each
+  std::shared_ptr<CrossKV> cross;
+  bool audio = false;
+  void *scratch = nullptr;
+  size_t scratch_cap = 0;
+  ~rw_decoder() {
+    if (self_kv) (void)hipFree(self_kv);
+    if (scratch) (void)hipFree(scratch);
+  }
+  float *self_k(int l) const { return self_kv + (size_t)l * 2 * p.n_ctx * n; }
+  float *self_v(int l) const { return self_kv + ((size_t)l * 2 + 1) * p.n_ctx * n; }
+};
+
+static int check_decoder_params(const rw_decoder_params *P) {
+  if (!P || !P->layers || !P->token_embedding || !P->positional || !P->ln_w || !P->ln_b)
+    return fail(RW_EINVAL, "decoder params, layers, token embedding, positional or final layernorm is NULL");
+  if (P->n_layer <= 0 || P->n_ctx <= 0) return fail(RW_EINVAL, "n_layer and n_ctx must be positive");
+  const size_t n = P->token_embedding->k;
+  if (P->n_head <= 0 || n != (size_t)P->n_head * ATT_DH)
+    return fail(RW_EINVAL, "n_state %zu != 64 * n_head (%d)", n, P->n_head);
+  const size_t f = P->layers[0].fc1 ? P->layers[0].fc1->n : 0;
+  for (int l = 0; l < P->n_layer; ++l) {
+    const rw_decoder_layer &L = P->layers[l];
+    const rw_weight *sq[8] = {L.q, L.k, L.v, L.out, L.cq, L.ck, L.cv, L.cout};
+    for (const rw_weight *w : sq)
+      if (!w || w->n != n || w->k != n) return fail(RW_EINVAL, "layer %d: attention weights must be [%zu, %zu]", l, n, n);
+    if (!L.fc1 || !L.fc2 || L.fc1->k != n || L.fc1->n != f || L.fc2->n != n || L.fc2->k != f)
+      return fail(RW_EINVAL, "layer %d: fc1 must be [f, %zu] and fc2 [%zu, f]", l, n, n);
+    const float *vec[6] = {L.attn_ln_w, L.attn_ln_b, L.cross_ln_w, L.cross_ln_b, L.mlp_ln_w, L.mlp_ln_b};
+    for (const float *v : vec)
+      if (!v) return fail(RW_EINVAL, "layer %d: a layernorm vector is NULL", l);
+  }
+  return RW_OK;
+}
+
+// the per-call scratch of forward_hidden for n_tok tokens
+struct DecScratch {
+  size_t off_tok, off_x, off_cur, off_q, off_a, off_p, off_h, off_act, off_att, bytes;
+  AttnLayout self_att, cross_att;
+};
+static DecScratch dec_scratch(const rw_decoder *d, size_t n_tok) {
+  DecScratch S{};
+  const size_t row = n_tok * d->n * 4;
+  S.self_att = attn_layout(n_tok, d->p.n_ctx, d->n);
+  S.cross_att = attn_layout(n_tok, d->n_audio, d->n);
+  S.off_tok = 0;
+  S.off_x = align_up(n_tok * 4, 256);
+  S.off_cur = align_up(S.off_x + row, 256);
+  S.off_q = align_up(S.off_cur + row, 256);
+  S.off_a = align_up(S.off_q + row, 256);
+  S.off_p = align_up(S.off_a + row, 256);
+  S.off_h = align_up(S.off_p + row, 256);
+  S.off_act = align_up(S.off_h + n_tok * d->f * 4, 256);
+  S.off_att = align_up(S.off_act + act_layout(n_tok, std::max(d->n, d->f)).bytes, 256);
+  S.bytes = align_up(S.off_att + std::max(S.self_att.bytes, S.cross_att.bytes), 256);
+  return S;
+}
+
+static int launch_layernorm(const float *x, size_t rows, size_t n, const float *w, const float *b, float *y,
+                            hipStream_t s) {
+  hipLaunchKernelGGL(k_layernorm, dim3((unsigned)rows), dim3(256), 0, s, x, (int)n, w, b, y);
+  LAUNCH_TRY("k_layernorm");
+  return RW_OK;
+}
+static int launch_add(float *x, const float *y, size_t cnt, hipStream_t s) {
+  hipLaunchKernelGGL(k_add, dim3((unsigned)cdiv(cnt, 256)), dim3(256), 0, s, x, y, cnt);
+  LAUNCH_TRY("k_add");
+  return RW_OK;
+}
+
+#define RW_TRY(expr)       \
+  do {                     \
+    int rc_ = (expr);      \
+    if (rc_) return rc_;   \
+  } while (0)
+
+static int decoder_forward(rw_decoder *d, size_t n_tok, float *hidden, char *b, const DecScratch &S, hipStream_t s) {
+  const size_t n = d->n, f = d->f, cnt = n_tok * n;
+  const int *tok = (const int *)(b + S.off_tok);
+  float *x = (float *)(b + S.off_x), *cur = (float *)(b + S.off_cur), *q = (float *)(b + S.off_q);
+  float *att = (float *)(b + S.off_a), *prj = (float *)(b + S.off_p), *h = (float *)(b + S.off_h);
+  void *act = b + S.off_act, *aws = b + S.off_att;
+  const rw_weight *E = d->p.token_embedding;
+  const size_t items = n_tok * (size_t)E->nb;
+#define RW_EMB(DT)                                                                                           \
+  hipLaunchKernelGGL(k_embed<DT>, dim3((unsigned)cdiv(items, 256)), dim3(256), 0, s, E->view, tok, (int)n_tok, \
+                     d->p.positional, (int)d->n_past, x)
+  switch (E->dtype) {
+    case RW_Q4_0: RW_EMB(RW_Q4_0); break;
+    case RW_Q4_1: RW_EMB(RW_Q4_1); break;
+    case RW_Q5_0: RW_EMB(RW_Q5_0); break;
+    case RW_Q5_1: RW_EMB(RW_Q5_1); break;
+    default: RW_EMB(RW_Q8_0); break;
+  }
+#undef RW_EMB
+  LAUNCH_TRY("k_embed");
+  const size_t t_kv = d->n_past + n_tok;
+  for (int l = 0; l < d->p.n_layer; ++l) {
+    const rw_decoder_layer &L = d->layers[l];
+    // causal self-attention over the cache and the new rows
+    RW_TRY(launch_layernorm(x, n_tok, n, L.attn_ln_w, L.attn_ln_b, cur, s));
+    RW_TRY(run_matmul(L.q, cur, n_tok, L.q_b, q, act, s));
+    RW_TRY(run_matmul(L.k, cur, n_tok, nullptr, d->self_k(l) + d->n_past * n, act, s));
+    RW_TRY(run_matmul(L.v, cur, n_tok, L.v_b, d->self_v(l) + d->n_past * n, act, s));
+    RW_TRY(run_attention(q, n, d->self_k(l), n, d->self_v(l), n, n_tok, t_kv, d->p.n_head, 1, att, n, S.self_att,
+                         aws, s));
+    RW_TRY(run_matmul(L.out, att, n_tok, L.out_b, prj, act, s));
+    RW_TRY(launch_add(x, prj, cnt, s));
+    // cross-attention to the window's K/V
+    RW_TRY(launch_layernorm(x, n_tok, n, L.cross_ln_w, L.cross_ln_b, cur, s));
+    RW_TRY(run_matmul(L.cq, cur, n_tok, L.cq_b, q, act, s));
+    const AttnPlanes cp = d->cross->planes(l);
+    RW_TRY(run_attention(q, n, nullptr, n, nullptr, n, n_tok, d->n_audio, d->p.n_head, 0, att, n, S.cross_att, aws,
+                         s, &cp));
+    RW_TRY(run_matmul(L.cout, att, n_tok, L.cout_b, prj, act, s));
+    RW_TRY(launch_add(x, prj, cnt, s));
+    // MLP
+    RW_TRY(launch_layernorm(x, n_tok, n, L.mlp_ln_w, L.mlp_ln_b, cur, s));
+    RW_TRY(run_matmul(L.fc1, cur, n_tok, L.fc1_b, h, act, s));
+    hipLaunchKernelGGL(k_gelu, dim3((unsigned)cdiv(n_tok * f, 256)), dim3(256), 0, s, h, n_tok * f);
+    LAUNCH_TRY("k_gelu");
+    RW_TRY(run_matmul(L.fc2, h, n_tok, L.fc2_b, prj, act, s));
+    RW_TRY(launch_add(x, prj, cnt, s));
+  }
+  return launch_layernorm(x, n_tok, n, d->p.ln_w, d->p.ln_b, hidden, s);
 }
 
 // ------------------------------------------------------ encoder layer
@@ -1328,6 +1488,164 @@ int rw_rocm_attention(const float *q, const float *k, const float *v, size_t t_q
   }
   HIP_TRY(hipMemcpyAsync(out, dout, t_q * n_state * 4, hipMemcpyDeviceToHost, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
+  return RW_OK;
+}
+
+int rw_rocm_decoder_create(const rw_decoder_params *params, size_t n_audio_ctx, rw_decoder **out) {
+  if (!out) return fail(RW_EINVAL, "out is NULL");
+  *out = nullptr;
+  int rc = check_decoder_params(params);
+  if (rc) return rc;
+  if (n_audio_ctx == 0 || n_audio_ctx > (1u << 20)) return fail(RW_EINVAL, "n_audio_ctx = %zu", n_audio_ctx);
+  HIP_TRY(hipSetDevice(params->token_embedding->device));
+  rw_decoder *d = new rw_decoder();
+  d->p = *params;
+  d->layers.assign(params->layers, params->layers + params->n_layer);
+  d->p.layers = d->layers.data();
+  d->device = params->token_embedding->device;
+  d->n = params->token_embedding->k;
+  d->f = params->layers[0].fc1->n;
+  d->n_audio = n_audio_ctx;
+  const size_t kv = (size_t)params->n_layer * 2 * params->n_ctx * d->n * 4;
+  if (hipMalloc(&d->self_kv, kv) != hipSuccess) {
+    (void)hipGetLastError();
+    d->self_kv = nullptr;
+    delete d;
+    return fail(RW_ENOMEM, "hipMalloc(%zu) for the self-attention caches failed", kv);
+  }
+  auto cross = std::make_shared<CrossKV>();
+  cross->device = d->device;
+  cross->n_audio = n_audio_ctx;
+  cross->n = d->n;
+  cross->n_layer = params->n_layer;
+  cross->tkv_pad = (int)align_up(n_audio_ctx, ATT_KVB);
+  cross->plane_bytes = align_up((size_t)params->n_head * ATT_DH * cross->tkv_pad * 2, 256);
+  cross->layer_bytes = 4 * cross->plane_bytes;
+  if (hipMalloc(&cross->buf, cross->layer_bytes * params->n_layer) != hipSuccess) {
+    (void)hipGetLastError();
+    cross->buf = nullptr;
+    delete d;
+    return fail(RW_ENOMEM, "hipMalloc for the cross-attention K/V failed");
+  }
+  d->cross = cross;
+  *out = d;
+  return RW_OK;
+}
+
+void rw_rocm_decoder_free(rw_decoder *d) { delete d; }
+
+static int dec_reserve(rw_decoder *d, size_t bytes) {
+  if (d->scratch_cap >= bytes) return RW_OK;
+  if (d->scratch) HIP_TRY(hipFree(d->scratch));
+  d->scratch = nullptr;
+  d->scratch_cap = 0;
+  const size_t want = align_up(bytes, (size_t)1 << 20);
+  if (hipMalloc(&d->scratch, want) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(RW_ENOMEM, "hipMalloc(%zu) for decoder scratch failed", want);
+  }
+  d->scratch_cap = want;
+  return RW_OK;
+}
+
+int rw_rocm_decoder_set_audio_dev(rw_decoder *d, const float *enc_out, void *stream) {
+  if (!d || !enc_out) return fail(RW_EINVAL, "decoder or encoder output is NULL");
+  if (d->cross.use_count() > 1) return fail(RW_EINVAL, "the cross K/V are shared with a fork; set audio on a fresh decoder");
+  HIP_TRY(hipSetDevice(d->device));
+  hipStream_t s = (hipStream_t)stream;
+  const size_t T = d->n_audio, n = d->n;
+  // k and v f32 for one layer, the activation workspace, then splitting
+  const AttnLayout A = attn_layout(1, T, n);
+  const size_t off_k = 0, off_v = align_up(T * n * 4, 256), off_act = align_up(off_v + T * n * 4, 256);
+  const size_t bytes = align_up(off_act + act_layout(T, n).bytes, 256);
+  int rc = dec_reserve(d, bytes);
+  if (rc) return rc;
+  char *b = (char *)d->scratch;
+  float *kf = (float *)(b + off_k), *vf = (float *)(b + off_v);
+  for (int l = 0; l < d->p.n_layer; ++l) {
+    const rw_decoder_layer &L = d->layers[l];
+    RW_TRY(run_matmul(L.ck, enc_out, T, nullptr, kf, b + off_act, s));  // the key has no bias
+    RW_TRY(run_matmul(L.cv, enc_out, T, L.cv_b, vf, b + off_act, s));
+    const AttnPlanes cp = d->cross->planes(l);
+    AttnPlanes P{nullptr, nullptr, cp.kh, cp.kl, cp.vh, cp.vl, A.tq_pad, cp.tkv_pad};
+    const size_t nk = (size_t)d->p.n_head * cp.tkv_pad * 8;
+    const int wk = (int)cdiv(nk, 256);
+    hipLaunchKernelGGL(k_attn_split, dim3((unsigned)(2 * wk)), dim3(256), 0, s, nullptr, (int)n, 0, kf, (int)n, vf,
+                       (int)n, (int)T, P, d->p.n_head, 0, wk);
+    LAUNCH_TRY("k_attn_split");
+  }
+  d->audio = true;
+  d->n_past = 0;
+  return RW_OK;
+}
+
+int rw_rocm_decoder_reset(rw_decoder *d) {
+  if (!d) return fail(RW_EINVAL, "decoder is NULL");
+  d->n_past = 0;
+  return RW_OK;
+}
+
+int rw_rocm_decoder_n_past(const rw_decoder *d, size_t *n_past) {
+  if (!d || !n_past) return fail(RW_EINVAL, "decoder or n_past is NULL");
+  *n_past = d->n_past;
+  return RW_OK;
+}
+
+int rw_rocm_decoder_fork(const rw_decoder *d, void *stream, rw_decoder **out) {
+  if (!d || !out) return fail(RW_EINVAL, "decoder or out is NULL");
+  *out = nullptr;
+  HIP_TRY(hipSetDevice(d->device));
+  rw_decoder *c = new rw_decoder();
+  c->p = d->p;
+  c->layers = d->layers;
+  c->p.layers = c->layers.data();
+  c->device = d->device;
+  c->n = d->n, c->f = d->f, c->n_audio = d->n_audio, c->n_past = d->n_past;
+  c->cross = d->cross;
+  c->audio = d->audio;
+  const size_t kv = (size_t)d->p.n_layer * 2 * d->p.n_ctx * d->n * 4;
+  if (hipMalloc(&c->self_kv, kv) != hipSuccess) {
+    (void)hipGetLastError();
+    c->self_kv = nullptr;
+    delete c;
+    return fail(RW_ENOMEM, "hipMalloc(%zu) for the forked caches failed", kv);
+  }
+  if (d->n_past) {
+    const size_t rows = d->n_past * d->n * 4;  // copy only the filled rows of each cache
+    for (int l = 0; l < d->p.n_layer; ++l) {
+      hipError_t e = hipMemcpyAsync(c->self_k(l), d->self_k(l), rows, hipMemcpyDeviceToDevice, (hipStream_t)stream);
+      if (e == hipSuccess)
+        e = hipMemcpyAsync(c->self_v(l), d->self_v(l), rows, hipMemcpyDeviceToDevice, (hipStream_t)stream);
+      if (e != hipSuccess) {
+        delete c;
+        return fail(RW_EHIP, "fork copy: %s", hipGetErrorString(e));
+      }
+    }
+  }
+  *out = c;
+  return RW_OK;
+}
+
+int rw_rocm_decoder_forward_hidden_dev(rw_decoder *d, const uint32_t *tokens, size_t n_tok, float *hidden,
+                                       void *stream) {
+  if (!d || !tokens || !hidden) return fail(RW_EINVAL, "decoder, tokens or hidden is NULL");
+  if (n_tok == 0) return fail(RW_EINVAL, "n_tok must be positive");
+  if (!d->audio) return fail(RW_EINVAL, "no audio window: call rw_rocm_decoder_set_audio_dev first");
+  if (d->n_past + n_tok > (size_t)d->p.n_ctx)
+    return fail(RW_EINVAL, "decoder context overflow: %zu + %zu > %d", d->n_past, n_tok, d->p.n_ctx);
+  const size_t n_vocab = d->p.token_embedding->n;
+  for (size_t i = 0; i < n_tok; ++i)
+    if (tokens[i] >= n_vocab) return fail(RW_EINVAL, "token id %u out of range", tokens[i]);
+  HIP_TRY(hipSetDevice(d->device));
+  const DecScratch S = dec_scratch(d, n_tok);
+  int rc = dec_reserve(d, S.bytes);
+  if (rc) return rc;
+  char *b = (char *)d->scratch;
+  hipStream_t s = (hipStream_t)stream;
+  HIP_TRY(hipMemcpyAsync(b + S.off_tok, tokens, n_tok * 4, hipMemcpyHostToDevice, s));
+  rc = decoder_forward(d, n_tok, hidden, b, S, s);
+  if (rc) return rc;
+  d->n_past += n_tok;
   return RW_OK;
 }
 
