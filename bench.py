@@ -309,6 +309,61 @@ def time_encoder_layers(A, torch, W, stream, steps: int, warmup: int):
     return e0.elapsed_time(e1) / steps, ok
 
 
+def time_decoder_tokens(A, synth, torch, D, stream, steps: int):
+    """The large-v3 decoder on the device, one beam: rw_decoder with the
+    decode workload's weights (32 layers x 10 linears, the token embedding as
+    both embedding and logits head), random layernorm and bias vectors, a
+    [1500, 1280] encoder output.  Returns (ms for set_audio, ms per token
+    for forward_hidden + the logits product)."""
+    cfg = synth.LARGE_V3
+    d, layers, vocab = cfg["d"], cfg["layers"], cfg["n_vocab"]
+    keep = D["keep"]
+    per = 10  # linears per layer, in decoder_layer_shapes order
+    names = ("q", "k", "v", "out", "cq", "ck", "cv", "cout", "fc1", "fc2")
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(31)
+    vec = lambda k, c=0.0: torch.randn(k, device="cuda:0", generator=g) * 0.1 + c  # noqa: E731
+    lay = []
+    for l in range(layers):
+        L = {nm: keep[4 * (per * l + i)] for i, nm in enumerate(names)}
+        for nm in ("attn_ln", "cross_ln", "mlp_ln"):
+            L[nm + "_w"], L[nm + "_b"] = vec(d, 1.0), vec(d)
+        for nm in ("q_b", "v_b", "out_b", "cq_b", "cv_b", "cout_b", "fc2_b"):
+            L[nm] = vec(d)
+        L["fc1_b"] = vec(4 * d)
+        lay.append(L)
+    emb = keep[4 * per * layers]
+    dec = A.Decoder(d // 64, 448, 1500, lay, emb, vec(448 * d), vec(d, 1.0), vec(d))
+    enc = torch.randn(1500, d, device="cuda:0", generator=g)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dec.set_audio(enc, stream)
+    torch.cuda.synchronize()
+    t_audio = (time.perf_counter() - t0) * 1e3
+    hid = torch.empty(4, d, device="cuda:0")
+    logits = torch.empty(1, vocab, device="cuda:0")
+    dec.forward_hidden([50258, 50259, 50359], hid[:3], stream)
+    tok = 50363
+
+    def one():
+        dec.forward_hidden([tok], hid[:1], stream)
+        emb.matmul_dev(hid[:1], 1, logits, stream=stream)
+
+    one()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        one()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    ok = bool(torch.isfinite(logits).all().item())
+    dec.free()
+    return t_audio, ms, ok
+
+
 def time_model_load(A, synth, dtype: int, path: str, reps: int = 2):
     """rw_rocm_model_load on a ggml .bin holding large-v3's quantized matrices
     (32 encoder layers x 6 linears, 32 decoder layers x 10, the token
@@ -521,6 +576,18 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "frac": round(gbs / HBM_PEAK_GBS, 4),
         }
+        if not args.no_layers:
+            t_audio, tok_ms, finite = time_decoder_tokens(A, synth, torch, D, stream, 20)
+            log(f"decoder on the device: set_audio {t_audio:.2f} ms, {tok_ms:.3f} ms per token with logits "
+                f"(finite={finite})")
+            result["decoder_tokens"] = {
+                "workload": "large-v3 decoder, one beam, Q5_0: per token the embedding, 32 layers (causal "
+                            "self-attention over the cache, cross-attention to 1500 positions, MLP), final "
+                            "layernorm and the [51866 x 1280] logits product, all on the device (rw_decoder)",
+                "ms_per_token": round(tok_ms, 4),
+                "set_audio_ms": round(t_audio, 3),
+                "finite": finite,
+            }
         del D
         torch.cuda.empty_cache()
 

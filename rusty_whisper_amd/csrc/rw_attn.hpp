@@ -185,8 +185,13 @@ __device__ inline void att_load_v(const AttnPlanes &P, int head, int blk, int h,
 // Workgroup (blockIdx.x, blockIdx.y) = (ATT_QB query rows from q0, head).
 // Wavefront w takes kv blocks w, w + 2, ...; a causal query row i (at
 // absolute position t_kv - t_q + i) sees kv rows up to its position.
+//
+// Split kv (few query blocks, e.g. one decoding step): with part != NULL,
+// workgroup z of gridDim.z takes the z-th run of the kv blocks and writes
+// its unnormalized O (2^12-scaled), running maximum and sum to part;
+// k_attn_combine merges the runs.
 __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, int causal,
-                                              float *__restrict__ out, int ld_out) {
+                                              float *__restrict__ out, int ld_out, float *__restrict__ part) {
   constexpr float LOG2E = 1.4426950408889634f;
   constexpr float NEG_INF = -__builtin_huge_valf();
   __shared__ __align__(16) float xo[ATT_QB * (ATT_DH + 4)];  // partial O^T exchange, then the output tile
@@ -208,7 +213,10 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
   }
   const int off = t_kv - t_q;  // absolute position of query row 0
   const int kv_end = causal ? min(t_kv, off + q0 + ATT_QB) : t_kv;
-  const int nblk = (kv_end + ATT_KVB - 1) / ATT_KVB;
+  const int nblk_all = (kv_end + ATT_KVB - 1) / ATT_KVB;
+  const int cs = (nblk_all + gridDim.z - 1) / gridDim.z;       // blocks per split
+  const int b_begin = min(nblk_all, (int)blockIdx.z * cs);
+  const int nblk = min(nblk_all, b_begin + cs);               // this workgroup: blocks [b_begin, nblk)
 
   att_v8h qh[ATT_QT][4], ql[ATT_QT][4];
 #pragma unroll
@@ -234,8 +242,8 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
   // after the scores and the softmax
   AttK cur, nxt;
   AttV vb;
-  if (wv < nblk) att_load_k(P, head, wv, h, n, cur);
-  for (int b = wv; b < nblk; b += 2) {
+  if (b_begin + wv < nblk) att_load_k(P, head, b_begin + wv, h, n, cur);
+  for (int b = b_begin + wv; b < nblk; b += 2) {
     att_load_v(P, head, b, h, n, vb);
     if (b + 2 < nblk) att_load_k(P, head, b + 2, h, n, nxt);
     // both query tiles' scores first, so the softmax of one tile can run on
@@ -320,7 +328,13 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
       const float s0 = __builtin_amdgcn_exp2f((m[qt] - mu) * LOG2E), s1 = __builtin_amdgcn_exp2f((m1 - mu) * LOG2E);
       float lt = lsum[qt] * s0 + l1 * s1;
       lt += __shfl_xor(lt, 32);
-      const float inv = 1.0f / (lt * ATT_PS);
+      const float inv = part ? 1.0f : 1.0f / (lt * ATT_PS);
+      if (part && h == 0 && q0 + qt * 32 + n < t_q) {
+        const size_t pr = ((size_t)blockIdx.z * gridDim.y + head) * P.tq_pad + q0 + qt * 32 + n;
+        float *pml = part + (size_t)gridDim.z * gridDim.y * P.tq_pad * ATT_DH;
+        pml[2 * pr] = mm;
+        pml[2 * pr + 1] = lt;
+      }
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
@@ -346,10 +360,39 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
   for (int it = 0; it < ATT_QB * 16 / 128; ++it) {
     const int c = it * 128 + (int)threadIdx.x;
     const int row = c >> 4, c4 = c & 15;
-    if (q0 + row < t_q)
-      *reinterpret_cast<float4 *>(out + (size_t)(q0 + row) * ld_out + head * ATT_DH + 4 * c4) =
-          *reinterpret_cast<const float4 *>(&xo[row * LD + 4 * c4]);
+    if (q0 + row < t_q) {
+      float *dst = part ? part + (((size_t)blockIdx.z * gridDim.y + head) * P.tq_pad + q0 + row) * ATT_DH + 4 * c4
+                        : out + (size_t)(q0 + row) * ld_out + head * ATT_DH + 4 * c4;
+      *reinterpret_cast<float4 *>(dst) = *reinterpret_cast<const float4 *>(&xo[row * LD + 4 * c4]);
+    }
   }
+}
+
+// Merge nsplit runs of k_attn: out = sum_z O_z 2^(m_z - m) / (2^12 sum_z l_z
+// 2^(m_z - m)), m the largest run maximum (runs that saw nothing have
+// m = -inf and weigh 0).  One thread per (query, head, d).
+__global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ part, int nsplit, int n_head,
+                                                      int tq_pad, int t_q, float *__restrict__ out, int ld_out) {
+  constexpr float LOG2E = 1.4426950408889634f;
+  constexpr float NEG_INF = -__builtin_huge_valf();
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (size_t)t_q * n_head * ATT_DH) return;
+  const int d = (int)(idx % ATT_DH);
+  const int head = (int)((idx / ATT_DH) % n_head), q = (int)(idx / ((size_t)ATT_DH * n_head));
+  const float *pml = part + (size_t)nsplit * n_head * tq_pad * ATT_DH;
+  float mx = NEG_INF;
+  for (int z = 0; z < nsplit; ++z) mx = fmaxf(mx, pml[2 * (((size_t)z * n_head + head) * tq_pad + q)]);
+  const float mu = mx == NEG_INF ? 0.0f : mx;
+  float num = 0.0f, den = 0.0f;
+  for (int z = 0; z < nsplit; ++z) {
+    const size_t pr = ((size_t)z * n_head + head) * tq_pad + q;
+    const float w = __builtin_amdgcn_exp2f((pml[2 * pr] - mu) * LOG2E);
+    if (w > 0.0f) {  // a run that saw no key holds no output
+      num += part[pr * ATT_DH + d] * w;
+      den += pml[2 * pr + 1] * w;
+    }
+  }
+  out[(size_t)q * ld_out + head * ATT_DH + d] = num / (den * ATT_PS);
 }
 
 #endif  // __HIPCC__

@@ -673,8 +673,8 @@ static int check_matmul_args(const rw_weight *w, const void *a, size_t m, size_t
 
 // Workspace of one attention call: the f16 pairs of q, k and v^T.
 struct AttnLayout {
-  int n_head, tq_pad, tkv_pad;
-  size_t off_qh, off_ql, off_kh, off_kl, off_vh, off_vl, bytes;
+  int n_head, tq_pad, tkv_pad, nsplit;
+  size_t off_qh, off_ql, off_kh, off_kl, off_vh, off_vl, off_part, bytes;
 };
 
 static AttnLayout attn_layout(size_t t_q, size_t t_kv, size_t n_state) {
@@ -689,7 +689,15 @@ static AttnLayout attn_layout(size_t t_q, size_t t_kv, size_t n_state) {
   L.off_kl = align_up(L.off_kh + kb, 256);
   L.off_vh = align_up(L.off_kl + kb, 256);
   L.off_vl = align_up(L.off_vh + kb, 256);
-  L.bytes = align_up(L.off_vl + kb, 256);
+  // few (query block, head) workgroups -- a decoding step: split the kv
+  // blocks over up to 16 workgroups each, merged by k_attn_combine
+  const size_t groups = (size_t)(L.tq_pad / ATT_QB) * L.n_head, nblk = cdiv(t_kv, ATT_KVB);
+  L.nsplit = 1;
+  if (groups < 256 && nblk >= 8)
+    L.nsplit = (int)std::min<size_t>(16, std::min(nblk / 4, cdiv(512, groups)));
+  L.off_part = align_up(L.off_vl + kb, 256);
+  const size_t part = L.nsplit > 1 ? (size_t)L.nsplit * L.n_head * L.tq_pad * (ATT_DH + 2) * 4 : 0;
+  L.bytes = align_up(L.off_part + part, 256);
   return L;
 }
 
@@ -739,9 +747,16 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
   hipLaunchKernelGGL(k_attn_split, dim3((unsigned)(wq + wk + wv)), dim3(256), 0, s, q, (int)ldq, (int)t_q, k,
                      (int)ldk, v, (int)ldv, (int)t_kv, P, n_head, wq, wk);
   LAUNCH_TRY("k_attn_split");
-  hipLaunchKernelGGL(k_attn, dim3((unsigned)(L.tq_pad / ATT_QB), (unsigned)n_head), dim3(128), 0, s, P, (int)t_q,
-                     (int)t_kv, causal ? 1 : 0, out, (int)ldo);
+  float *part = L.nsplit > 1 ? (float *)(b + L.off_part) : nullptr;
+  hipLaunchKernelGGL(k_attn, dim3((unsigned)(L.tq_pad / ATT_QB), (unsigned)n_head, (unsigned)L.nsplit), dim3(128), 0, s,
+                     P, (int)t_q, (int)t_kv, causal ? 1 : 0, out, (int)ldo, part);
   LAUNCH_TRY("k_attn");
+  if (part) {
+    const size_t nz = t_q * (size_t)n_head * ATT_DH;
+    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)cdiv(nz, 256)), dim3(256), 0, s, part, L.nsplit, n_head,
+                       L.tq_pad, (int)t_q, out, (int)ldo);
+    LAUNCH_TRY("k_attn_combine");
+  }
   return RW_OK;
 }
 

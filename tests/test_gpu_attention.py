@@ -70,6 +70,8 @@ SHAPES = [
     (1, 1500, 1280, 20, False, 1.0),     # cross-attention, one token
     (130, 130, 192, 3, True, 2.0),
     (200, 300, 128, 2, False, 1e-3),     # small values: f16 residuals would be subnormal
+    (5, 448, 384, 6, True, 1.0),         # split kv (few query blocks), causal
+    (2, 1500, 384, 6, False, 2.0),       # split kv over 11 runs
 ]
 
 
