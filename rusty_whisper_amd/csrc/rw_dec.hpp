@@ -1,6 +1,7 @@
 // rw_dec.hpp -- the small element-wise kernels of the decoder step (device
-// code): the token + position embedding, a float32 layernorm, the residual
-// add and GELU.  The products and attention are the kernels of
+// code): the token + position embedding, a float32 layernorm (with the
+// residual add of src/decoder.rs:168-170, 191-193 and mlp_block folded in
+// front of it) and GELU.  The products and attention are the kernels of
 // rw_kernels.hpp and rw_attn.hpp.
 #pragma once
 #include <stdint.h>
@@ -33,12 +34,19 @@ __global__ __launch_bounds__(256) void k_embed(WeightView w, const int *__restri
 
 // y = layernorm(x) row by row (src/tensor.rs:274-287): mean, mean of squared
 // deviations, inv = 1 / sqrt(var + 1e-5), (x - mean) * inv * w + b; the sums
-// in tree order.  One workgroup per row.
-__global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, int n, const float *__restrict__ w,
-                                                   const float *__restrict__ b, float *__restrict__ y) {
+// in tree order.  One workgroup per row.  With r != NULL the residual add
+// comes first: x += r (stored back), then y = layernorm(x).
+__global__ __launch_bounds__(256) void k_layernorm(float *__restrict__ x, int n, const float *__restrict__ w,
+                                                   const float *__restrict__ b, float *__restrict__ y,
+                                                   const float *__restrict__ r) {
   __shared__ float part[2][4];
   const int row = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
-  const float *xr = x + (size_t)row * n;
+  float *xr = x + (size_t)row * n;
+  if (r) {
+    const float *rr = r + (size_t)row * n;
+    for (int c = t; c < n; c += 256) xr[c] = xr[c] + rr[c];
+    __syncthreads();
+  }
   auto reduce = [&](float v, int slot) {
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
@@ -58,12 +66,6 @@ __global__ __launch_bounds__(256) void k_layernorm(const float *__restrict__ x, 
   const float inv = __fdiv_rn(1.0f, __fsqrt_rn(var + 1e-5f));
   float *yr = y + (size_t)row * n;
   for (int c = t; c < n; c += 256) yr[c] = (xr[c] - mean) * inv * w[c] + b[c];
-}
-
-// x += y (the residual adds of src/decoder.rs:168-170, 191-193 and mlp_block)
-__global__ __launch_bounds__(256) void k_add(float *__restrict__ x, const float *__restrict__ y, size_t n) {
-  const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t < n) x[t] = x[t] + y[t];
 }
 
 // h = gelu(h), the tanh form of src/tensor.rs:289-305 in its order

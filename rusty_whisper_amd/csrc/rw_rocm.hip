@@ -843,15 +843,11 @@ static DecScratch dec_scratch(const rw_decoder *d, size_t n_tok) {
   return S;
 }
 
-static int launch_layernorm(const float *x, size_t rows, size_t n, const float *w, const float *b, float *y,
-                            hipStream_t s) {
-  hipLaunchKernelGGL(k_layernorm, dim3((unsigned)rows), dim3(256), 0, s, x, (int)n, w, b, y);
+// y = layernorm(x (+= r first when r is given))
+static int launch_layernorm(float *x, size_t rows, size_t n, const float *w, const float *b, float *y,
+                            hipStream_t s, const float *r = nullptr) {
+  hipLaunchKernelGGL(k_layernorm, dim3((unsigned)rows), dim3(256), 0, s, x, (int)n, w, b, y, r);
   LAUNCH_TRY("k_layernorm");
-  return RW_OK;
-}
-static int launch_add(float *x, const float *y, size_t cnt, hipStream_t s) {
-  hipLaunchKernelGGL(k_add, dim3((unsigned)cdiv(cnt, 256)), dim3(256), 0, s, x, y, cnt);
-  LAUNCH_TRY("k_add");
   return RW_OK;
 }
 
@@ -862,7 +858,7 @@ static int launch_add(float *x, const float *y, size_t cnt, hipStream_t s) {
   } while (0)
 
 static int decoder_forward(rw_decoder *d, size_t n_tok, float *hidden, char *b, const DecScratch &S, hipStream_t s) {
-  const size_t n = d->n, f = d->f, cnt = n_tok * n;
+  const size_t n = d->n, f = d->f;
   const int *tok = (const int *)(b + S.off_tok);
   float *x = (float *)(b + S.off_x), *cur = (float *)(b + S.off_cur), *q = (float *)(b + S.off_q);
   float *att = (float *)(b + S.off_a), *prj = (float *)(b + S.off_p), *h = (float *)(b + S.off_h);
@@ -882,34 +878,34 @@ static int decoder_forward(rw_decoder *d, size_t n_tok, float *hidden, char *b, 
 #undef RW_EMB
   LAUNCH_TRY("k_embed");
   const size_t t_kv = d->n_past + n_tok;
+  bool pending = false;  // prj holds a residual not yet added to x
   for (int l = 0; l < d->p.n_layer; ++l) {
     const rw_decoder_layer &L = d->layers[l];
     // causal self-attention over the cache and the new rows
-    RW_TRY(launch_layernorm(x, n_tok, n, L.attn_ln_w, L.attn_ln_b, cur, s));
+    RW_TRY(launch_layernorm(x, n_tok, n, L.attn_ln_w, L.attn_ln_b, cur, s, pending ? prj : nullptr));
     RW_TRY(run_matmul(L.q, cur, n_tok, L.q_b, q, act, s));
     RW_TRY(run_matmul(L.k, cur, n_tok, nullptr, d->self_k(l) + d->n_past * n, act, s));
     RW_TRY(run_matmul(L.v, cur, n_tok, L.v_b, d->self_v(l) + d->n_past * n, act, s));
     RW_TRY(run_attention(q, n, d->self_k(l), n, d->self_v(l), n, n_tok, t_kv, d->p.n_head, 1, att, n, S.self_att,
                          aws, s));
     RW_TRY(run_matmul(L.out, att, n_tok, L.out_b, prj, act, s));
-    RW_TRY(launch_add(x, prj, cnt, s));
-    // cross-attention to the window's K/V
-    RW_TRY(launch_layernorm(x, n_tok, n, L.cross_ln_w, L.cross_ln_b, cur, s));
+    // cross-attention to the window's K/V (the residual add fused into the layernorm)
+    RW_TRY(launch_layernorm(x, n_tok, n, L.cross_ln_w, L.cross_ln_b, cur, s, prj));
     RW_TRY(run_matmul(L.cq, cur, n_tok, L.cq_b, q, act, s));
     const AttnPlanes cp = d->cross->planes(l);
     RW_TRY(run_attention(q, n, nullptr, n, nullptr, n, n_tok, d->n_audio, d->p.n_head, 0, att, n, S.cross_att, aws,
                          s, &cp));
     RW_TRY(run_matmul(L.cout, att, n_tok, L.cout_b, prj, act, s));
-    RW_TRY(launch_add(x, prj, cnt, s));
     // MLP
-    RW_TRY(launch_layernorm(x, n_tok, n, L.mlp_ln_w, L.mlp_ln_b, cur, s));
+    RW_TRY(launch_layernorm(x, n_tok, n, L.mlp_ln_w, L.mlp_ln_b, cur, s, prj));
     RW_TRY(run_matmul(L.fc1, cur, n_tok, L.fc1_b, h, act, s));
     hipLaunchKernelGGL(k_gelu, dim3((unsigned)cdiv(n_tok * f, 256)), dim3(256), 0, s, h, n_tok * f);
     LAUNCH_TRY("k_gelu");
     RW_TRY(run_matmul(L.fc2, h, n_tok, L.fc2_b, prj, act, s));
-    RW_TRY(launch_add(x, prj, cnt, s));
+    // the MLP's residual add goes into the next layer's first layernorm
+    pending = true;
   }
-  return launch_layernorm(x, n_tok, n, d->p.ln_w, d->p.ln_b, hidden, s);
+  return launch_layernorm(x, n_tok, n, d->p.ln_w, d->p.ln_b, hidden, s, pending ? prj : nullptr);
 }
 
 // ------------------------------------------------------ encoder layer
