@@ -366,11 +366,16 @@ static int run_gemm(const rw_weight *const *w, const float *const *bias, float *
 
 // ------------------------------------------------------ decode GEMV
 
-// The split of a row's octets over wavefronts depends on the weight only:
-// split while every wavefront keeps at least 4 octets.
-static int gemv_ks(const rw_weight *w) {
+// The split of a row's octets over wavefronts depends on the weight and the
+// launch form only.  Grouped launches have workgroups to spare and split
+// while every wavefront keeps at least 4 octets; a single linear's launch
+// is short of workgroups at decode sizes (5 for a 1280-row weight) and
+// splits while every wavefront keeps 2, which halves its latency.  The two
+// forms then differ only by the f32 reassociation of the parts' sums.
+static int gemv_ks(const rw_weight *w, bool single = false) {
+  const int keep = single ? 2 : 4;
   int ks = 1;
-  while (ks < 4 && w->noct / (2 * ks) >= 4) ks *= 2;
+  while (ks < 4 && w->noct / (2 * ks) >= keep) ks *= 2;
   return ks;
 }
 static int gemv_wgs(const rw_weight *w, int ks) { return (int)cdiv(w->ngroups, GEMV_NG * (4 / ks)); }
@@ -383,8 +388,8 @@ static int gemv_wgs(const rw_weight *w, int ks) { return (int)cdiv(w->ngroups, G
 #ifndef GEMV_LDS_CAP
 #define GEMV_LDS_CAP 32768
 #endif
-static int gemv_need(const rw_weight *w) {
-  const int ks = gemv_ks(w);
+static int gemv_need(const rw_weight *w, bool single = false) {
+  const int ks = gemv_ks(w, single);
   return ks * (int)cdiv(w->noct, ks);
 }
 static int gemv_cap(int m, int need) {
@@ -393,14 +398,14 @@ static int gemv_cap(int m, int need) {
   return need < cap ? need : cap;
 }
 
-static GemvItem gemv_item(const rw_weight *w, const float *a, const float *bias, float *out) {
+static GemvItem gemv_item(const rw_weight *w, const float *a, const float *bias, float *out, bool single = false) {
   GemvItem it{};
   it.w = w->view;
   it.a = a;
   it.bias = bias;
   it.out = out;
   it.n = (int)w->n;
-  const int ks = gemv_ks(w);
+  const int ks = gemv_ks(w, single);
   it.lks = ks == 4 ? 2 : ks == 2 ? 1 : 0;
   return it;
 }
@@ -448,12 +453,13 @@ static int run_product(const rw_weight *w, size_t m, const float *bias, float *o
   ActLayout L = act_layout(m, w->k);
   ActView av = act_view(L, (void *)ws);
   if (m <= GEMV_MAX_M) {
-    GemvItem one = gemv_item(w, nullptr, bias, out);
+    GemvItem one = gemv_item(w, nullptr, bias, out, true);
     one.qa = av.qa;
     one.qda = av.da;
     one.qpa = av.pa;
     one.qsa = av.sa;
-    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, gemv_wgs(w, gemv_ks(w)), gemv_cap((int)m, gemv_need(w)), s);
+    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, gemv_wgs(w, gemv_ks(w, true)), gemv_cap((int)m, gemv_need(w, true)),
+                     s);
     LAUNCH_TRY("k_gemv");
   } else {
     return run_gemm(&w, &bias, &out, 1, av, (int)m, s);
@@ -467,8 +473,9 @@ static int run_matmul(const rw_weight *w, const float *a, size_t m, const float 
                       hipStream_t s) {
   if (m == 0) return RW_OK;
   if (m <= GEMV_MAX_M) {
-    GemvItem one = gemv_item(w, a, bias, out);
-    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, gemv_wgs(w, gemv_ks(w)), gemv_cap((int)m, gemv_need(w)), s);
+    GemvItem one = gemv_item(w, a, bias, out, true);
+    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, gemv_wgs(w, gemv_ks(w, true)), gemv_cap((int)m, gemv_need(w, true)),
+                     s);
     LAUNCH_TRY("k_gemv");
     return RW_OK;
   }

@@ -12,8 +12,10 @@ Bars (written in each test):
   * quantizing inside the decode launch and quantizing separately
     (rw_rocm_quantize_dev + rw_rocm_matmul_prequant_dev) give bitwise the
     same outputs, in both regimes;
-  * a grouped launch and a prepared group give, per item, bitwise what the
-    same linear gives alone;
+  * a prepared group gives bitwise what a grouped launch gives; both give,
+    per item, what the same linear gives alone up to the f32 reassociation
+    of the k-split parts (a single linear splits k over more wavefronts):
+    within 1e-6 of the row's L2 norm;
   * device and host entry points agree bitwise;
   * outputs stay within 1e-3 of the reference CPU path (max error over the
     reference row's L2 norm), also when the activations go through LDS in
@@ -117,7 +119,7 @@ def _group_items(torch, specs, seed):
     return items, host
 
 
-def test_grouped_matches_single_bitwise(torch):
+def test_grouped_matches_single(torch):
     items, host = _group_items(torch, GROUP, seed=900)
     arr = A.make_linears(items)
     wsz = A.grouped_workspace_size(arr)
@@ -129,7 +131,7 @@ def test_grouped_matches_single_bitwise(torch):
             assert torch.isnan(out).all(), "an m = 0 entry must write nothing"
             continue
         got = out.cpu().numpy()
-        assert np.array_equal(_bits(got), _bits(_single(torch, w, a, b))), (w.dtype, m, w.n, w.k)
+        assert rel_row_l2(got, _single(torch, w, a, b)) <= 1e-6, (w.dtype, m, w.n, w.k)
         ref = O.matmul_emul(a, w.dtype, raw, w.n, bias=b)
         assert rel_row_l2(got, ref) <= NORTH_STAR_TOL, (w.dtype, m, w.n, w.k)
 
@@ -165,7 +167,7 @@ def test_grouped_back_to_back_calls_keep_their_tables(torch):
     for items, host in ((items1, host1), (items2, host2)):
         for (w, _, _, out, m), (_, a, b, _) in zip(items, host):
             if m:
-                assert np.array_equal(_bits(out.cpu().numpy()), _bits(_single(torch, w, a, b)))
+                assert rel_row_l2(out.cpu().numpy(), _single(torch, w, a, b)) <= 1e-6
 
 
 @pytest.mark.parametrize("dtype", [2, 7], ids=["Q4_0", "Q5_1"])
