@@ -290,23 +290,41 @@ def time_encoder_layers(A, torch, W, stream, steps: int, warmup: int):
     wsz = layers[0].workspace_size(m)
     ws = torch.empty(wsz, dtype=torch.uint8, device="cuda:0")
 
-    def run():
+    def run(s):
         x.copy_(x0)
         for L in layers:
-            L.run(x, m, ws, wsz, stream)
+            L.run(x, m, ws, wsz, s)
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
 
     for _ in range(warmup):
-        run()
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        run()
-    e1.record()
-    torch.cuda.synchronize()
+        run(stream)
+    eager = timed(lambda: run(stream))
     ok = bool(torch.isfinite(x).all().item())
-    return e0.elapsed_time(e1) / steps, ok
+    ref = x.clone()
+    # the same pass captured once and replayed (every launch is a kernel: no
+    # memset, no host wait), checked against the eager result
+    g = torch.cuda.CUDAGraph()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cs):
+        run(cs.cuda_stream)  # warm the capture stream's allocations
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=cs):
+            run(cs.cuda_stream)
+    torch.cuda.current_stream().wait_stream(cs)
+    graph = timed(g.replay)
+    ok = ok and bool(torch.equal(x, ref))
+    return eager, graph, ok
 
 
 def time_decoder_tokens(A, synth, torch, D, stream, steps: int):
@@ -544,15 +562,17 @@ def main() -> int:
         },
     }
     if not args.no_layers:
-        lms, finite = time_encoder_layers(A, torch, W, stream, max(3, args.steps // 2), 1)
-        log(f"32 encoder layers on the device {lms:.3f} ms ({lms * 1e3 / 32:.1f} us per layer, finite={finite})")
+        eager_l, lms, finite = time_encoder_layers(A, torch, W, stream, max(3, args.steps // 2), 1)
+        log(f"32 encoder layers on the device: graph replay {lms:.3f} ms ({lms * 1e3 / 32:.1f} us per layer), "
+            f"eager {eager_l:.3f} ms (finite and replay == eager: {finite})")
         result["encoder_layers"] = {
             "workload": f"large-v3 encoder, 32 layers, {args.quant}, M={args.m}: per layer layernorm + q/k/v + "
                         "attention (20 heads) + out + residual, layernorm + fc1 + GELU + fc2 + residual, all on the "
-                        "device (rw_rocm_encoder_layer_dev)",
+                        "device (rw_rocm_encoder_layer_dev), captured in a HIP graph and replayed",
             "ms_per_pass": round(lms, 4),
             "us_per_layer": round(lms * 1e3 / 32, 2),
-            "finite": finite,
+            "eager_ms_per_pass": round(eager_l, 4),
+            "finite_and_replay_equal": finite,
         }
 
     del W
