@@ -597,6 +597,16 @@ struct GemvItem {
   int pad;
 };
 
+// Up to GEMV_SET linears of one dtype that read one activation, launched
+// together without a device table: workgroups [end[t-1], end[t]) run item t.
+constexpr int GEMV_SET = 4;
+struct GemvSet {
+  GemvItem it[GEMV_SET];
+  int end[GEMV_SET];
+  int count;
+};
+
+
 // LDS record of one activation block for the decode kernel (m = MR rows):
 //   [0, 32 MR)         the rows' int8 quants, MFMA order (the A operand)
 //   [32 MR, +16)       zeros: the A operand of lanes whose row is >= MR
@@ -852,14 +862,34 @@ __device__ inline void gemv_fold_oct(const uint8_t *orec, int a_off, int h, int 
 // zeros) and zero activation records: they add exactly +0.
 template <int DT, int MR, bool GROUPED>
 __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restrict__ items, const int2 *__restrict__ wg_item,
-                                              GemvItem one, int cap_oct) {
+                                              GemvSet one, int cap_oct) {
   extern __shared__ __align__(16) uint8_t lds[];
   constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR;
   constexpr int QB = DT == 8 ? 32 : 16;                // qs bytes per row-block
   // the descriptor is wave-uniform: scalar loads from the table or kernarg
-  const int2 wt = GROUPED ? wg_item[blockIdx.x] : make_int2(0, (int)blockIdx.x);  // (item, tile)
+  int2 wt;  // (item, tile)
+  if constexpr (GROUPED) {
+    wt = wg_item[blockIdx.x];
+  } else {  // the set's item by uniform compares (no runtime index into the argument)
+    int ii = 0;
+#pragma unroll
+    for (int t = 0; t + 1 < GEMV_SET; ++t)
+      if (t + 1 < one.count && (int)blockIdx.x >= one.end[t]) ii = t + 1;
+    int first = 0;
+#pragma unroll
+    for (int t = 0; t + 1 < GEMV_SET; ++t)
+      if (ii == t + 1) first = one.end[t];
+    wt = make_int2(ii, (int)blockIdx.x - first);
+  }
   if (wt.x < 0) return;  // a slot no item uses (the whole workgroup)
-  const GemvItem I = GROUPED ? items[wt.x] : one;
+  GemvItem I = one.it[0];
+  if constexpr (GROUPED) {
+    I = items[wt.x];
+  } else {
+#pragma unroll
+    for (int t = 1; t < GEMV_SET; ++t)
+      if (wt.x == t) I = one.it[t];
+  }
   const WeightView &w = I.w;
   const int nb = w.nb;
   const int lks = I.lks, KS = 1 << lks;

@@ -411,7 +411,7 @@ static GemvItem gemv_item(const rw_weight *w, const float *a, const float *bias,
 }
 
 template <int DT, int MR>
-static void launch_gemv_mr(const GemvItem *items, const int2 *wg_item, const GemvItem &one, int wgs, int cap_oct,
+static void launch_gemv_mr(const GemvItem *items, const int2 *wg_item, const GemvSet &one, int wgs, int cap_oct,
                            hipStream_t s) {
   if (items)
     hipLaunchKernelGGL((k_gemv<DT, MR, true>), dim3((unsigned)wgs), dim3(256), gemv_lds_bytes(MR, cap_oct), s,
@@ -422,9 +422,9 @@ static void launch_gemv_mr(const GemvItem *items, const int2 *wg_item, const Gem
 }
 
 // one k_gemv launch: `items` (device) + `wg_item` (device) for a group, or
-// items == NULL and the single item `one`
+// items == NULL and the set `one` (kernel arguments)
 template <int DT>
-static void launch_gemv_dt(int m, const GemvItem *items, const int2 *wg_item, const GemvItem &one, int wgs,
+static void launch_gemv_dt(int m, const GemvItem *items, const int2 *wg_item, const GemvSet &one, int wgs,
                            int cap_oct, hipStream_t s) {
   switch (m) {
     case 1: launch_gemv_mr<DT, 1>(items, wg_item, one, wgs, cap_oct, s); break;
@@ -453,13 +453,15 @@ static int run_product(const rw_weight *w, size_t m, const float *bias, float *o
   ActLayout L = act_layout(m, w->k);
   ActView av = act_view(L, (void *)ws);
   if (m <= GEMV_MAX_M) {
-    GemvItem one = gemv_item(w, nullptr, bias, out, true);
-    one.qa = av.qa;
-    one.qda = av.da;
-    one.qpa = av.pa;
-    one.qsa = av.sa;
-    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, gemv_wgs(w, gemv_ks(w, true)), gemv_cap((int)m, gemv_need(w, true)),
-                     s);
+    GemvSet one{};
+    one.it[0] = gemv_item(w, nullptr, bias, out, true);
+    one.it[0].qa = av.qa;
+    one.it[0].qda = av.da;
+    one.it[0].qpa = av.pa;
+    one.it[0].qsa = av.sa;
+    one.count = 1;
+    one.end[0] = gemv_wgs(w, gemv_ks(w, true));
+    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, one.end[0], gemv_cap((int)m, gemv_need(w, true)), s);
     LAUNCH_TRY("k_gemv");
   } else {
     return run_gemm(&w, &bias, &out, 1, av, (int)m, s);
@@ -473,9 +475,11 @@ static int run_matmul(const rw_weight *w, const float *a, size_t m, const float 
                       hipStream_t s) {
   if (m == 0) return RW_OK;
   if (m <= GEMV_MAX_M) {
-    GemvItem one = gemv_item(w, a, bias, out, true);
-    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, gemv_wgs(w, gemv_ks(w, true)), gemv_cap((int)m, gemv_need(w, true)),
-                     s);
+    GemvSet one{};
+    one.it[0] = gemv_item(w, a, bias, out, true);
+    one.count = 1;
+    one.end[0] = gemv_wgs(w, gemv_ks(w, true));
+    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, one.end[0], gemv_cap((int)m, gemv_need(w, true)), s);
     LAUNCH_TRY("k_gemv");
     return RW_OK;
   }
@@ -483,6 +487,32 @@ static int run_matmul(const rw_weight *w, const float *a, size_t m, const float 
   int rc = launch_quantize(a, m, w->k, L, ws, s);
   if (rc) return rc;
   return run_product(w, m, bias, out, ws, s);
+}
+
+// several linears of one dtype and k on one activation a: one GEMV launch
+// (kernel-argument set) at m <= 8, else one quantization and one GEMM launch
+static int run_matmul_set(const rw_weight *const *w, size_t count, const float *a, size_t m,
+                          const float *const *bias, float *const *out, void *ws, hipStream_t s) {
+  if (m == 0) return RW_OK;
+  if (count < 1 || count > (size_t)GEMV_SET) return fail(RW_EINVAL, "a set holds 1 to %d linears", GEMV_SET);
+  if (m <= GEMV_MAX_M) {
+    GemvSet set{};
+    int wgs = 0, need = 0;
+    for (size_t i = 0; i < count; ++i) {
+      set.it[i] = gemv_item(w[i], a, bias ? bias[i] : nullptr, out[i], true);
+      wgs += gemv_wgs(w[i], gemv_ks(w[i], true));
+      set.end[i] = wgs;
+      need = std::max(need, gemv_need(w[i], true));
+    }
+    set.count = (int)count;
+    RW_DISPATCH_GEMV(w[0], m, nullptr, nullptr, set, wgs, gemv_cap((int)m, need), s);
+    LAUNCH_TRY("k_gemv");
+    return RW_OK;
+  }
+  ActLayout L = act_layout(m, w[0]->k);
+  int rc = launch_quantize(a, m, w[0]->k, L, ws, s);
+  if (rc) return rc;
+  return run_gemm(w, bias, out, count, act_view(L, ws), (int)m, s);
 }
 
 // ------------------------------------------------- grouped decode GEMV
@@ -644,7 +674,7 @@ static int launch_group(const std::vector<GroupLaunch> &launches, const void *ta
   const GemvItem *dtab = (const GemvItem *)table;
   const int2 *dmap = (const int2 *)((const char *)table + map_off);
   const int2 *qmap = (const int2 *)((const char *)table + qmap_off);
-  const GemvItem none{};
+  const GemvSet none{};
   for (const GroupLaunch &L : launches) {
     switch (L.dt) {
       case RW_Q4_0: launch_records_dt<RW_Q4_0>(L.m, dtab, qmap + L.qwg_first, L.qwgs, s); break;
@@ -890,9 +920,17 @@ static int decoder_forward(rw_decoder *d, size_t n_tok, float *hidden, char *b, 
     const rw_decoder_layer &L = d->layers[l];
     // causal self-attention over the cache and the new rows
     RW_TRY(launch_layernorm(x, n_tok, n, L.attn_ln_w, L.attn_ln_b, cur, s, pending ? prj : nullptr));
-    RW_TRY(run_matmul(L.q, cur, n_tok, L.q_b, q, act, s));
-    RW_TRY(run_matmul(L.k, cur, n_tok, nullptr, d->self_k(l) + d->n_past * n, act, s));
-    RW_TRY(run_matmul(L.v, cur, n_tok, L.v_b, d->self_v(l) + d->n_past * n, act, s));
+    {
+      // q, k and v in one launch; k and v land in the cache rows
+      const rw_weight *w3[3] = {L.q, L.k, L.v};
+      const float *b3[3] = {L.q_b, nullptr, L.v_b};
+      float *o3[3] = {q, d->self_k(l) + d->n_past * n, d->self_v(l) + d->n_past * n};
+      if (L.q->dtype == L.k->dtype && L.q->dtype == L.v->dtype) {
+        RW_TRY(run_matmul_set(w3, 3, cur, n_tok, b3, o3, act, s));
+      } else {
+        for (int i = 0; i < 3; ++i) RW_TRY(run_matmul(w3[i], cur, n_tok, b3[i], o3[i], act, s));
+      }
+    }
     RW_TRY(run_attention(q, n, d->self_k(l), n, d->self_v(l), n, n_tok, t_kv, d->p.n_head, 1, att, n, S.self_att,
                          aws, s));
     RW_TRY(run_matmul(L.out, att, n_tok, L.out_b, prj, act, s));
