@@ -592,9 +592,10 @@ struct GemvItem {
   float *out;
   uint8_t *rec;  // activation records [noct*8][gemv_rec_bytes(m)] written by
                  // k_gemv_records (grouped launches), or NULL
+  const float *lnw, *lnb;  // single / set launches: layernorm the rows of `a` first (or NULL)
   int n;
-  int lks;   // log2 of the number of wavefronts that split a row's octets
-  int pad;
+  int lks;    // log2 of the number of wavefronts that split a row's octets
+  int flags;  // GEMM_GELU, GEMM_ACC: the GEMM's epilogue options
 };
 
 // Up to GEMV_SET linears of one dtype that read one activation, launched
@@ -636,8 +637,11 @@ __device__ inline void gemv_zero_slots(uint8_t *lds, int nslots, int t) {
 // or copied from an already quantized workspace (I.qa).  (block, row) pairs
 // block-major, 4 passes of 32 per batch so their global loads are in flight
 // together.  Records of the tail blocks past nb are zeroed.
+// With I.lnw the rows are layernormed first (mean mu[i], inv iv[i] of row i,
+// then (x - mu) * iv * w + b, src/tensor.rs:274-287) and the result quantized.
 template <int DT, int MR>
-__device__ inline void gemv_fill(const GemvItem &I, int nb, int c0, int c1, uint8_t *base, int t) {
+__device__ inline void gemv_fill(const GemvItem &I, int nb, int c0, int c1, uint8_t *base, int t,
+                                 const float (&mu)[MR], const float (&iv)[MR]) {
   constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR, SO = ZO + 16, DO = SO + 32, PO = DO + 32;
   constexpr int OFF = DT == 2 ? 8 : DT == 6 ? 16 : 0;
   const int bb0 = c0 * OCT, cnb = min(nb, c1 * OCT) - bb0;
@@ -652,6 +656,18 @@ __device__ inline void gemv_fill(const GemvItem &I, int nb, int c0, int c1, uint
         if (rb < total) {
           const int lb = rb / MR, i = rb - lb * MR;
           x[u] = ldg_f4(I.a + ((size_t)i * nb + bb0 + lb) * QK + 4 * lt);
+          if (I.lnw) {
+            float m0 = mu[0], v0 = iv[0];
+#pragma unroll
+            for (int k = 1; k < MR; ++k)
+              if (i == k) m0 = mu[k], v0 = iv[k];
+            const size_t e = (size_t)(bb0 + lb) * QK + 4 * lt;
+            const float4 w4 = ldg_f4(I.lnw + e), b4 = ldg_f4(I.lnb + e);
+            x[u].x = (x[u].x - m0) * v0 * w4.x + b4.x;
+            x[u].y = (x[u].y - m0) * v0 * w4.y + b4.y;
+            x[u].z = (x[u].z - m0) * v0 * w4.z + b4.z;
+            x[u].w = (x[u].w - m0) * v0 * w4.w + b4.w;
+          }
         }
       }
 #pragma unroll
@@ -860,6 +876,18 @@ __device__ inline void gemv_fold_oct(const uint8_t *orec, int a_off, int h, int 
 // depends on its weight row and activation row alone.  Blocks past nb in the
 // last octet meet zero weight planes (the upload writes the padding as
 // zeros) and zero activation records: they add exactly +0.
+// y + bias, then GELU (flag 1) and accumulation into the output (flag 2):
+// the epilogue options the GEMM takes (GEMM_GELU, GEMM_ACC)
+__device__ inline void gemv_store(const GemvItem &I, size_t idx, int col, float y) {
+  if (I.bias) y = y + ldg_f(I.bias + col);
+  if (I.flags & 1) {
+    const float inner = 0.7978846f * (y + 0.044715f * y * y * y);
+    y = 0.5f * y * (1.0f + tanhf(inner));
+  }
+  if (I.flags & 2) y = I.out[idx] + y;
+  stg_f(I.out + idx, y);
+}
+
 template <int DT, int MR, bool GROUPED>
 __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restrict__ items, const int2 *__restrict__ wg_item,
                                               GemvSet one, int cap_oct) {
@@ -911,10 +939,6 @@ __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restri
   const int a_off = r < MR ? 32 * r + 16 * h : ZO;
   const int rot = (32 - 2 * h) & 31;  // rotr by this = rotl by 2h
 
-  // zero the parts of every record slot the fills never write (records
-  // copied whole need none)
-  if (!GROUPED) gemv_zero_slots<MR>(lds, cap_oct * OCT, t);
-
   float acc[GEMV_NG][4], accm[GEMV_NG][4];
 #pragma unroll
   for (int j = 0; j < GEMV_NG; ++j)
@@ -923,6 +947,57 @@ __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restri
       acc[j][v] = 0.0f;
       accm[j][v] = 0.0f;
     }
+
+  // layernorm statistics of the m activation rows (single / set launches
+  // with I.lnw): every workgroup computes them, in the same tree order
+  float ln_mu[MR], ln_iv[MR];
+#pragma unroll
+  for (int i = 0; i < MR; ++i) ln_mu[i] = 0.0f, ln_iv[i] = 0.0f;
+  if constexpr (!GROUPED) {
+    if (I.lnw) {
+      const int K = nb * QK;
+      float *sred = reinterpret_cast<float *>(lds);  // [4 wavefronts][MR], before any record
+      auto row_sums = [&](float (&v)[MR]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < MR; ++i) {
+          float a = v[i];
+#pragma unroll
+          for (int o = 1; o < 64; o <<= 1) a += __shfl_xor(a, o);
+          if (l == 0) sred[wv * MR + i] = a;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < MR; ++i) v[i] = (sred[i] + sred[MR + i]) + (sred[2 * MR + i] + sred[3 * MR + i]);
+        __syncthreads();
+      };
+      float acc_s[MR];
+#pragma unroll
+      for (int i = 0; i < MR; ++i) {
+        float a = 0.0f;
+        for (int c = t; c < K; c += 256) a += I.a[(size_t)i * K + c];
+        acc_s[i] = a;
+      }
+      row_sums(acc_s);
+#pragma unroll
+      for (int i = 0; i < MR; ++i) {
+        ln_mu[i] = __fdiv_rn(acc_s[i], (float)K);
+        float a = 0.0f;
+        for (int c = t; c < K; c += 256) {
+          const float d = I.a[(size_t)i * K + c] - ln_mu[i];
+          a += d * d;
+        }
+        acc_s[i] = a;
+      }
+      row_sums(acc_s);
+#pragma unroll
+      for (int i = 0; i < MR; ++i) ln_iv[i] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(acc_s[i], (float)K) + 1e-5f));
+    }
+  }
+
+  // zero the parts of every record slot the fills never write (records
+  // copied whole need none); after the statistics, whose partial sums use
+  // the start of LDS
+  if (!GROUPED) gemv_zero_slots<MR>(lds, cap_oct * OCT, t);
 
   // chunks: step cc covers octets [s_p + cc, s_p + cc + ch) of every part
   // p (s_p its first octet), in LDS slots [p*ch, (p+1)*ch), so that every
@@ -945,7 +1020,7 @@ __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restri
         for (int z = t; z < (c1 - c0) * OCT * (REC / 16); z += 256)
           reinterpret_cast<uint4 *>(base)[z] = ldg_u4(src + z);
       } else {
-        gemv_fill<DT, MR>(I, nb, c0, c1, base, t);
+        gemv_fill<DT, MR>(I, nb, c0, c1, base, t, ln_mu, ln_iv);
       }
     }
     __syncthreads();
@@ -977,7 +1052,7 @@ __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restri
 #pragma unroll
         for (int v = 0; v < 4; ++v)
           if (4 * h + v < MR)
-            stg_f(I.out + (size_t)(4 * h + v) * n + col, I.bias ? y[j][v] + ldg_f(I.bias + col) : y[j][v]);
+            gemv_store(I, (size_t)(4 * h + v) * n + col, col, y[j][v]);
     }
     return;
   }
@@ -998,7 +1073,7 @@ __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restri
           if (4 * h + v < MR) {
             float tt = red[(wv * 4 * GEMV_NG + 4 * j + v) * 64 + l];
             for (int p = 1; p < KS; ++p) tt = tt + red[((wv + p) * 4 * GEMV_NG + 4 * j + v) * 64 + l];
-            stg_f(I.out + (size_t)(4 * h + v) * n + col, I.bias ? tt + ldg_f(I.bias + col) : tt);
+            gemv_store(I, (size_t)(4 * h + v) * n + col, col, tt);
           }
     }
   }

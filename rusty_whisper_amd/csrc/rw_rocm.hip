@@ -489,10 +489,25 @@ static int run_matmul(const rw_weight *w, const float *a, size_t m, const float 
   return run_product(w, m, bias, out, ws, s);
 }
 
+#define RW_TRY(expr)       \
+  do {                     \
+    int rc_ = (expr);      \
+    if (rc_) return rc_;   \
+  } while (0)
+
+static int launch_layernorm(float *x, size_t rows, size_t n, const float *w, const float *b, float *y,
+                            hipStream_t s, const float *r);
+
 // several linears of one dtype and k on one activation a: one GEMV launch
-// (kernel-argument set) at m <= 8, else one quantization and one GEMM launch
+// (kernel-argument set) at m <= 8, else one quantization and one GEMM launch.
+// With lnw the rows of a are layernormed (lnw, lnb) before they are
+// quantized, inside that launch; `flags` (GEMM_GELU, GEMM_ACC) go to every
+// linear's epilogue.  `tmp` ([m, k] f32, or NULL) takes the layernormed rows
+// where the GEMM's quantizer cannot fold the layernorm (k > 8192).
 static int run_matmul_set(const rw_weight *const *w, size_t count, const float *a, size_t m,
-                          const float *const *bias, float *const *out, void *ws, hipStream_t s) {
+                          const float *const *bias, float *const *out, void *ws, hipStream_t s,
+                          const float *lnw = nullptr, const float *lnb = nullptr, int flags = 0,
+                          float *tmp = nullptr) {
   if (m == 0) return RW_OK;
   if (count < 1 || count > (size_t)GEMV_SET) return fail(RW_EINVAL, "a set holds 1 to %d linears", GEMV_SET);
   if (m <= GEMV_MAX_M) {
@@ -500,6 +515,9 @@ static int run_matmul_set(const rw_weight *const *w, size_t count, const float *
     int wgs = 0, need = 0;
     for (size_t i = 0; i < count; ++i) {
       set.it[i] = gemv_item(w[i], a, bias ? bias[i] : nullptr, out[i], true);
+      set.it[i].lnw = lnw;
+      set.it[i].lnb = lnb;
+      set.it[i].flags = flags;
       wgs += gemv_wgs(w[i], gemv_ks(w[i], true));
       set.end[i] = wgs;
       need = std::max(need, gemv_need(w[i], true));
@@ -509,10 +527,23 @@ static int run_matmul_set(const rw_weight *const *w, size_t count, const float *
     LAUNCH_TRY("k_gemv");
     return RW_OK;
   }
-  ActLayout L = act_layout(m, w[0]->k);
-  int rc = launch_quantize(a, m, w[0]->k, L, ws, s);
-  if (rc) return rc;
-  return run_gemm(w, bias, out, count, act_view(L, ws), (int)m, s);
+  const size_t k = w[0]->k;
+  ActLayout L = act_layout(m, k);
+  if (lnw && (L.nb + 7) / 8 > 32) {  // layernorm in its own launch
+    if (!tmp) return fail(RW_EINVAL, "layernorm + product over k = %zu needs a row buffer", k);
+    RW_TRY(launch_layernorm(const_cast<float *>(a), m, k, lnw, lnb, tmp, s, nullptr));
+    a = tmp;
+    lnw = lnb = nullptr;
+  }
+  RW_TRY(launch_quantize(a, m, k, L, ws, s, lnw, lnb));
+  const int fl[GEMV_SET] = {flags, flags, flags, flags};
+  return run_gemm(w, bias, out, count, act_view(L, ws), (int)m, s, flags ? fl : nullptr);
+}
+
+// one linear (count 1) with the options of run_matmul_set
+static int run_linear(const rw_weight *w, const float *a, size_t m, const float *bias, float *out, void *ws,
+                      hipStream_t s, const float *lnw, const float *lnb, int flags, float *tmp) {
+  return run_matmul_set(&w, 1, a, m, &bias, &out, ws, s, lnw, lnb, flags, tmp);
 }
 
 // ------------------------------------------------- grouped decode GEMV
@@ -859,7 +890,7 @@ static int check_decoder_params(const rw_decoder_params *P) {
 
 // the per-call scratch of forward_hidden for n_tok tokens
 struct DecScratch {
-  size_t off_tok, off_x, off_cur, off_q, off_a, off_p, off_h, off_act, off_att, bytes;
+  size_t off_tok, off_x, off_cur, off_q, off_a, off_h, off_act, off_att, bytes;
   AttnLayout self_att, cross_att;
 };
 static DecScratch dec_scratch(const rw_decoder *d, size_t n_tok) {
@@ -872,8 +903,7 @@ static DecScratch dec_scratch(const rw_decoder *d, size_t n_tok) {
   S.off_cur = align_up(S.off_x + row, 256);
   S.off_q = align_up(S.off_cur + row, 256);
   S.off_a = align_up(S.off_q + row, 256);
-  S.off_p = align_up(S.off_a + row, 256);
-  S.off_h = align_up(S.off_p + row, 256);
+  S.off_h = align_up(S.off_a + row, 256);
   S.off_act = align_up(S.off_h + n_tok * d->f * 4, 256);
   S.off_att = align_up(S.off_act + act_layout(n_tok, std::max(d->n, d->f)).bytes, 256);
   S.bytes = align_up(S.off_att + std::max(S.self_att.bytes, S.cross_att.bytes), 256);
@@ -882,23 +912,17 @@ static DecScratch dec_scratch(const rw_decoder *d, size_t n_tok) {
 
 // y = layernorm(x (+= r first when r is given))
 static int launch_layernorm(float *x, size_t rows, size_t n, const float *w, const float *b, float *y,
-                            hipStream_t s, const float *r = nullptr) {
+                            hipStream_t s, const float *r) {
   hipLaunchKernelGGL(k_layernorm, dim3((unsigned)rows), dim3(256), 0, s, x, (int)n, w, b, y, r);
   LAUNCH_TRY("k_layernorm");
   return RW_OK;
 }
 
-#define RW_TRY(expr)       \
-  do {                     \
-    int rc_ = (expr);      \
-    if (rc_) return rc_;   \
-  } while (0)
-
 static int decoder_forward(rw_decoder *d, size_t n_tok, float *hidden, char *b, const DecScratch &S, hipStream_t s) {
-  const size_t n = d->n, f = d->f;
+  const size_t n = d->n;
   const int *tok = (const int *)(b + S.off_tok);
   float *x = (float *)(b + S.off_x), *cur = (float *)(b + S.off_cur), *q = (float *)(b + S.off_q);
-  float *att = (float *)(b + S.off_a), *prj = (float *)(b + S.off_p), *h = (float *)(b + S.off_h);
+  float *att = (float *)(b + S.off_a), *h = (float *)(b + S.off_h);
   void *act = b + S.off_act, *aws = b + S.off_att;
   const rw_weight *E = d->p.token_embedding;
   const size_t items = n_tok * (size_t)E->nb;
@@ -915,42 +939,38 @@ static int decoder_forward(rw_decoder *d, size_t n_tok, float *hidden, char *b, 
 #undef RW_EMB
   LAUNCH_TRY("k_embed");
   const size_t t_kv = d->n_past + n_tok;
-  bool pending = false;  // prj holds a residual not yet added to x
+  // x is the residual stream: every layernorm is folded into the product
+  // that reads it, and every residual add (src/decoder.rs:168-170, 191-193,
+  // mlp_block) into the epilogue of the product that makes it
   for (int l = 0; l < d->p.n_layer; ++l) {
     const rw_decoder_layer &L = d->layers[l];
     // causal self-attention over the cache and the new rows
-    RW_TRY(launch_layernorm(x, n_tok, n, L.attn_ln_w, L.attn_ln_b, cur, s, pending ? prj : nullptr));
     {
       // q, k and v in one launch; k and v land in the cache rows
       const rw_weight *w3[3] = {L.q, L.k, L.v};
       const float *b3[3] = {L.q_b, nullptr, L.v_b};
       float *o3[3] = {q, d->self_k(l) + d->n_past * n, d->self_v(l) + d->n_past * n};
       if (L.q->dtype == L.k->dtype && L.q->dtype == L.v->dtype) {
-        RW_TRY(run_matmul_set(w3, 3, cur, n_tok, b3, o3, act, s));
+        RW_TRY(run_matmul_set(w3, 3, x, n_tok, b3, o3, act, s, L.attn_ln_w, L.attn_ln_b, 0, cur));
       } else {
+        RW_TRY(launch_layernorm(x, n_tok, n, L.attn_ln_w, L.attn_ln_b, cur, s, nullptr));
         for (int i = 0; i < 3; ++i) RW_TRY(run_matmul(w3[i], cur, n_tok, b3[i], o3[i], act, s));
       }
     }
     RW_TRY(run_attention(q, n, d->self_k(l), n, d->self_v(l), n, n_tok, t_kv, d->p.n_head, 1, att, n, S.self_att,
                          aws, s));
-    RW_TRY(run_matmul(L.out, att, n_tok, L.out_b, prj, act, s));
-    // cross-attention to the window's K/V (the residual add fused into the layernorm)
-    RW_TRY(launch_layernorm(x, n_tok, n, L.cross_ln_w, L.cross_ln_b, cur, s, prj));
-    RW_TRY(run_matmul(L.cq, cur, n_tok, L.cq_b, q, act, s));
+    RW_TRY(run_linear(L.out, att, n_tok, L.out_b, x, act, s, nullptr, nullptr, GEMM_ACC, nullptr));
+    // cross-attention to the window's K/V
+    RW_TRY(run_linear(L.cq, x, n_tok, L.cq_b, q, act, s, L.cross_ln_w, L.cross_ln_b, 0, cur));
     const AttnPlanes cp = d->cross->planes(l);
     RW_TRY(run_attention(q, n, nullptr, n, nullptr, n, n_tok, d->n_audio, d->p.n_head, 0, att, n, S.cross_att, aws,
                          s, &cp));
-    RW_TRY(run_matmul(L.cout, att, n_tok, L.cout_b, prj, act, s));
+    RW_TRY(run_linear(L.cout, att, n_tok, L.cout_b, x, act, s, nullptr, nullptr, GEMM_ACC, nullptr));
     // MLP
-    RW_TRY(launch_layernorm(x, n_tok, n, L.mlp_ln_w, L.mlp_ln_b, cur, s, prj));
-    RW_TRY(run_matmul(L.fc1, cur, n_tok, L.fc1_b, h, act, s));
-    hipLaunchKernelGGL(k_gelu, dim3((unsigned)cdiv(n_tok * f, 256)), dim3(256), 0, s, h, n_tok * f);
-    LAUNCH_TRY("k_gelu");
-    RW_TRY(run_matmul(L.fc2, h, n_tok, L.fc2_b, prj, act, s));
-    // the MLP's residual add goes into the next layer's first layernorm
-    pending = true;
+    RW_TRY(run_linear(L.fc1, x, n_tok, L.fc1_b, h, act, s, L.mlp_ln_w, L.mlp_ln_b, GEMM_GELU, cur));
+    RW_TRY(run_linear(L.fc2, h, n_tok, L.fc2_b, x, act, s, nullptr, nullptr, GEMM_ACC, nullptr));
   }
-  return launch_layernorm(x, n_tok, n, d->p.ln_w, d->p.ln_b, hidden, s, pending ? prj : nullptr);
+  return launch_layernorm(x, n_tok, n, d->p.ln_w, d->p.ln_b, hidden, s, nullptr);
 }
 
 // ------------------------------------------------------ encoder layer
