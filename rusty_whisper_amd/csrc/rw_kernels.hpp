@@ -601,6 +601,7 @@ struct GemvItem {
 // Up to GEMV_SET linears of one dtype that read one activation, launched
 // together without a device table: workgroups [end[t-1], end[t]) run item t.
 constexpr int GEMV_SET = 4;
+constexpr int GEMV_MR_MAX = 8;  // activation rows k_gemv takes
 struct GemvSet {
   GemvItem it[GEMV_SET];
   int end[GEMV_SET];
@@ -637,11 +638,12 @@ __device__ inline void gemv_zero_slots(uint8_t *lds, int nslots, int t) {
 // or copied from an already quantized workspace (I.qa).  (block, row) pairs
 // block-major, 4 passes of 32 per batch so their global loads are in flight
 // together.  Records of the tail blocks past nb are zeroed.
-// With I.lnw the rows are layernormed first (mean mu[i], inv iv[i] of row i,
-// then (x - mu) * iv * w + b, src/tensor.rs:274-287) and the result quantized.
+// With I.lnw the rows are layernormed first (mean ln[i] and inverse deviation
+// ln[GEMV_MR_MAX + i] of row i, in LDS; then (x - mean) * inv * w + b,
+// src/tensor.rs:274-287) and the result quantized.
 template <int DT, int MR>
 __device__ inline void gemv_fill(const GemvItem &I, int nb, int c0, int c1, uint8_t *base, int t,
-                                 const float (&mu)[MR], const float (&iv)[MR]) {
+                                 const float *ln) {
   constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR, SO = ZO + 16, DO = SO + 32, PO = DO + 32;
   constexpr int OFF = DT == 2 ? 8 : DT == 6 ? 16 : 0;
   const int bb0 = c0 * OCT, cnb = min(nb, c1 * OCT) - bb0;
@@ -657,10 +659,7 @@ __device__ inline void gemv_fill(const GemvItem &I, int nb, int c0, int c1, uint
           const int lb = rb / MR, i = rb - lb * MR;
           x[u] = ldg_f4(I.a + ((size_t)i * nb + bb0 + lb) * QK + 4 * lt);
           if (I.lnw) {
-            float m0 = mu[0], v0 = iv[0];
-#pragma unroll
-            for (int k = 1; k < MR; ++k)
-              if (i == k) m0 = mu[k], v0 = iv[k];
+            const float m0 = ln[i], v0 = ln[GEMV_MR_MAX + i];
             const size_t e = (size_t)(bb0 + lb) * QK + 4 * lt;
             const float4 w4 = ldg_f4(I.lnw + e), b4 = ldg_f4(I.lnb + e);
             x[u].x = (x[u].x - m0) * v0 * w4.x + b4.x;
@@ -949,10 +948,9 @@ __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restri
     }
 
   // layernorm statistics of the m activation rows (single / set launches
-  // with I.lnw): every workgroup computes them, in the same tree order
-  float ln_mu[MR], ln_iv[MR];
-#pragma unroll
-  for (int i = 0; i < MR; ++i) ln_mu[i] = 0.0f, ln_iv[i] = 0.0f;
+  // with I.lnw): every workgroup computes them, in the same tree order, and
+  // keeps them in LDS for the fills
+  __shared__ float ln_s[2 * GEMV_MR_MAX];
   if constexpr (!GROUPED) {
     if (I.lnw) {
       const int K = nb * QK;
@@ -978,19 +976,26 @@ __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restri
         acc_s[i] = a;
       }
       row_sums(acc_s);
+      float mean[MR];
 #pragma unroll
       for (int i = 0; i < MR; ++i) {
-        ln_mu[i] = __fdiv_rn(acc_s[i], (float)K);
+        mean[i] = __fdiv_rn(acc_s[i], (float)K);
         float a = 0.0f;
         for (int c = t; c < K; c += 256) {
-          const float d = I.a[(size_t)i * K + c] - ln_mu[i];
+          const float d = I.a[(size_t)i * K + c] - mean[i];
           a += d * d;
         }
         acc_s[i] = a;
       }
       row_sums(acc_s);
+      if (t == 0) {
 #pragma unroll
-      for (int i = 0; i < MR; ++i) ln_iv[i] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(acc_s[i], (float)K) + 1e-5f));
+        for (int i = 0; i < MR; ++i) {
+          ln_s[i] = mean[i];
+          ln_s[GEMV_MR_MAX + i] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(acc_s[i], (float)K) + 1e-5f));
+        }
+      }
+      __syncthreads();
     }
   }
 
@@ -1020,7 +1025,7 @@ __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restri
         for (int z = t; z < (c1 - c0) * OCT * (REC / 16); z += 256)
           reinterpret_cast<uint4 *>(base)[z] = ldg_u4(src + z);
       } else {
-        gemv_fill<DT, MR>(I, nb, c0, c1, base, t, ln_mu, ln_iv);
+        gemv_fill<DT, MR>(I, nb, c0, c1, base, t, ln_s);
       }
     }
     __syncthreads();
