@@ -3,7 +3,7 @@
 The oracle is the CPU restatement of rusty_whisper's quantized matmul
 (src/quant.rs, the f16 codec of src/model.rs and the f32 dot of src/tensor.rs).
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
-this module, and only as the checker or the timed CPU baseline; the product
+this module, and only as the parity reference or the timed CPU baseline; the product
 package (rusty_whisper_amd) never imports it.
 
 See oracle.h for which reference lines each function restates and what pins

@@ -1,7 +1,7 @@
 /*
  * oracle.c -- CPU restatement of rusty_whisper src/quant.rs (and the f16
  * codec of src/model.rs, the f32 dot of src/tensor.rs) for the quantized
- * linear-layer matmul.  TEST INFRASTRUCTURE ONLY: the checker used by tests/,
+ * linear-layer matmul.  TEST INFRASTRUCTURE ONLY: the reference values for tests/,
  * __graft_entry__.smoke() and bench.py's cpu_baseline leg.  The product
  * (rusty_whisper_amd/, include/) never links or calls it.
  *

@@ -1,7 +1,7 @@
 /*
  * oracle.h -- CPU restatement of rusty_whisper's quantized linear-layer
  * matmul (src/quant.rs), used ONLY as test infrastructure: the parity
- * checker for tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * reference for tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
  * leg.  Nothing in the product (rusty_whisper_amd/, include/) links or calls
  * this code.
  *

@@ -77,7 +77,7 @@ def edge_activation_rows(k: int) -> np.ndarray:
 
 
 def rel_row_l2(got: np.ndarray, ref: np.ndarray) -> float:
-    """max_ij |got-ref| / ||ref_i||_2 -- the north-star output tolerance."""
+    """max_ij |got-ref| / ||ref_i||_2 -- the output tolerance of the products (1e-3)."""
     ref64 = ref.astype(np.float64)
     norms = np.linalg.norm(ref64, axis=1, keepdims=True)
     norms = np.where(norms > 0, norms, 1.0)

@@ -31,7 +31,7 @@ from _data import DTYPES, NAMES, activations, check_combine, edge_activation_row
 
 pytestmark = pytest.mark.gpu
 
-NORTH_STAR_TOL = 1e-3
+ROW_L2_TOL = 1e-3
 
 
 @pytest.fixture(scope="module")
@@ -83,7 +83,7 @@ def test_prequant_matches_fused_bitwise(torch, dtype, m):
     w.matmul_prequant_dev(ws, m, out)
     torch.cuda.synchronize()
     assert np.array_equal(_bits(out.cpu().numpy()), _bits(fused))
-    assert rel_row_l2(fused, O.matmul_emul(a, dtype, raw, n)) <= NORTH_STAR_TOL
+    assert rel_row_l2(fused, O.matmul_emul(a, dtype, raw, n)) <= ROW_L2_TOL
 
 
 # (dtype, m, n, k, bias): every k split (k = 384 -> 2, 768 / 1280 -> 1,
@@ -133,7 +133,7 @@ def test_grouped_matches_single(torch):
         got = out.cpu().numpy()
         assert rel_row_l2(got, _single(torch, w, a, b)) <= 1e-6, (w.dtype, m, w.n, w.k)
         ref = O.matmul_emul(a, w.dtype, raw, w.n, bias=b)
-        assert rel_row_l2(got, ref) <= NORTH_STAR_TOL, (w.dtype, m, w.n, w.k)
+        assert rel_row_l2(got, ref) <= ROW_L2_TOL, (w.dtype, m, w.n, w.k)
 
 
 def test_prepared_group_matches_grouped_bitwise(torch):
@@ -181,7 +181,7 @@ def test_gemv_chunked_k_rows_independent_of_m(torch, dtype):
     got8 = _single(torch, w, a)
     got1 = _single(torch, w, a[:1])
     assert np.array_equal(_bits(got8[:1]), _bits(got1))
-    assert rel_row_l2(got8, O.matmul_emul(a, dtype, raw, n)) <= NORTH_STAR_TOL
+    assert rel_row_l2(got8, O.matmul_emul(a, dtype, raw, n)) <= ROW_L2_TOL
 
 
 def test_grouped_rejects_bad_items(torch):
@@ -336,7 +336,7 @@ def test_prequant_multi(torch, dtype, m, ns, k, hasb):
     got = run(m)
     for w, raw, b, y in zip(ws_, raws, biases, got):
         ref = O.matmul_emul(a, dtype, raw, w.n, bias=b)
-        assert rel_row_l2(y, ref) <= NORTH_STAR_TOL
+        assert rel_row_l2(y, ref) <= ROW_L2_TOL
         check_combine(y, a, dtype, raw, w.n, b)
         if m <= A.GEMV_MAX_M:  # decode shape: bitwise the single-weight call
             single = torch.empty(m, w.n, device="cuda:0")

@@ -16,7 +16,7 @@ import _modelfile as MF
 
 pytestmark = pytest.mark.gpu
 
-NORTH_STAR_TOL = 1e-3
+ROW_L2_TOL = 1e-3
 HP = [51865, 1500, 384, 6, 4, 448, 384, 6, 4, 80, 1]
 
 
@@ -61,6 +61,6 @@ def test_loaded_weights_match_direct_upload(tmp_path, container):
             y = w.matmul(a)
             assert np.array_equal(y.view(np.uint32), direct.matmul(a).view(np.uint32)), (NAMES[dt], mrows)
             ref = O.matmul_emul(a, dt, raw, n, tier=O.TIER_VNNI)
-            assert rel_row_l2(y, ref) <= NORTH_STAR_TOL, (NAMES[dt], mrows)
+            assert rel_row_l2(y, ref) <= ROW_L2_TOL, (NAMES[dt], mrows)
         direct.free()
     m.free()

@@ -21,7 +21,7 @@ from _data import DTYPES, NAMES, activations, check_combine, edge_activation_row
 
 pytestmark = pytest.mark.gpu
 
-NORTH_STAR_TOL = 1e-3
+ROW_L2_TOL = 1e-3
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -141,12 +141,12 @@ def test_matmul_parity(dtype, m, k, n):
     w = A.DeviceWeight(dtype, n, k, raw)
     got = w.matmul(a)
     ref = O.matmul_emul(a, dtype, raw, n, tier=O.TIER_VNNI)
-    assert rel_row_l2(got, ref) <= NORTH_STAR_TOL
+    assert rel_row_l2(got, ref) <= ROW_L2_TOL
     check_combine(got, a, dtype, raw, n)
     got_b = w.matmul(a, bias)
     assert np.array_equal(got_b.view(np.uint32), (got + bias[None, :]).view(np.uint32))
     ref_b = O.matmul_emul(a, dtype, raw, n, bias=bias, tier=O.TIER_AVX2)
-    assert rel_row_l2(got_b, ref_b) <= NORTH_STAR_TOL
+    assert rel_row_l2(got_b, ref_b) <= ROW_L2_TOL
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: NAMES[d])
@@ -162,7 +162,7 @@ def test_rows_independent_of_m(dtype):
     for m in range(1, 8):  # GEMV family: bitwise
         assert np.array_equal(w.matmul(a[:m]).view(np.uint32), small[:m].view(np.uint32))
     # across the two families: exact block sums vs f16 operands
-    assert rel_row_l2(small, big[:8]) <= NORTH_STAR_TOL
+    assert rel_row_l2(small, big[:8]) <= ROW_L2_TOL
 
 
 def test_m_zero_is_a_noop():
@@ -179,7 +179,7 @@ def test_scale_spread_and_outliers(dtype):
     a = activations(m, k, seed=22, outliers=0.01)
     got = A.DeviceWeight(dtype, n, k, raw).matmul(a)
     ref = O.matmul_emul(a, dtype, raw, n)
-    assert rel_row_l2(got, ref) <= NORTH_STAR_TOL
+    assert rel_row_l2(got, ref) <= ROW_L2_TOL
     check_combine(got, a, dtype, raw, n)
 
 
@@ -208,7 +208,7 @@ def test_matmul_t_q_real_encoder_shape_q5_1():
     got = A.DeviceWeight(7, n, k, raw).matmul(a)
     _dense_check(got, a, raw, 7, n, k)
     ref = O.matmul_emul(a, 7, raw, n)
-    assert rel_row_l2(got, ref) <= NORTH_STAR_TOL
+    assert rel_row_l2(got, ref) <= ROW_L2_TOL
 
 
 @pytest.mark.parametrize("dtype,sa,sb", [(8, 17, 19), (7, 23, 29)], ids=["Q8_0", "Q5_1"])
@@ -291,7 +291,7 @@ def test_gemm_k_splits(dtype, m, k, n):
     w = A.DeviceWeight(dtype, n, k, raw)
     got = w.matmul(a, bias)
     ref = O.matmul_emul(a, dtype, raw, n, bias=bias)
-    assert rel_row_l2(got, ref) <= NORTH_STAR_TOL
+    assert rel_row_l2(got, ref) <= ROW_L2_TOL
     check_combine(got, a, dtype, raw, n, bias)
     # a row's result does not depend on m
     assert np.array_equal(w.matmul(a[:9], bias).view(np.uint32), got[:9].view(np.uint32))

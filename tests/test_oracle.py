@@ -132,7 +132,7 @@ def test_unpack_rejects_unknown_dtype():
 
 
 def _numpy_unpack(dtype, raw, nblk):
-    """Independent restatement of the ggml byte maps."""
+    """Independent restatement of the ggml byte maps (ggml-format block layouts)."""
     bb = O.BLOCK_BYTES[dtype]
     b = raw.reshape(nblk, bb)
     d = b[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(nblk)
