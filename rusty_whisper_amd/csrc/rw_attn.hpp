@@ -190,8 +190,14 @@ __device__ inline void att_load_v(const AttnPlanes &P, int head, int blk, int h,
 // workgroup z of gridDim.z takes the z-th run of the kv blocks and writes
 // its unnormalized O (2^12-scaled), running maximum and sum to part;
 // k_attn_combine merges the runs.
+//
+// With qf != NULL the queries come as f32 rows (qf, ldq) and are scaled and
+// split here, exactly as k_attn_split would store them (P.qh, P.ql unused):
+// the decoder's cross-attention, whose K and v^T planes are kept, then needs
+// no split launch.
 __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, int causal,
-                                              float *__restrict__ out, int ld_out, float *__restrict__ part) {
+                                              float *__restrict__ out, int ld_out, float *__restrict__ part,
+                                              const float *__restrict__ qf, int ldq) {
   constexpr float LOG2E = 1.4426950408889634f;
   constexpr float NEG_INF = -__builtin_huge_valf();
   __shared__ __align__(16) float xo[ATT_QB * (ATT_DH + 4)];  // partial O^T exchange, then the output tile
@@ -224,8 +230,28 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
     const size_t qrow = ((size_t)head * P.tq_pad + q0 + qt * 32 + n) * ATT_DH + 8 * h;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      qh[qt][s] = att_ld(P.qh + qrow + 16 * s);
-      ql[qt][s] = att_ld(P.ql + qrow + 16 * s);
+      if (qf) {
+        const int row = q0 + qt * 32 + n;
+        float v[8];
+        if (row < t_q) {
+          const float4 *src = reinterpret_cast<const float4 *>(qf + (size_t)row * ldq + head * ATT_DH + 8 * h + 16 * s);
+          const float4 a = src[0], b = src[1];
+          v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          uint16_t hb, lb;
+          att_split(v[e] * 0.125f, hb, lb);
+          qh[qt][s][e] = __builtin_bit_cast(_Float16, hb);
+          ql[qt][s][e] = __builtin_bit_cast(_Float16, lb);
+        }
+      } else {
+        qh[qt][s] = att_ld(P.qh + qrow + 16 * s);
+        ql[qt][s] = att_ld(P.ql + qrow + 16 * s);
+      }
     }
   }
   att_v16f o[ATT_QT][2];  // O^T

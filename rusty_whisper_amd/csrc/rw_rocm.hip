@@ -804,20 +804,22 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
     return RW_OK;
   }
   // kv_split: K and v^T already split (the decoder's cross-attention); only q
-  // is split here
+  // needs splitting, which k_attn does as it loads it
   AttnPlanes P{qh, ql, kh, kl, vh, vl, L.tq_pad, L.tkv_pad};
   if (kv_split) {
     P.kh = kv_split->kh, P.kl = kv_split->kl, P.vh = kv_split->vh, P.vl = kv_split->vl;
     P.tkv_pad = kv_split->tkv_pad;
   }
-  const size_t nq = (size_t)n_head * L.tq_pad * 8, nk = kv_split ? 0 : (size_t)n_head * L.tkv_pad * 8;
-  const int wq = (int)cdiv(nq, 256), wk = (int)cdiv(nk, 256), wv = wk;  // v^T: as many items as k
-  hipLaunchKernelGGL(k_attn_split, dim3((unsigned)(wq + wk + wv)), dim3(256), 0, s, q, (int)ldq, (int)t_q, k,
-                     (int)ldk, v, (int)ldv, (int)t_kv, P, n_head, wq, wk);
-  LAUNCH_TRY("k_attn_split");
+  if (!kv_split) {
+    const size_t nq = (size_t)n_head * L.tq_pad * 8, nk = (size_t)n_head * L.tkv_pad * 8;
+    const int wq = (int)cdiv(nq, 256), wk = (int)cdiv(nk, 256), wv = wk;  // v^T: as many items as k
+    hipLaunchKernelGGL(k_attn_split, dim3((unsigned)(wq + wk + wv)), dim3(256), 0, s, q, (int)ldq, (int)t_q, k,
+                       (int)ldk, v, (int)ldv, (int)t_kv, P, n_head, wq, wk);
+    LAUNCH_TRY("k_attn_split");
+  }
   float *part = L.nsplit > 1 ? (float *)(b + L.off_part) : nullptr;
   hipLaunchKernelGGL(k_attn, dim3((unsigned)(L.tq_pad / ATT_QB), (unsigned)n_head, (unsigned)L.nsplit), dim3(128), 0, s,
-                     P, (int)t_q, (int)t_kv, causal ? 1 : 0, out, (int)ldo, part);
+                     P, (int)t_q, (int)t_kv, causal ? 1 : 0, out, (int)ldo, part, kv_split ? q : nullptr, (int)ldq);
   LAUNCH_TRY("k_attn");
   if (part) {
     const size_t nz = t_q * (size_t)n_head * ATT_DH;
