@@ -40,6 +40,7 @@ constexpr int ATT_DH = 64;   // head size (every whisper model)
 constexpr int ATT_KVB = 32;  // kv rows per block
 constexpr int ATT_QT = 2;    // 32-query tiles per workgroup
 constexpr int ATT_QB = 32 * ATT_QT;
+constexpr int ATT_MAX_SPLIT = 16;  // kv runs of one (query block, head) at most
 
 // kv index (within a 16-block) stored at position p of the v^T plane: the
 // middle quads swap (an involution)
@@ -406,16 +407,30 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
   const int d = (int)(idx % ATT_DH);
   const int head = (int)((idx / ATT_DH) % n_head), q = (int)(idx / ((size_t)ATT_DH * n_head));
   const float *pml = part + (size_t)nsplit * n_head * tq_pad * ATT_DH;
+  // every run's maximum, sum and output value requested at once (one memory
+  // round trip), then folded in run order
+  float mz[ATT_MAX_SPLIT], lz[ATT_MAX_SPLIT], oz[ATT_MAX_SPLIT];
+#pragma unroll
+  for (int z = 0; z < ATT_MAX_SPLIT; ++z) {
+    mz[z] = NEG_INF, lz[z] = 0.0f, oz[z] = 0.0f;
+    if (z < nsplit) {
+      const size_t pr = ((size_t)z * n_head + head) * tq_pad + q;
+      mz[z] = pml[2 * pr];
+      lz[z] = pml[2 * pr + 1];
+      oz[z] = part[pr * ATT_DH + d];
+    }
+  }
   float mx = NEG_INF;
-  for (int z = 0; z < nsplit; ++z) mx = fmaxf(mx, pml[2 * (((size_t)z * n_head + head) * tq_pad + q)]);
+#pragma unroll
+  for (int z = 0; z < ATT_MAX_SPLIT; ++z) mx = fmaxf(mx, mz[z]);
   const float mu = mx == NEG_INF ? 0.0f : mx;
   float num = 0.0f, den = 0.0f;
-  for (int z = 0; z < nsplit; ++z) {
-    const size_t pr = ((size_t)z * n_head + head) * tq_pad + q;
-    const float w = __builtin_amdgcn_exp2f((pml[2 * pr] - mu) * LOG2E);
-    if (w > 0.0f) {  // a run that saw no key holds no output
-      num += part[pr * ATT_DH + d] * w;
-      den += pml[2 * pr + 1] * w;
+#pragma unroll
+  for (int z = 0; z < ATT_MAX_SPLIT; ++z) {
+    const float w = __builtin_amdgcn_exp2f((mz[z] - mu) * LOG2E);
+    if (z < nsplit && w > 0.0f) {  // a run that saw no key holds no output
+      num += oz[z] * w;
+      den += lz[z] * w;
     }
   }
   out[(size_t)q * ld_out + head * ATT_DH + d] = num / (den * ATT_PS);

@@ -947,6 +947,17 @@ __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restri
       accm[j][v] = 0.0f;
     }
 
+  const int span = (w.noct + KS - 1) >> lks;  // the longest part
+  const int ch = min(span, max(1, cap_oct >> lks));
+  // the first octet's weights are requested before the records and the
+  // layernorm statistics (so the memory latencies overlap) where its
+  // registers fit beside the fill's: grouped launches copy records and
+  // always can; fills can for Q4_0, and for Q4_1 and Q5_0 at one row (the
+  // other forms would spill)
+  constexpr bool EARLY = GROUPED || DT == 2 || (MR == 1 && (DT == 3 || DT == 6));
+  GemvOct<DT> cur;
+  if (EARLY && o0 < min(o1, o0 + ch)) gemv_load_oct<DT>(w, gw, o0, rq, rd, rm, rh, vq, vs, vh, cur);
+
   // layernorm statistics of the m activation rows (single / set launches
   // with I.lnw): every workgroup computes them, in the same tree order, and
   // keeps them in LDS for the fills
@@ -1007,18 +1018,10 @@ __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restri
   // chunks: step cc covers octets [s_p + cc, s_p + cc + ch) of every part
   // p (s_p its first octet), in LDS slots [p*ch, (p+1)*ch), so that every
   // part advances through every chunk
-  const int span = (w.noct + KS - 1) >> lks;  // the longest part
-  // the first octet's weights are requested before the records (so the two
-  // memory latencies overlap) where its registers fit beside the fill's:
-  // grouped launches copy records and always can; fills can for Q4_0, and
-  // for Q4_1 and Q5_0 at one row (the other forms would spill)
-  constexpr bool EARLY = GROUPED || DT == 2 || (MR == 1 && (DT == 3 || DT == 6));
-  const int ch = min(span, max(1, cap_oct >> lks));
   for (int cc = 0; cc < span; cc += ch) {
     // this part's octets in the chunk
     const int p0 = o0 + cc, p1 = min(o1, p0 + ch);
-    GemvOct<DT> cur;
-    if (EARLY && p0 < p1) gemv_load_oct<DT>(w, gw, p0, rq, rd, rm, rh, vq, vs, vh, cur);
+    if (EARLY && cc && p0 < p1) gemv_load_oct<DT>(w, gw, p0, rq, rd, rm, rh, vq, vs, vh, cur);
     if (cc) __syncthreads();  // every wavefront is done with the previous chunk
     for (int pp = 0; pp < KS; ++pp) {
       const int c0 = ((w.noct * pp) >> lks) + cc, c1 = min((w.noct * (pp + 1)) >> lks, c0 + ch);

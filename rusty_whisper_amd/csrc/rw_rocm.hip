@@ -762,7 +762,7 @@ static AttnLayout attn_layout(size_t t_q, size_t t_kv, size_t n_state) {
   const size_t groups = (size_t)(L.tq_pad / ATT_QB) * L.n_head, nblk = cdiv(t_kv, ATT_KVB);
   L.nsplit = 1;
   if (groups < 256 && nblk >= 8)
-    L.nsplit = (int)std::min<size_t>(16, std::min(nblk / 4, cdiv(512, groups)));
+    L.nsplit = (int)std::min<size_t>(ATT_MAX_SPLIT, std::min(nblk / 4, cdiv(512, groups)));
   L.off_part = align_up(L.off_vl + kb, 256);
   const size_t part = L.nsplit > 1 ? (size_t)L.nsplit * L.n_head * L.tq_pad * (ATT_DH + 2) * 4 : 0;
   L.bytes = align_up(L.off_part + part, 256);
