@@ -979,24 +979,32 @@ __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restri
         for (int i = 0; i < MR; ++i) v[i] = (sred[i] + sred[MR + i]) + (sred[2 * MR + i] + sred[3 * MR + i]);
         __syncthreads();
       };
+      // a thread's values of a row, c = t, t + 256, ..., summed in that
+      // order; loaded 8 at a time so that their latencies overlap
+      auto thread_sum = [&](const float *row, float mu, bool sq) __attribute__((always_inline)) {
+        float a = 0.0f;
+        for (int c0 = t; c0 < K; c0 += 8 * 256) {
+          float v[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) v[u] = c0 + 256 * u < K ? row[c0 + 256 * u] : 0.0f;
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            if (c0 + 256 * u < K) {
+              const float d = v[u] - mu;
+              a += sq ? d * d : v[u];
+            }
+        }
+        return a;
+      };
       float acc_s[MR];
 #pragma unroll
-      for (int i = 0; i < MR; ++i) {
-        float a = 0.0f;
-        for (int c = t; c < K; c += 256) a += I.a[(size_t)i * K + c];
-        acc_s[i] = a;
-      }
+      for (int i = 0; i < MR; ++i) acc_s[i] = thread_sum(I.a + (size_t)i * K, 0.0f, false);
       row_sums(acc_s);
       float mean[MR];
 #pragma unroll
       for (int i = 0; i < MR; ++i) {
         mean[i] = __fdiv_rn(acc_s[i], (float)K);
-        float a = 0.0f;
-        for (int c = t; c < K; c += 256) {
-          const float d = I.a[(size_t)i * K + c] - mean[i];
-          a += d * d;
-        }
-        acc_s[i] = a;
+        acc_s[i] = thread_sum(I.a + (size_t)i * K, mean[i], true);
       }
       row_sums(acc_s);
       if (t == 0) {
