@@ -805,13 +805,15 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
   }
   // kv_split: K and v^T already split (the decoder's cross-attention); only q
   // needs splitting, which k_attn does as it loads it
-  AttnPlanes P{qh, ql, kh, kl, vh, vl, L.tq_pad, L.tkv_pad};
+  // planes padded to this call's t_kv (the layout may be sized for a longer
+  // one, e.g. a decoder's n_ctx)
+  AttnPlanes P{qh, ql, kh, kl, vh, vl, L.tq_pad, (int)std::min<size_t>(align_up(t_kv, ATT_KVB), L.tkv_pad)};
   if (kv_split) {
     P.kh = kv_split->kh, P.kl = kv_split->kl, P.vh = kv_split->vh, P.vl = kv_split->vl;
     P.tkv_pad = kv_split->tkv_pad;
   }
   if (!kv_split) {
-    const size_t nq = (size_t)n_head * L.tq_pad * 8, nk = (size_t)n_head * L.tkv_pad * 8;
+    const size_t nq = (size_t)n_head * L.tq_pad * 8, nk = (size_t)n_head * P.tkv_pad * 8;
     const int wq = (int)cdiv(nq, 256), wk = (int)cdiv(nk, 256), wv = wk;  // v^T: as many items as k
     hipLaunchKernelGGL(k_attn_split, dim3((unsigned)(wq + wk + wv)), dim3(256), 0, s, q, (int)ldq, (int)t_q, k,
                        (int)ldk, v, (int)ldv, (int)t_kv, P, n_head, wq, wk);
