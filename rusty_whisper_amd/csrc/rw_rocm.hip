@@ -745,6 +745,13 @@ struct AttnLayout {
   size_t off_qh, off_ql, off_kh, off_kl, off_vh, off_vl, off_part, bytes;
 };
 
+// few (query block, head) workgroups -- a decoding step: split the kv
+// blocks over up to ATT_MAX_SPLIT workgroups each, merged by k_attn_combine
+static int attn_nsplit(size_t groups, size_t nblk) {
+  if (groups < 256 && nblk >= 8) return (int)std::min<size_t>(ATT_MAX_SPLIT, std::min(nblk / 4, cdiv(512, groups)));
+  return 1;
+}
+
 static AttnLayout attn_layout(size_t t_q, size_t t_kv, size_t n_state) {
   AttnLayout L{};
   L.n_head = (int)(n_state / ATT_DH);
@@ -757,12 +764,7 @@ static AttnLayout attn_layout(size_t t_q, size_t t_kv, size_t n_state) {
   L.off_kl = align_up(L.off_kh + kb, 256);
   L.off_vh = align_up(L.off_kl + kb, 256);
   L.off_vl = align_up(L.off_vh + kb, 256);
-  // few (query block, head) workgroups -- a decoding step: split the kv
-  // blocks over up to 16 workgroups each, merged by k_attn_combine
-  const size_t groups = (size_t)(L.tq_pad / ATT_QB) * L.n_head, nblk = cdiv(t_kv, ATT_KVB);
-  L.nsplit = 1;
-  if (groups < 256 && nblk >= 8)
-    L.nsplit = (int)std::min<size_t>(ATT_MAX_SPLIT, std::min(nblk / 4, cdiv(512, groups)));
+  L.nsplit = attn_nsplit((size_t)(L.tq_pad / ATT_QB) * L.n_head, cdiv(t_kv, ATT_KVB));
   L.off_part = align_up(L.off_vl + kb, 256);
   const size_t part = L.nsplit > 1 ? (size_t)L.nsplit * L.n_head * L.tq_pad * (ATT_DH + 2) * 4 : 0;
   L.bytes = align_up(L.off_part + part, 256);
@@ -819,13 +821,16 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
                        (int)ldk, v, (int)ldv, (int)t_kv, P, n_head, wq, wk);
     LAUNCH_TRY("k_attn_split");
   }
-  float *part = L.nsplit > 1 ? (float *)(b + L.off_part) : nullptr;
-  hipLaunchKernelGGL(k_attn, dim3((unsigned)(L.tq_pad / ATT_QB), (unsigned)n_head, (unsigned)L.nsplit), dim3(128), 0, s,
+  // this call's split (the layout's is for its longest kv; the rule grows
+  // with the kv length, so this one fits the layout's part buffer)
+  const int nsplit = std::min(L.nsplit, attn_nsplit((size_t)(L.tq_pad / ATT_QB) * n_head, cdiv(t_kv, ATT_KVB)));
+  float *part = nsplit > 1 ? (float *)(b + L.off_part) : nullptr;
+  hipLaunchKernelGGL(k_attn, dim3((unsigned)(L.tq_pad / ATT_QB), (unsigned)n_head, (unsigned)nsplit), dim3(128), 0, s,
                      P, (int)t_q, (int)t_kv, causal ? 1 : 0, out, (int)ldo, part, kv_split ? q : nullptr, (int)ldq);
   LAUNCH_TRY("k_attn");
   if (part) {
     const size_t nz = t_q * (size_t)n_head * ATT_DH;
-    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)cdiv(nz, 256)), dim3(256), 0, s, part, L.nsplit, n_head,
+    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)cdiv(nz, 256)), dim3(256), 0, s, part, nsplit, n_head,
                        L.tq_pad, (int)t_q, out, (int)ldo);
     LAUNCH_TRY("k_attn_combine");
   }
