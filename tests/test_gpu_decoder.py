@@ -92,3 +92,23 @@ def test_fork_and_reset(torch):
         step(torch, d, list(range(14)), n)
     with pytest.raises(A.RwError, match="out of range"):
         step(torch, d, [300], n)
+
+
+def test_decoder_long_cache(torch):
+    """A 300-token prompt and steps past it: causal self-attention over the
+    prompt and over a 301-303 row cache both split their kv blocks over two
+    workgroups (some prompt query blocks' runs see no key) and merge them."""
+    n, heads, n_audio = 128, 2, 120
+    p = decoder_params(n=n, f=4 * n, n_layer=1, n_vocab=300, n_ctx=448, dtype=6, seed=7)
+    enc = np.random.default_rng(3).standard_normal((n_audio, n)).astype(np.float32)
+    prompt = [int(t) for t in np.random.default_rng(5).integers(0, 300, 300)]
+    print("decoder long cache: prompt 300, n_ctx 448", flush=True)
+    d = device_decoder(torch, p, heads, n_audio)
+    d.set_audio(torch.from_numpy(enc).to("cuda:0"))
+    o = OD(p, heads, enc)
+    errs = [rel(step(torch, d, prompt, n), o.forward_hidden(prompt))]
+    for t in (17, 250, 4):
+        errs.append(rel(step(torch, d, [t], n), o.forward_hidden([t])))
+    print("  errors", ["%.2g" % e for e in errs], flush=True)
+    assert d.n_past == 303
+    assert max(errs) <= TOL, errs
