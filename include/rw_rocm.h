@@ -16,10 +16,12 @@
  * with S = sum(q_a*q_b) the per-block integer sum.  Decode-shape products
  * (m <= 8) form S exactly and combine in f32 as the reference does.
  * Encoder-shape products (m > 8) multiply the same values as f16 operands
- * d_a*q_a and d_b*q_b + m_b (one rounding each) with exact products and f32
- * accumulation on the matrix cores: within 2^-10 * sum|a||w| plus f32
- * accumulation error of the exact result, far inside the 1e-3 (row-L2)
- * agreement with the reference CPU path.
+ * d_a*q_a and d_b*q_b + m_b (one rounding each; each activation row and each
+ * weight row scaled by its own power of two first, so no operand overflows
+ * or loses precision to f16 subnormals whatever the block scales are) with
+ * exact products and f32 accumulation on the matrix cores: within
+ * 2^-10 * sum|a||w| plus f32 accumulation error of the exact result, far
+ * inside the 1e-3 (row-L2) agreement with the reference CPU path.
  *
  * Conventions (the crate's existing C ABI, src/wasm.rs:25-110, returns an
  * i32 status and keeps error text separately):
@@ -32,7 +34,12 @@
  * threads on shared rw_weight handles (the reference shares &Model across
  * transcription threads, src/transcribe.rs:1525-1552).  Host-pointer entries
  * are synchronous.  Device-pointer entries are asynchronous on the stream
- * passed in.
+ * passed in; called without a workspace they use one buffer of the
+ * library's per (device, stream), which a call holds until its launches are
+ * queued, so concurrent calls on one stream queue one after the other and
+ * never share it.  Calls that pass one caller workspace race on it unless
+ * the caller orders them.  An rw_decoder is one decoding state: its calls
+ * must not overlap.
  */
 #ifndef RW_ROCM_H
 #define RW_ROCM_H
@@ -157,9 +164,14 @@ typedef struct rw_linear {
 /* Run `count` independent linears, each with m <= 8 (the decode-GEMV
  * regime), in two launches per distinct (dtype, m): every linear's
  * activation is quantized once, then all products run; entries with m == 0
- * are skipped.  Device pointers, asynchronous on `stream`.  Each result is
- * bitwise identical to the same linear run alone through
- * rw_rocm_matmul_t_q_dev.  The launch tables go to `workspace` (>=
+ * are skipped.  Device pointers, asynchronous on `stream`.  Each result
+ * has the same exact per-block integer sums and the same per-block combine
+ * as the same linear run alone through rw_rocm_matmul_t_q_dev, and agrees
+ * with it within a few f32 roundings: a single linear's launch splits a
+ * row's blocks over more wavefronts (it is short of workgroups at decode
+ * sizes), so the parts' f32 sums are added in another order.  Results of one
+ * call do not depend on the other items of the call.  The launch tables go
+ * to `workspace` (>=
  * rw_rocm_grouped_workspace_size bytes; NULL = a buffer of the library's own
  * for this stream) through pinned host memory on `stream`, and the quantized
  * activations are kept there; calls that overlap on one workspace race.

@@ -414,6 +414,12 @@ class Decoder:
         check(lib().rw_rocm_decoder_create(C.byref(prm), n_audio_ctx, C.byref(h)))
         self.handle = h.value
 
+    @property
+    def token_embedding(self) -> DeviceWeight:
+        """The tied embedding, whose product with the hidden rows is the
+        logits (src/decoder.rs:315-321)."""
+        return self._keep[1]
+
     def set_audio(self, enc_out, stream: int | None = None) -> None:
         check(lib().rw_rocm_decoder_set_audio_dev(self.handle, _ptr(enc_out), stream))
 

@@ -194,11 +194,94 @@ __device__ inline void read_block(const uint8_t *p, uint16_t &d, uint16_t &m, ui
   for (int i = 0; i < nq; ++i) q[i] = p[qo + i];
 }
 
-// one thread per (row, block) of the padded matrix
+// element e of a block read by read_block as the centered int8 of
+// unpack_block (src/quant.rs:98-131)
+template <int DT>
+__device__ inline int raw_q(const uint8_t *q, uint32_t qh, int e) {
+  if (DT == 8) return (int)(int8_t)q[e];
+  int v = e < 16 ? (q[e] & 15) : (q[e - 16] >> 4);
+  if (has_high(DT)) v |= (int)((qh >> e) & 1u) << 4;
+  if (DT == 2) v -= 8;
+  if (DT == 6) v -= 16;
+  return v;
+}
+
+__device__ inline float finite_max(float b, float v) {
+  const float a = fabsf(v);
+  return a <= 3.4028235e38f ? fmaxf(b, a) : b;  // inf and NaN do not count
+}
+
+// The GEMM's offset and power-of-two scale of each weight row (GemmPlanes::
+// cm, cs): one wavefront per row of the padded matrix, lanes striding over
+// the blocks.  cm = the mean of the row's finite values d*q + m (f32, summed
+// per lane, then in a butterfly over the lanes); the row's largest finite
+// |d*q + m - cm|, |d| or |m - cm| is in [2^(E-1), 2^E), and cs = 2^(E-15)
+// moves it to [2^14, 2^15).  Finite f16 scales bound E to [-23, 25], so cs is
+// a normal f32.  Zero rows (and padding rows) keep cs = 1, cm = 0.
+template <int DT>
+__global__ __launch_bounds__(256) void k_row_scale(const uint8_t *__restrict__ raw, int n, int nb, int rows,
+                                                   float *__restrict__ cs, float *__restrict__ cm) {
+  constexpr int BB = DT == 2 ? 18 : DT == 3 ? 20 : DT == 6 ? 22 : DT == 7 ? 24 : 34;
+  const int lane = threadIdx.x & 63;
+  const int j = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (j >= rows) return;  // whole wavefronts
+  auto fold = [&](float v) __attribute__((always_inline)) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
+    return v;
+  };
+  float sum = 0.0f, cnt = 0.0f;
+  if (j < n) {
+    for (int bl = lane; bl < nb; bl += 64) {
+      uint16_t d, m;
+      uint32_t h;
+      uint8_t q[32];
+      read_block<DT>(raw + ((size_t)j * nb + bl) * BB, d, m, h, q);
+      const float df = h2f_exact(d), mf = has_min(DT) ? h2f_exact(m) : 0.0f;
+      for (int e = 0; e < QK; ++e) {
+        const float v = __fadd_rn(__fmul_rn(df, (float)raw_q<DT>(q, h, e)), mf);
+        if (fabsf(v) <= 3.4028235e38f) {
+          sum += v;
+          cnt += 1.0f;
+        }
+      }
+    }
+  }
+  sum = fold(sum);
+  cnt = fold(cnt);
+  const float c = cnt > 0.0f ? sum / cnt : 0.0f;
+  float mx = 0.0f;
+  if (j < n) {
+    for (int bl = lane; bl < nb; bl += 64) {
+      uint16_t d, m;
+      uint32_t h;
+      uint8_t q[32];
+      read_block<DT>(raw + ((size_t)j * nb + bl) * BB, d, m, h, q);
+      const float df = h2f_exact(d), mf = (has_min(DT) ? h2f_exact(m) : 0.0f) - c;
+      mx = finite_max(finite_max(mx, df), mf);
+      for (int e = 0; e < QK; ++e) mx = finite_max(mx, __fadd_rn(__fmul_rn(df, (float)raw_q<DT>(q, h, e)), mf));
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if (lane == 0) {
+    float sc = 1.0f;
+    if (mx > 0.0f) {
+      int e;
+      frexpf(mx, &e);
+      sc = ldexpf(1.0f, e - 15);
+    }
+    stg_f(cs + j, sc);
+    stg_f(cm + j, c);
+  }
+}
+
+// one thread per (row, block) of the padded matrix; cs and cm from k_row_scale
 template <int DT>
 __global__ __launch_bounds__(256) void k_repack(const uint8_t *__restrict__ raw, int n, int nb, uint8_t *qs,
                                                 uint32_t *qh, uint16_t *dd, uint16_t *mm, uint32_t *dm,
-                                                uint8_t *q8, int nb_pad, int noct, int ngroups) {
+                                                uint8_t *q8, int nb_pad, int noct, int ngroups,
+                                                const float *__restrict__ cs, const float *__restrict__ cm) {
   constexpr int BB = DT == 2 ? 18 : DT == 3 ? 20 : DT == 6 ? 22 : DT == 7 ? 24 : 34;
   constexpr int QSB = DT == 8 ? 32 : 16;
   size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -232,7 +315,13 @@ __global__ __launch_bounds__(256) void k_repack(const uint8_t *__restrict__ raw,
   size_t si = sc_index(w, g, bl, r);
   dd[si] = d;
   if (has_min(DT)) mm[si] = m;
-  dm[slot] = (uint32_t)d | ((uint32_t)m << 16);
+  // the GEMM's scalars: d and m - cm divided by the row's power of two (one
+  // rounding each; inf and NaN stay non-finite).  Blocks past nb are zeros.
+  const float inv = __fdiv_rn(1.0f, cs[j]);
+  const float mc = bl < nb ? __fsub_rn(has_min(DT) ? h2f_exact(m) : 0.0f, cm[j]) : 0.0f;
+  const uint32_t ds = __half_as_ushort(__float2half_rn(__fmul_rn(h2f_exact(d), inv)));
+  const uint32_t ms = __half_as_ushort(__float2half_rn(__fmul_rn(mc, inv)));
+  dm[slot] = ds | (ms << 16);
   if (has_high(DT)) {
     uint32_t x = 0;
     for (int e = 0; e < 32; ++e) x |= ((h >> e) & 1u) << qh_bit(e);
@@ -361,10 +450,11 @@ __device__ inline float quant_q(float v) {
 template <int NP, int WPR, bool LN>
 __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ a, int m, int k, int nb,
                                                       uint16_t *__restrict__ a16, float *__restrict__ rs,
-                                                      const float *__restrict__ lnw, const float *__restrict__ lnb) {
+                                                      float *__restrict__ ps, const float *__restrict__ lnw,
+                                                      const float *__restrict__ lnb) {
   static_assert(WPR == 1 || WPR == 2 || WPR == 4, "a workgroup holds whole rows");
   __shared__ float part_max[4];
-  __shared__ float part_sum[2][4];
+  __shared__ float part_sum[3][4];
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // workgroup 8j + x runs on XCD x; the 8 * WPR workgroups of a row group
   // all take the same x, so the group's interleaved f16 lines are written
@@ -477,7 +567,11 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
         const int bl = first(c, p) + lb;
         if (bl < nb) *reinterpret_cast<uint2 *>(a16 + a16_index(nb, g, bl, r, 4 * lt)) = make_uint2(0u, 0u);
       }
-    if (part == 0 && lane == 0) rs[row] = 0.0f;
+    row_sum(0.0f, 2);  // the row-sum reduction's barrier, as the live rows
+    if (part == 0 && lane == 0) {
+      rs[row] = 0.0f;
+      ps[row] = 0.0f;
+    }
     return;
   }
   int e = 15;  // zero, inf or NaN rows: no scaling
@@ -487,6 +581,7 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
   }
   const float down = ldexpf(1.0f, 15 - e);
   constexpr int NC = (NP + 7) / 8;
+  float ptot = 0.0f;  // this lane's blocks' d_a * sum(q_a) (one lane per block)
   for (int c = 0; c < nch; ++c) {
     if (nch > 1) {
       load(c);
@@ -508,9 +603,13 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
       const int b0 = first(c, p);
       if (b0 >= nb) return;  // uniform
       const float inv = bcast8<p & 7>(iv[p >> 3], lt);
-      const float dd = bcast8<p & 7>(dv[p >> 3], lt) * down;
+      const float da = bcast8<p & 7>(dv[p >> 3], lt);
+      const float dd = da * down;
       const float q0 = quant_q(__fmul_rn(v[p].x, inv)), q1 = quant_q(__fmul_rn(v[p].y, inv));
       const float q2 = quant_q(__fmul_rn(v[p].z, inv)), q3 = quant_q(__fmul_rn(v[p].w, inv));
+      // the block's sum(q_a) (exact integers), times d_a, counted once
+      const int bsum = sum8((int)q0 + (int)q1 + (int)q2 + (int)q3);
+      if (lt == 0) ptot += __fmul_rn(da, (float)bsum);
       const h2v lo2 = {(_Float16)__fmul_rn(q0, dd), (_Float16)__fmul_rn(q1, dd)};
       const h2v hi2 = {(_Float16)__fmul_rn(q2, dd), (_Float16)__fmul_rn(q3, dd)};
       if (b0 + lb < nb) {
@@ -523,7 +622,11 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
       (pass(std::integral_constant<int, P>{}), ...);
     }(std::make_integer_sequence<int, NP>{});
   }
-  if (part == 0 && lane == 0) rs[row] = ldexpf(1.0f, e - 15);
+  ptot = row_sum(ptot, 2);
+  if (part == 0 && lane == 0) {
+    rs[row] = ldexpf(1.0f, e - 15);
+    ps[row] = ptot;
+  }
 }
 
 // --------------------------------------------------- MFMA operand unpack
@@ -1190,12 +1293,15 @@ struct GemmSet {
   int count, nb, nb_pad;
 };
 
-// Encoder-shape GEMM (m > 8): out = rs * (A' W'^T) (+ bias), with A' the f16
-// values of the quantized activations (k_quantize_f16) and W' = f16(d_b*q_b
-// + m_b) formed in registers from the byte plane with one packed f16 fma per
-// two weights (a single rounding).  Products of f16 operands are exact and
-// accumulate in f32 inside v_mfma_f32_32x32x16_f16, so |y - exact| <=
-// 2^-10 sum|a||w| plus the f32 accumulation error.
+// Encoder-shape GEMM (m > 8): out = rs * (A' W'^T) * cs + cm * ps (+ bias),
+// with A' the f16 values of the quantized activations (k_quantize_f16), ps
+// their exact row sums, and W' = f16((d_b*q_b + m_b - cm) / cs) formed in
+// registers from the byte plane with one packed f16 fma per two weights (a
+// single rounding; cs and cm are the weight row's power of two and offset,
+// so W' never overflows and rounds relative to the row's spread).  Products
+// of f16 operands are exact and accumulate in f32 inside
+// v_mfma_f32_32x32x16_f16, so |y - exact| <= 2^-10 sum|a||w - cm| plus the
+// f32 accumulation error.
 // A launch covers up to GEMM_MAX_SET weights that share the activation (the
 // column tiles of the launch run through the weights in turn).  A
 // workgroup owns one tile of TM activation row groups x TN weight row
@@ -1335,16 +1441,24 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int
   // last one)
   constexpr int TPW = KW > 1 ? TM / KW : TM;  // row groups finished per wavefront
   static_assert(KW == 1 || TM % KW == 0, "row groups split evenly over the k-waves");
-  float4 sc[TPW][4];
-  float bv[TN];
+  float4 sc[TPW][4], pv[TPW][4];
+  float bv[TN], cv[TN], mv[TN];
 #pragma unroll
   for (int ii = 0; ii < TPW; ++ii) {
     const int tg = min(by * TM + (KW > 1 ? kw * TPW + ii : ii), a.mgroups - 1);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) sc[ii][q] = ldg_f4(a.rs + tg * RG + 8 * q + 4 * h);
+    for (int q = 0; q < 4; ++q) {
+      sc[ii][q] = ldg_f4(a.rs + tg * RG + 8 * q + 4 * h);
+      pv[ii][q] = ldg_f4(a.ps + tg * RG + 8 * q + 4 * h);
+    }
   }
 #pragma unroll
-  for (int j = 0; j < TN; ++j) bv[j] = bias ? ldg_f(bias + min((bx * TN + j) * RG + r, n - 1)) : 0.0f;
+  for (int j = 0; j < TN; ++j) {
+    const int wr = min(bx * TN + j, ngroups - 1) * RG + r;  // weight row (padding rows: cs 1, cm 0)
+    bv[j] = bias ? ldg_f(bias + min((bx * TN + j) * RG + r, n - 1)) : 0.0f;
+    cv[j] = ldg_f(gp.cs + wr);
+    mv[j] = ldg_f(gp.cm + wr);
+  }
   float4 *red = reinterpret_cast<float4 *>(lds);
   if (KW > 1) {
 #pragma unroll
@@ -1388,11 +1502,14 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int
         } else {
           v = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
         }
-        const float4 c = sc[ii][q];
-        y[4 * q] = v.x * c.x;
-        y[4 * q + 1] = v.y * c.y;
-        y[4 * q + 2] = v.z * c.z;
-        y[4 * q + 3] = v.w * c.w;
+        // row scale, then column scale: both powers of two, so exact (the
+        // row scale first keeps the intermediate in range); then the weight
+        // row's offset times the activation row's sum, one rounding
+        const float4 c = sc[ii][q], pp = pv[ii][q];
+        y[4 * q] = __builtin_fmaf(mv[j], pp.x, (v.x * c.x) * cv[j]);
+        y[4 * q + 1] = __builtin_fmaf(mv[j], pp.y, (v.y * c.y) * cv[j]);
+        y[4 * q + 2] = __builtin_fmaf(mv[j], pp.z, (v.z * c.z) * cv[j]);
+        y[4 * q + 3] = __builtin_fmaf(mv[j], pp.w, (v.w * c.w) * cv[j]);
         if (bias) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) y[4 * q + e] += bv[j];

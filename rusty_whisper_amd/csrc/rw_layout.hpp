@@ -37,7 +37,10 @@
 // GEMM planes (weights), indexed like qs:
 //   q8  [ngroups][nb_pad][32 rows][32 B]  every quant as one byte in MFMA
 //        order (Q4/Q5 the unsigned value as stored; Q8_0 reads qs itself)
-//   dm  [ngroups][nb_pad][32 rows]        u32: f16 d_b (low), f16 m_b (high)
+//   dm  [ngroups][nb_pad][32 rows]        u32: f16 d_b (low), f16 m_b - cm
+//        (high), both divided by the row's power-of-two scale cs (GemmPlanes)
+//   cs  [ngroups][32 rows]                f32 2^s per row
+//   cm  [ngroups][32 rows]                f32 offset per row
 //
 // Quantized activations ([m, k] f32 in, quantize_acts_i8 semantics) are
 // written by the quantize kernels in the same row-group form:
@@ -49,6 +52,7 @@
 //   f16 layout (encoder GEMM):
 //     a16 f16(d_a * q_a * 2^(15 - e_row)) at a16_index (below), one rounding
 //     rs  [rows] f32 2^(e_row - 15), applied to the GEMM's output rows
+//     ps  [rows] f32 sum over the row's blocks of d_a * sum(q_a)
 //
 // Decode records (k_gemv, k_gemv_records): per block of an m-row activation,
 // the rows' 32 int8 quants in MFMA order, 16 zero bytes (the A operand of
@@ -98,6 +102,7 @@ struct ActView {
   const int32_t *sa;    // sum(q_a)
   const uint16_t *a16;  // f16(d_a * q_a * 2^-e_row), GEMM operand order (a16_index)
   const float *rs;      // 2^e_row per row
+  const float *ps;      // per row: sum over blocks of d_a * sum(q_a), in f32
   int nb, mgroups;
 };
 
@@ -105,9 +110,24 @@ struct ActView {
 // q8 holds every quant as one byte, in MFMA order within the block, biased to
 // unsigned: the 4/5-bit quants as stored (0..15 / 0..31), Q8_0 as q + 128
 // (for Q8_0 the plane is qs itself, read with the sign bit flipped).
+//
+// Each weight row j carries an offset cm[j] (the mean of its finite values
+// d*q + m) and a power of two cs[j] = 2^s_j, chosen at upload so that the
+// row's largest finite |d*q + m - cm|, |d| or |m - cm| lands in [2^14, 2^15)
+// once divided by it.  dm holds f16(d_b / cs[j]) and f16((m_b - cm[j]) /
+// cs[j]), so the f16 operand (d*q + m - cm) / cs never overflows, keeps
+// f16's full precision for every value above 2^-28 of the row's largest,
+// whatever the block scales are, and rounds relative to the row's spread
+// rather than to a common offset (a row of Q4_1 / Q5_1 blocks whose mins
+// dwarf their ranges).  The GEMM multiplies its output column j by cs[j]
+// and adds cm[j] * P_i, P_i the exact sum of activation row i's quantized
+// values (ActView::ps), as the reference adds each block's min term
+// m_b * d_a * sum(q_a) in f32.
 struct GemmPlanes {
   const uint8_t *q8;   // [group][nb_pad][32][32]
-  const uint32_t *dm;  // f16 d_b (low half) and m_b (high half, 0 for _0 formats)
+  const uint32_t *dm;  // f16 d_b / cs (low half) and (m_b - cm) / cs (high half)
+  const float *cs;     // [group * 32] 2^s per weight row (1 for padding rows)
+  const float *cm;     // [group * 32] the row's offset (0 for padding rows)
 };
 
 // element offsets

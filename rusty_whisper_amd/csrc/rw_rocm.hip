@@ -30,6 +30,7 @@
 #include "rw_attn.hpp"
 #include "rw_kernels.hpp"
 #include "rw_dec.hpp"
+#include "rw_pool.hpp"
 #include "rw_rocm.h"
 
 using namespace rw;
@@ -78,6 +79,7 @@ static int bb_of(int dtype) {
 }
 
 static size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+static bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 static size_t cdiv(size_t a, size_t b) { return (a + b - 1) / b; }
 
 // ------------------------------------------------------------ devices
@@ -176,25 +178,35 @@ struct CtxGuard {
   }
 };
 
-// per-(device, stream) workspaces for rw_rocm_matmul_t_q_dev(workspace=NULL)
-static std::mutex g_sws_mu;
-static std::map<std::pair<int, void *>, std::pair<void *, size_t>> g_stream_ws;
+// Per-(device, stream) workspaces for the device-pointer entries called
+// without a caller workspace.  The caller holds its stream's buffer until its
+// launches are queued (rw_pool.hpp): no other thread frees or grows it
+// meanwhile, and launches of two threads on one stream never interleave
+// over it.
+using StreamKey = std::pair<int, void *>;
+using WsPool = WorkspacePool<StreamKey>;
+using WsHold = HoldWs<WsPool>;
 
-static int stream_workspace(int device, void *stream, size_t bytes, void **out) {
-  std::lock_guard<std::mutex> lk(g_sws_mu);
-  auto &slot = g_stream_ws[std::make_pair(device, stream)];
-  if (slot.second < bytes) {
-    if (slot.first) HIP_TRY(hipFree(slot.first));
-    slot.first = nullptr;
-    slot.second = 0;
-    size_t want = align_up(bytes, (size_t)1 << 20);
-    if (hipMalloc(&slot.first, want) != hipSuccess) {
-      (void)hipGetLastError();
-      return fail(RW_ENOMEM, "hipMalloc(%zu) for a stream workspace failed", want);
-    }
-    slot.second = want;
+static int ws_alloc(size_t bytes, void **out) {
+  if (hipMalloc(out, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return RW_ENOMEM;
   }
-  *out = slot.first;
+  return RW_OK;
+}
+static void ws_free(void *p) { (void)hipFree(p); }
+static WsPool &ws_pool() {
+  static WsPool *pool = new WsPool(ws_alloc, ws_free, (size_t)1 << 20);  // lives until the process ends
+  return *pool;
+}
+
+static int stream_workspace(int device, void *stream, size_t bytes, WsHold &hold, void **out) {
+  WsPool::Slot *slot = nullptr;
+  if (ws_pool().acquire(std::make_pair(device, stream), bytes, &slot))
+    return fail(RW_ENOMEM, "hipMalloc(%zu) for a stream workspace failed", bytes);
+  hold.pool = &ws_pool();
+  hold.slot = slot;
+  *out = slot->p;
   return RW_OK;
 }
 
@@ -208,7 +220,7 @@ constexpr size_t GEMV_MAX_M = 8;
 struct ActLayout {
   int nb, mgroups;
   bool f16;
-  size_t off_qa, off_da, off_pa, off_sa, off_a16, off_rs, bytes;
+  size_t off_qa, off_da, off_pa, off_sa, off_a16, off_rs, off_ps, bytes;
 };
 
 static ActLayout act_layout_kind(size_t m, size_t k, bool f16) {
@@ -218,11 +230,12 @@ static ActLayout act_layout_kind(size_t m, size_t k, bool f16) {
   L.f16 = f16;
   size_t rows = (size_t)L.mgroups * RG;
   size_t nsc = rows * L.nb;
-  L.off_qa = L.off_da = L.off_pa = L.off_sa = L.off_a16 = L.off_rs = 0;
+  L.off_qa = L.off_da = L.off_pa = L.off_sa = L.off_a16 = L.off_rs = L.off_ps = 0;
   if (f16) {
     L.off_a16 = 0;
     L.off_rs = align_up(rows * k * 2, 256);
-    L.bytes = align_up(L.off_rs + rows * 4, 256);
+    L.off_ps = align_up(L.off_rs + rows * 4, 256);
+    L.bytes = align_up(L.off_ps + rows * 4, 256);
   } else {
     L.off_qa = 0;
     L.off_da = align_up(rows * k, 256);
@@ -237,10 +250,11 @@ static ActLayout act_layout(size_t m, size_t k) { return act_layout_kind(m, k, m
 
 static ActView act_view(const ActLayout &L, void *ws) {
   char *b = (char *)ws;
-  ActView v{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, L.nb, L.mgroups};
+  ActView v{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, L.nb, L.mgroups};
   if (L.f16) {
     v.a16 = (const uint16_t *)(b + L.off_a16);
     v.rs = (const float *)(b + L.off_rs);
+    v.ps = (const float *)(b + L.off_ps);
   } else {
     v.qa = (const int8_t *)(b + L.off_qa);
     v.da = (const float *)(b + L.off_da);
@@ -264,10 +278,10 @@ static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &
     // blocks per wavefront in registers (longer rows are read twice)
     const size_t g8 = align_up((size_t)L.mgroups, 8);  // row groups, padded to whole XCD rounds
     uint16_t *a16 = (uint16_t *)(b + L.off_a16);
-    float *rs = (float *)(b + L.off_rs);
+    float *rs = (float *)(b + L.off_rs), *ps = (float *)(b + L.off_ps);
 #define RW_QF16(NP, WPR, LN)                                                                                \
   hipLaunchKernelGGL((k_quantize_f16<NP, WPR, LN>), dim3((unsigned)(g8 * RG * WPR / 4)), dim3(256), 0, s, a,     \
-                     (int)m, (int)k, L.nb, a16, rs, lnw, lnb)
+                     (int)m, (int)k, L.nb, a16, rs, ps, lnw, lnb)
     const int passes = (L.nb + 7) / 8;
     if (lnw) {
       if (passes <= 1) RW_QF16(1, 1, true);
@@ -752,12 +766,16 @@ static int attn_nsplit(size_t groups, size_t nblk) {
   return 1;
 }
 
-static AttnLayout attn_layout(size_t t_q, size_t t_kv, size_t n_state) {
+// kv_planes = false: the call reads K/V planes split beforehand (the
+// decoder's cross-attention), so the layout holds q's planes and the split
+// runs' partial results only
+static AttnLayout attn_layout(size_t t_q, size_t t_kv, size_t n_state, bool kv_planes = true) {
   AttnLayout L{};
   L.n_head = (int)(n_state / ATT_DH);
   L.tq_pad = (int)align_up(t_q, ATT_QB);
   L.tkv_pad = (int)align_up(t_kv, ATT_KVB);
-  const size_t qb = (size_t)L.n_head * L.tq_pad * ATT_DH * 2, kb = (size_t)L.n_head * L.tkv_pad * ATT_DH * 2;
+  const size_t qb = (size_t)L.n_head * L.tq_pad * ATT_DH * 2;
+  const size_t kb = kv_planes ? (size_t)L.n_head * L.tkv_pad * ATT_DH * 2 : 0;
   L.off_qh = 0;
   L.off_ql = align_up(L.off_qh + qb, 256);
   L.off_kh = align_up(L.off_ql + qb, 256);
@@ -891,9 +909,13 @@ static int check_decoder_params(const rw_decoder_params *P) {
     if (!L.fc1 || !L.fc2 || L.fc1->k != n || L.fc1->n != f || L.fc2->n != n || L.fc2->k != f)
       return fail(RW_EINVAL, "layer %d: fc1 must be [f, %zu] and fc2 [%zu, f]", l, n, n);
     const float *vec[6] = {L.attn_ln_w, L.attn_ln_b, L.cross_ln_w, L.cross_ln_b, L.mlp_ln_w, L.mlp_ln_b};
-    for (const float *v : vec)
+    for (const float *v : vec) {
       if (!v) return fail(RW_EINVAL, "layer %d: a layernorm vector is NULL", l);
+      // the products that fold a layernorm in read it 16 bytes at a time
+      if (!al16(v)) return fail(RW_EINVAL, "layer %d: layernorm vectors must be 16-byte aligned", l);
+    }
   }
+  if (!al16(P->ln_w) || !al16(P->ln_b)) return fail(RW_EINVAL, "the final layernorm vectors must be 16-byte aligned");
   return RW_OK;
 }
 
@@ -906,7 +928,7 @@ static DecScratch dec_scratch(const rw_decoder *d, size_t n_tok) {
   DecScratch S{};
   const size_t row = n_tok * d->n * 4;
   S.self_att = attn_layout(n_tok, d->p.n_ctx, d->n);
-  S.cross_att = attn_layout(n_tok, d->n_audio, d->n);
+  S.cross_att = attn_layout(n_tok, d->n_audio, d->n, false);  // K/V: the window's kept planes
   S.off_tok = 0;
   S.off_x = align_up(n_tok * 4, 256);
   S.off_cur = align_up(S.off_x + row, 256);
@@ -1009,7 +1031,6 @@ static LayerLayout layer_layout(size_t n, size_t f, size_t t) {
   return L;
 }
 
-static bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 static int check_layer(const rw_encoder_layer *E, size_t t) {
   if (!E) return fail(RW_EINVAL, "layer is NULL");
@@ -1143,7 +1164,9 @@ int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, siz
   size_t off_m = align_up(off_d + nsc * 2, 256);
   size_t off_dm = align_up(off_m + (has_min(dtype) ? nsc * 2 : 0), 256);
   size_t off_q8 = align_up(off_dm + nsc * 4, 256);  // the GEMM's byte plane (Q8_0 reads qs)
-  w->bytes = align_up(off_q8 + (dtype == RW_Q8_0 ? 0 : nsc * 32), 256);
+  size_t off_cs = align_up(off_q8 + (dtype == RW_Q8_0 ? 0 : nsc * 32), 256);  // the GEMM's row scales
+  size_t off_cm = align_up(off_cs + rows * 4, 256);                             // and row offsets
+  w->bytes = align_up(off_cm + rows * 4, 256);
   // the kernels address each plane with 32-bit byte offsets
   if (nsc * 32 >= ((size_t)1 << 32)) {
     delete w;
@@ -1157,7 +1180,8 @@ int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, siz
   char *b = (char *)w->base;
   w->view = WeightView{(const uint8_t *)b, (const uint32_t *)(b + off_qh), (const uint16_t *)(b + off_d),
                        (const uint16_t *)(b + off_m), w->nb, w->nb_pad, w->noct, w->ngroups};
-  w->gemm = GemmPlanes{(const uint8_t *)(dtype == RW_Q8_0 ? b : b + off_q8), (const uint32_t *)(b + off_dm)};
+  w->gemm = GemmPlanes{(const uint8_t *)(dtype == RW_Q8_0 ? b : b + off_q8), (const uint32_t *)(b + off_dm),
+                       (const float *)(b + off_cs), (const float *)(b + off_cm)};
 
   void *tmp = nullptr;
   hipError_t e = hipMalloc(&tmp, raw_len);
@@ -1165,11 +1189,14 @@ int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, siz
   if (e == hipSuccess) {
     size_t threads = nsc;
     dim3 grid((unsigned)cdiv(threads, 256));
+    // the GEMM's row scales first (one wavefront per row), then the planes
 #define RW_REPACK(DT)                                                                                      \
+  hipLaunchKernelGGL(k_row_scale<DT>, dim3((unsigned)cdiv(rows, 4)), dim3(256), 0, 0, (const uint8_t *)tmp,   \
+                     (int)n, (int)nb, (int)rows, (float *)(b + off_cs), (float *)(b + off_cm));           \
   hipLaunchKernelGGL(k_repack<DT>, grid, dim3(256), 0, 0, (const uint8_t *)tmp, (int)n, (int)nb, (uint8_t *)b, \
                      (uint32_t *)(b + off_qh), (uint16_t *)(b + off_d), (uint16_t *)(b + off_m),                \
                      (uint32_t *)(b + off_dm), (uint8_t *)(b + off_q8), w->nb_pad,                        \
-                     w->noct, w->ngroups)
+                     w->noct, w->ngroups, (const float *)(b + off_cs), (const float *)(b + off_cm))
     switch (dtype) {
       case RW_Q4_0: RW_REPACK(RW_Q4_0); break;
       case RW_Q4_1: RW_REPACK(RW_Q4_1); break;
@@ -1225,12 +1252,13 @@ int rw_rocm_matmul_t_q_dev(const rw_weight *w, const float *a, size_t m, size_t 
   HIP_TRY(hipSetDevice(w->device));
   size_t need = act_layout(m, k).bytes;
   void *ws = workspace;
+  WsHold hold;  // the stream's workspace, held until the launches are queued
   if (m <= GEMV_MAX_M) {
     ws = nullptr;  // the decode shape quantizes inside its launch
   } else if (ws) {
     if (workspace_len < need) return fail(RW_EINVAL, "workspace of %zu bytes < %zu needed", workspace_len, need);
   } else {
-    rc = stream_workspace(w->device, stream, need, &ws);
+    rc = stream_workspace(w->device, stream, need, hold, &ws);
     if (rc) return rc;
   }
   return run_matmul(w, a, m, bias, out, ws, (hipStream_t)stream);
@@ -1329,10 +1357,11 @@ int rw_rocm_matmul_grouped_dev(const rw_linear *items, size_t count, void *works
   const int device = items[0].w->device;
   HIP_TRY(hipSetDevice(device));
   void *ws = workspace;
+  WsHold hold;
   if (ws) {
     if (workspace_len < P.total) return fail(RW_EINVAL, "workspace of %zu bytes < %zu needed", workspace_len, P.total);
   } else {
-    int rc = stream_workspace(device, stream, P.total, &ws);
+    int rc = stream_workspace(device, stream, P.total, hold, &ws);
     if (rc) return rc;
   }
   hipStream_t s = (hipStream_t)stream;
@@ -1531,10 +1560,11 @@ int rw_rocm_attention_dev(const float *q, size_t ldq, const float *k, size_t ldk
   if (rc) return rc;
   const AttnLayout L = attn_layout(t_q, t_kv, n_state);
   void *ws = workspace;
+  WsHold hold;
   if (ws) {
     if (workspace_len < L.bytes) return fail(RW_EINVAL, "workspace of %zu bytes < %zu needed", workspace_len, L.bytes);
   } else {
-    rc = stream_workspace(dev, stream, L.bytes, &ws);
+    rc = stream_workspace(dev, stream, L.bytes, hold, &ws);
     if (rc) return rc;
   }
   return run_attention(q, ldq, k, ldk, v, ldv, t_q, t_kv, n_head, causal, out, ldo, L, ws, (hipStream_t)stream);
@@ -1635,6 +1665,7 @@ static int dec_reserve(rw_decoder *d, size_t bytes) {
 
 int rw_rocm_decoder_set_audio_dev(rw_decoder *d, const float *enc_out, void *stream) {
   if (!d || !enc_out) return fail(RW_EINVAL, "decoder or encoder output is NULL");
+  if (!al16(enc_out)) return fail(RW_EINVAL, "the encoder output must be 16-byte aligned");
   if (d->cross.use_count() > 1) return fail(RW_EINVAL, "the cross K/V are shared with a fork; set audio on a fresh decoder");
   HIP_TRY(hipSetDevice(d->device));
   hipStream_t s = (hipStream_t)stream;
@@ -1747,10 +1778,11 @@ int rw_rocm_encoder_layer_dev(const rw_encoder_layer *layer, float *x, size_t t,
   HIP_TRY(hipSetDevice(layer->q->device));
   const size_t need = layer_layout(layer->q->k, layer->fc1->n, t).bytes;
   void *ws = workspace;
+  WsHold hold;
   if (ws) {
     if (workspace_len < need) return fail(RW_EINVAL, "workspace of %zu bytes < %zu needed", workspace_len, need);
   } else {
-    rc = stream_workspace(layer->q->device, stream, need, &ws);
+    rc = stream_workspace(layer->q->device, stream, need, hold, &ws);
     if (rc) return rc;
   }
   return run_encoder_layer(layer, x, t, ws, (hipStream_t)stream);

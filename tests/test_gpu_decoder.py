@@ -112,3 +112,53 @@ def test_decoder_long_cache(torch):
     print("  errors", ["%.2g" % e for e in errs], flush=True)
     assert d.n_past == 303
     assert max(errs) <= TOL, errs
+
+
+def test_decoder_mixed_qkv_dtypes(torch):
+    """q, k and v of different dtypes (Q5_0 / Q8_0 / Q5_0): the step's
+    layernorm runs alone and the three products go one by one, in both
+    product regimes (a 12-token prompt, then single tokens)."""
+    n, heads, n_audio = 256, 4, 120
+    p = decoder_params(n=n, f=4 * n, n_layer=2, n_vocab=300, n_ctx=40, dtype=6, seed=17, dtypes={"k": 8})
+    enc = np.random.default_rng(17).standard_normal((n_audio, n)).astype(np.float32)
+    d = device_decoder(torch, p, heads, n_audio)
+    d.set_audio(torch.from_numpy(enc).to("cuda:0"))
+    o = OD(p, heads, enc)
+    prompt = list(range(3, 15))
+    errs = [rel(step(torch, d, prompt, n), o.forward_hidden(prompt))]
+    for t in (17, 250, 4):
+        errs.append(rel(step(torch, d, [t], n), o.forward_hidden([t])))
+    print("  errors", ["%.2g" % e for e in errs], flush=True)
+    assert max(errs) <= TOL, errs
+
+
+def test_large_v3_decoder_slice_with_logits(torch):
+    """The large-v3 decoder's shapes (n = 1280, 20 heads, fc 5120, vocabulary
+    51866, 1500 audio rows, 448 context rows) on two of its 32 layers, Q5_0:
+    a 3-token prompt and three single-token steps against the oracle, and the
+    tied-embedding logits [51866 x 1280] (src/decoder.rs:315-321) of every
+    step against the oracle's product of the same hidden rows."""
+    import oracle as O
+    from _data import rel_row_l2
+
+    n, heads, n_audio, n_vocab = 1280, 20, 1500, 51866
+    p = decoder_params(n=n, f=4 * n, n_layer=2, n_vocab=n_vocab, n_ctx=448, dtype=6, seed=1280)
+    enc = np.random.default_rng(1280).standard_normal((n_audio, n)).astype(np.float32)
+    print("large-v3 decoder slice: 2 layers, vocab 51866, 1500 audio rows", flush=True)
+    d = device_decoder(torch, p, heads, n_audio)
+    d.set_audio(torch.from_numpy(enc).to("cuda:0"))
+    o = OD(p, heads, enc)
+    tok = d.token_embedding
+    errs, lerrs = [], []
+    for toks in ([50258, 50259, 50359], [440], [3111], [50257]):
+        h = step(torch, d, toks, n)
+        errs.append(rel(h, o.forward_hidden(toks)))
+        hd = torch.from_numpy(h).to("cuda:0")
+        logits = torch.empty(len(toks), n_vocab, device="cuda:0")
+        tok.matmul_dev(hd, len(toks), logits)
+        torch.cuda.synchronize()
+        ref = O.matmul_emul(h, 6, p["tok"]["raw"], n_vocab)
+        lerrs.append(rel_row_l2(logits.cpu().numpy(), ref))
+    print("  hidden errors", ["%.2g" % e for e in errs], "logits errors", ["%.2g" % e for e in lerrs], flush=True)
+    assert max(errs) <= TOL, errs
+    assert max(lerrs) <= 1e-3, lerrs

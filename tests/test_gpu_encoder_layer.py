@@ -29,11 +29,16 @@ def rel_row(got, ref):
     return float(np.max(np.max(np.abs(got - ref), axis=1) / np.linalg.norm(ref, axis=1)))
 
 
-def build(torch, n, f, dtype, seed, wscale=0.05):
+def build(torch, n, f, dtype, seed, wscale=0.05, spread=False):
+    """Layer parameters; `spread` scales every weight block by 10**U(-1, 1)."""
     rng = np.random.default_rng(seed)
     p, dev = {}, {}
     for name, rows, cols in (("q", n, n), ("k", n, n), ("v", n, n), ("out", n, n), ("fc1", f, n), ("fc2", n, f)):
-        raw = O.quantize(dtype, (rng.standard_normal((rows, cols)) * wscale).astype(np.float32))
+        x = (rng.standard_normal((rows, cols)) * wscale).astype(np.float32)
+        if spread:
+            s = (10.0 ** rng.uniform(-1.0, 1.0, size=(rows, cols // 32, 1))).astype(np.float32)
+            x = (x.reshape(rows, cols // 32, 32) * s).reshape(rows, cols)
+        raw = O.quantize(dtype, x)
         p[name] = {"dtype": dtype, "raw": raw, "n": rows}
         dev[name] = A.DeviceWeight(dtype, rows, cols, raw)
     for name, size, s, c in (("attn_ln_w", n, 0.1, 1.0), ("attn_ln_b", n, 0.1, 0.0), ("q_b", n, 0.1, 0.0),
@@ -45,13 +50,21 @@ def build(torch, n, f, dtype, seed, wscale=0.05):
     return p, dev
 
 
-@pytest.mark.parametrize("t,n,dtype", [(1500, 384, 7), (200, 512, 8), (37, 256, 2), (1500, 1280, 7)],
+# (t, n, dtype, variant): tiny.en and large-v3 in Q5_1; small.en in Q8_0 with
+# 1% of the input channels x20; large-v3 in Q4_0 and Q4_1 with every weight
+# block scaled by 10**U(-1, 1)
+@pytest.mark.parametrize("t,n,dtype,variant", [(1500, 384, 7, ""), (200, 512, 8, ""), (37, 256, 2, ""),
+                                               (1500, 1280, 7, ""), (1500, 768, 8, "outliers"),
+                                               (1500, 1280, 2, "spread"), (1500, 1280, 3, "spread")],
                          ids=lambda x: str(x))
-def test_encoder_layer_parity(torch, t, n, dtype):
+def test_encoder_layer_parity(torch, t, n, dtype, variant):
     heads, f = n // 64, 4 * n
-    print(f"encoder layer t={t} n={n} dtype={dtype}", flush=True)
-    p, dev = build(torch, n, f, dtype, seed=t + n)
+    print(f"encoder layer t={t} n={n} dtype={dtype} {variant}", flush=True)
+    p, dev = build(torch, n, f, dtype, seed=t + n, spread=variant == "spread")
     x = np.random.default_rng(t).standard_normal((t, n)).astype(np.float32)
+    if variant == "outliers":
+        ch = np.random.default_rng(n).choice(n, size=max(1, n // 100), replace=False)
+        x[:, ch] *= np.float32(20.0)
     layer = A.EncoderLayer(heads, **dev)
     xd = torch.from_numpy(x).to("cuda:0")
     layer.run(xd, t)
