@@ -124,6 +124,23 @@ int rw_rocm_matmul_t_q_dev(const rw_weight *w, const float *a, size_t m, size_t 
 /* Workspace bytes rw_rocm_matmul_t_q_dev needs for an [m, k] activation. */
 size_t rw_rocm_matmul_workspace_size(size_t m, size_t k);
 
+/* rw_rocm_matmul_t_q_dev without any allocation: the same kernels and bit
+ * for bit the same results, with the quantized activation kept in a fixed
+ * RW_NOALLOC_SCRATCH_BYTES array of device memory that each GPU running the
+ * library holds until the process ends.  No hipMalloc, hipFree or other
+ * allocating call happens inside it.  Inputs whose workspace
+ * (rw_rocm_matmul_workspace_size) exceeds the array are rejected with
+ * RW_EINVAL; 16 MiB covers m = 1500 rows at k = 5120.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (two streams, or
+ * two threads) race on it, so a caller orders them.  Call rw_rocm_init for
+ * the device first where possible (it looks the array's address up; the
+ * first call on a device does otherwise).  Has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid it). */
+#define RW_NOALLOC_SCRATCH_BYTES (16 << 20)
+int rw_rocm_matmul_t_q_dev_noalloc(const rw_weight *w, const float *a, size_t m, size_t k,
+                                   const float *bias, float *out, void *stream);
+
 /* The two halves of rw_rocm_matmul_t_q_dev, for callers that reuse one
  * quantized activation across several weights.  rw_rocm_quantize_dev runs
  * quantize_acts_i8 (src/quant.rs:691-716) on device a[m, k] into `workspace`;

@@ -58,6 +58,8 @@ _SIGNATURES = {
     "rw_rocm_matmul_t_q_dev": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p,
                                          C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
     "rw_rocm_matmul_workspace_size": (C.c_size_t, [C.c_size_t, C.c_size_t]),
+    "rw_rocm_matmul_t_q_dev_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p,
+                                                 C.c_void_p, C.c_void_p]),
     "rw_rocm_quantize_dev": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_size_t,
                                        C.c_void_p]),
     "rw_rocm_matmul_prequant_dev": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p,
@@ -200,6 +202,10 @@ class DeviceWeight:
         """Device pointers (ints or torch tensors), queued on `stream`."""
         check(lib().rw_rocm_matmul_t_q_dev(self.handle, _ptr(a), m, self.k, _ptr(bias), _ptr(out),
                                            _ptr(workspace), workspace_len, stream))
+
+    def matmul_dev_noalloc(self, a, m: int, out, bias=None, stream: int | None = None) -> None:
+        """matmul_dev with the library's fixed device scratch (no allocation)."""
+        check(lib().rw_rocm_matmul_t_q_dev_noalloc(self.handle, _ptr(a), m, self.k, _ptr(bias), _ptr(out), stream))
 
     def matmul_prequant_dev(self, workspace, m: int, out, bias=None, stream: int | None = None) -> None:
         """out = (activations quantized into `workspace`) W^T (+ bias)."""

@@ -210,6 +210,33 @@ static int stream_workspace(int device, void *stream, size_t bytes, WsHold &hold
   return RW_OK;
 }
 
+// The workspace of rw_rocm_matmul_t_q_dev_noalloc: a fixed array in device
+// memory that every GPU running this library holds until the process ends
+// (no hipMalloc at call time).  Host code never passes `scratch` itself to a
+// kernel -- its host-side name is only a handle -- but the device address
+// hipGetSymbolAddress returns for the current device, taken once per device.
+static __device__ __align__(256) uint8_t scratch[RW_NOALLOC_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mu;
+static std::map<int, void *> g_scratch_ptr;  // device -> address of its scratch
+
+// with `device` current
+static int scratch_setup(int device, void **out) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  auto it = g_scratch_ptr.find(device);
+  if (it == g_scratch_ptr.end()) {
+    void *ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      (void)hipGetLastError();
+      return fail(RW_EHIP, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+    }
+    it = g_scratch_ptr.emplace(device, ptr).first;
+  }
+  if (out) *out = it->second;
+  return RW_OK;
+}
+
 // ----------------------------------------------- activation workspace
 
 // Products with m <= GEMV_MAX_M read the int8 layout (qa, da, pa, sa); the
@@ -1123,7 +1150,7 @@ int rw_rocm_init(int device) {
   int rc = check_device(device);
   if (rc) return rc;
   HIP_TRY(hipSetDevice(device));
-  return RW_OK;
+  return scratch_setup(device, nullptr);
 }
 
 int rw_rocm_block_bytes(int dtype) {
@@ -1262,6 +1289,24 @@ int rw_rocm_matmul_t_q_dev(const rw_weight *w, const float *a, size_t m, size_t 
     if (rc) return rc;
   }
   return run_matmul(w, a, m, bias, out, ws, (hipStream_t)stream);
+}
+
+int rw_rocm_matmul_t_q_dev_noalloc(const rw_weight *w, const float *a, size_t m, size_t k, const float *bias,
+                                   float *out, void *stream) {
+  int rc = check_matmul_args(w, a, m, k, out);
+  if (rc) return rc;
+  if (m == 0) return RW_OK;
+  const size_t need = m <= GEMV_MAX_M ? 0 : act_layout(m, k).bytes;  // the decode shape needs none
+  if (need > (size_t)RW_NOALLOC_SCRATCH_BYTES)
+    return fail(RW_EINVAL, "[%zu, %zu] activation needs %zu workspace bytes, more than the %d of the fixed scratch", m,
+                k, need, RW_NOALLOC_SCRATCH_BYTES);
+  HIP_TRY(hipSetDevice(w->device));
+  void *ws = nullptr;
+  rc = scratch_setup(w->device, &ws);
+  if (rc) return rc;
+  // every byte the product reads is written by its quantizer first (padding
+  // rows included), so nothing needs clearing between calls
+  return run_matmul(w, a, m, bias, out, m <= GEMV_MAX_M ? nullptr : ws, (hipStream_t)stream);
 }
 
 int rw_rocm_quantize_dev(const float *a, size_t m, size_t k, void *workspace, size_t workspace_len,
