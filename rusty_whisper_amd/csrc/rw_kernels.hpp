@@ -214,7 +214,8 @@ __device__ inline float finite_max(float b, float v) {
 // The GEMM's offset and power-of-two scale of each weight row (GemmPlanes::
 // cm, cs): one wavefront per row of the padded matrix, lanes striding over
 // the blocks.  cm = the mean of the row's finite values d*q + m (f32, summed
-// per lane, then in a butterfly over the lanes); the row's largest finite
+// per lane, then in a butterfly over the lanes) where that mean exceeds the
+// values' standard deviation, else 0; the row's largest finite
 // |d*q + m - cm|, |d| or |m - cm| is in [2^(E-1), 2^E), and cs = 2^(E-15)
 // moves it to [2^14, 2^15).  Finite f16 scales bound E to [-23, 25], so cs is
 // a normal f32.  Zero rows (and padding rows) keep cs = 1, cm = 0.
@@ -249,7 +250,25 @@ __global__ __launch_bounds__(256) void k_row_scale(const uint8_t *__restrict__ r
   }
   sum = fold(sum);
   cnt = fold(cnt);
-  const float c = cnt > 0.0f ? sum / cnt : 0.0f;
+  const float mean = cnt > 0.0f ? sum / cnt : 0.0f;
+  float dev = 0.0f;  // sum of squared deviations from the mean
+  if (j < n) {
+    for (int bl = lane; bl < nb; bl += 64) {
+      uint16_t d, m;
+      uint32_t h;
+      uint8_t q[32];
+      read_block<DT>(raw + ((size_t)j * nb + bl) * BB, d, m, h, q);
+      const float df = h2f_exact(d), mf = has_min(DT) ? h2f_exact(m) : 0.0f;
+      for (int e = 0; e < QK; ++e) {
+        const float v = __fadd_rn(__fmul_rn(df, (float)raw_q<DT>(q, h, e)), mf);
+        if (fabsf(v) <= 3.4028235e38f) dev += (v - mean) * (v - mean);
+      }
+    }
+  }
+  dev = fold(dev);
+  // an offset only where it dominates the spread; elsewhere rounding
+  // relative to each value is as good
+  const float c = (cnt > 0.0f && mean * mean > dev / cnt) ? mean : 0.0f;
   float mx = 0.0f;
   if (j < n) {
     for (int bl = lane; bl < nb; bl += 64) {
@@ -1265,7 +1284,7 @@ __device__ inline void weight_f16(uint4 qb, uint32_t dmw, v8h &b0, v8h &b1) {
   b1 = __builtin_elementwise_fma(q1, dv, mv);
 }
 
-constexpr int GEMM_TM = 4, GEMM_TN = 2, GEMM_P = 2;
+constexpr int GEMM_TN = 2, GEMM_P = 2;
 
 // The weights of one k_gemm launch (all of one dtype and k, against one
 // quantized activation): column tiles [tile0, tile0 + cdiv(ngroups, TN)) of
@@ -1305,18 +1324,20 @@ struct GemmSet {
 // A launch covers up to GEMM_MAX_SET weights that share the activation (the
 // column tiles of the launch run through the weights in turn).  A
 // workgroup owns one tile of TM activation row groups x TN weight row
-// groups (128 x 64) and has KW wavefronts, each taking every KW-th block
+// groups (32 TM x 64; TM = 4, or 2 for inputs of at most 64 rows) and has
+// KW wavefronts, each taking every KW-th block
 // (block kw, kw + KW, ...).  A wavefront loads its operands straight into
 // registers, P blocks ahead, and needs no other wavefront until the end: no
 // LDS and no barrier in the k loop.  Each step issues the loads of block
 // s + P, then runs the 16 MFMAs of block s while the VALU dequantizes the
 // weights of block s + 1 (one MFMA, then three VALU instructions).  At the
-// end the KW partial tiles meet in LDS and are summed in kw order, each
-// wavefront finishing TM / KW row groups.  KW comes from the weights'
-// shapes alone, so a row's result never depends on m.
-template <int DT, int KW>
+// end the KW partial tiles meet in LDS and are summed in kw order, the
+// 32 x 32 output tiles dealt to the wavefronts in turn.  KW comes from the
+// weights' shapes alone and TM changes which rows share a workgroup, not
+// how a row is summed, so a row's result never depends on m.
+template <int DT, int KW, int TM, bool OFFS>
 __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int m) {
-  constexpr int TM = GEMM_TM, TN = GEMM_TN, P = GEMM_P, S = P + 1;
+  constexpr int TN = GEMM_TN, P = GEMM_P, S = P + 1;
   constexpr int RED = KW > 1 ? KW * TM * TN * 16 * 64 * 4 : 16;
   __shared__ __align__(16) uint8_t lds[RED];
   const int l = threadIdx.x & 63;
@@ -1436,28 +1457,37 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int
       bc = bn;
     }
 
-  // epilogue inputs for this wavefront's row groups and columns, in flight
-  // while the partials meet in LDS (rows and columns past the end read the
-  // last one)
-  constexpr int TPW = KW > 1 ? TM / KW : TM;  // row groups finished per wavefront
-  static_assert(KW == 1 || TM % KW == 0, "row groups split evenly over the k-waves");
-  float4 sc[TPW][4], pv[TPW][4];
-  float bv[TN], cv[TN], mv[TN];
+  // The workgroup's TM x TN output tiles (32 x 32 each, tile u = TN i + j)
+  // are dealt to the KW wavefronts in runs of UPW: a wavefront finishes RPW
+  // row groups x CPW column groups.  Their epilogue inputs load while the
+  // partials meet in LDS (rows and columns past the end read the last one).
+  constexpr int NU = TM * TN, UPW = (NU + KW - 1) / KW;
+  static_assert(UPW < TN || UPW % TN == 0, "a run covers whole row groups");
+  constexpr int RPW = UPW >= TN ? UPW / TN : 1, CPW = UPW >= TN ? TN : 1;
+  const int u0 = KW > 1 ? kw * UPW : 0;  // first tile of this wavefront
+  const int i0 = u0 / TN, j0 = UPW >= TN ? 0 : u0 % TN;
+  // OFFS: some weight of the launch has rows with an offset (GemmPlanes::cm;
+  // a weight without one has cm == NULL and reads 0)
+  const bool offs = OFFS && gp.cm != nullptr;  // uniform
+  const float *bp = bias ? bias : gp.cs;
+  const float *cmp = offs ? gp.cm : gp.cs;
+  float4 sc[RPW][4], pv[RPW][4];
+  float bv[CPW], cv[CPW], mv[CPW];
 #pragma unroll
-  for (int ii = 0; ii < TPW; ++ii) {
-    const int tg = min(by * TM + (KW > 1 ? kw * TPW + ii : ii), a.mgroups - 1);
+  for (int rr = 0; rr < RPW; ++rr) {
+    const int tg = min(by * TM + min(i0 + rr, TM - 1), a.mgroups - 1);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      sc[ii][q] = ldg_f4(a.rs + tg * RG + 8 * q + 4 * h);
-      pv[ii][q] = ldg_f4(a.ps + tg * RG + 8 * q + 4 * h);
+      sc[rr][q] = ldg_f4(a.rs + tg * RG + 8 * q + 4 * h);
+      if (OFFS) pv[rr][q] = ldg_f4(a.ps + tg * RG + 8 * q + 4 * h);
     }
   }
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int wr = min(bx * TN + j, ngroups - 1) * RG + r;  // weight row (padding rows: cs 1, cm 0)
-    bv[j] = bias ? ldg_f(bias + min((bx * TN + j) * RG + r, n - 1)) : 0.0f;
-    cv[j] = ldg_f(gp.cs + wr);
-    mv[j] = ldg_f(gp.cm + wr);
+  for (int cc = 0; cc < CPW; ++cc) {
+    const int cg = min(bx * TN + j0 + cc, ngroups - 1), wr = cg * RG + r;  // padding rows: cs 1, cm 0
+    bv[cc] = ldg_f(bp + (bias ? min((bx * TN + j0 + cc) * RG + r, n - 1) : wr));
+    cv[cc] = ldg_f(gp.cs + wr);
+    if (OFFS) mv[cc] = offs ? ldg_f(cmp + wr) : 0.0f;
   }
   float4 *red = reinterpret_cast<float4 *>(lds);
   if (KW > 1) {
@@ -1474,71 +1504,76 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int
   // every epilogue load has landed before the first store: stores count in
   // the same counter, and a wait placed behind them would wait for them
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  if (u0 >= NU) return;  // a wavefront with no tile of its own (after the barrier)
 #pragma unroll
-  for (int ii = 0; ii < TPW; ++ii) {
-    const int i = KW > 1 ? kw * TPW + ii : ii;
-    const int tg = by * TM + i;
-    if (tg >= a.mgroups) break;
+  for (int rr = 0; rr < RPW; ++rr)
+#pragma unroll
+  for (int cc = 0; cc < CPW; ++cc) {
+    const int i = i0 + rr, j = j0 + cc;  // compile-time with one wavefront
+    const int tg = by * TM + i, cg = bx * TN + j;
+    if (tg >= a.mgroups || cg >= ngroups) continue;
     const bool rows_full = (tg + 1) * RG <= m;
+    const int col = cg * RG + r;
+    float y[16];
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int cg = bx * TN + j;
-      if (cg >= ngroups) continue;
-      const int col = cg * RG + r;
-      float y[16];
+    for (int q = 0; q < 4; ++q) {
+      float4 v;
+      if constexpr (KW > 1) {
+        v = red[((i * TN + j) * 4 + q) * 64 + l];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float4 v;
-        if (KW > 1) {
-          v = red[((i * TN + j) * 4 + q) * 64 + l];
-#pragma unroll
-          for (int kk = 1; kk < KW; ++kk) {
-            const float4 p = red[(((kk * TM + i) * TN + j) * 4 + q) * 64 + l];
-            v.x += p.x;
-            v.y += p.y;
-            v.z += p.z;
-            v.w += p.w;
-          }
-        } else {
-          v = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+        for (int kk = 1; kk < KW; ++kk) {
+          const float4 p = red[(((kk * TM + i) * TN + j) * 4 + q) * 64 + l];
+          v.x += p.x;
+          v.y += p.y;
+          v.z += p.z;
+          v.w += p.w;
         }
-        // row scale, then column scale: both powers of two, so exact (the
-        // row scale first keeps the intermediate in range); then the weight
-        // row's offset times the activation row's sum, one rounding
-        const float4 c = sc[ii][q], pp = pv[ii][q];
-        y[4 * q] = __builtin_fmaf(mv[j], pp.x, (v.x * c.x) * cv[j]);
-        y[4 * q + 1] = __builtin_fmaf(mv[j], pp.y, (v.y * c.y) * cv[j]);
-        y[4 * q + 2] = __builtin_fmaf(mv[j], pp.z, (v.z * c.z) * cv[j]);
-        y[4 * q + 3] = __builtin_fmaf(mv[j], pp.w, (v.w * c.w) * cv[j]);
-        if (bias) {
+      } else {
+        v = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+      }
+      // row scale, then column scale: both powers of two, so exact (the
+      // row scale first keeps the intermediate in range); then the weight
+      // row's offset times the activation row's sum, one rounding
+      const float4 c = sc[rr][q];
+      y[4 * q] = (v.x * c.x) * cv[cc];
+      y[4 * q + 1] = (v.y * c.y) * cv[cc];
+      y[4 * q + 2] = (v.z * c.z) * cv[cc];
+      y[4 * q + 3] = (v.w * c.w) * cv[cc];
+      if (OFFS && offs) {
+        const float4 pp = pv[rr][q];
+        y[4 * q] = __builtin_fmaf(mv[cc], pp.x, y[4 * q]);
+        y[4 * q + 1] = __builtin_fmaf(mv[cc], pp.y, y[4 * q + 1]);
+        y[4 * q + 2] = __builtin_fmaf(mv[cc], pp.z, y[4 * q + 2]);
+        y[4 * q + 3] = __builtin_fmaf(mv[cc], pp.w, y[4 * q + 3]);
+      }
+      if (bias) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) y[4 * q + e] += bv[j];
+        for (int e = 0; e < 4; ++e) y[4 * q + e] += bv[cc];
+      }
+    }
+    if (flags & GEMM_GELU) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) y[v] = gelu_tanh(y[v]);
+    }
+    // lane (h, r) holds rows 8q + 4h + e (e < 4) of column col
+    float *o = out + (size_t)(tg * RG + 4 * h) * n + col;
+    if (rows_full && (cg + 1) * RG <= n) {
+      if (flags & GEMM_ACC) {
+        float x[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) x[v] = o[(size_t)(8 * (v >> 2) + (v & 3)) * n];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) y[v] = x[v] + y[v];
+      }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) stg_f(o + (size_t)(8 * (v >> 2) + (v & 3)) * n, y[v]);
+    } else if (col < n) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        if (tg * RG + 4 * h + 8 * (v >> 2) + (v & 3) < m) {
+          float *p = o + (size_t)(8 * (v >> 2) + (v & 3)) * n;
+          stg_f(p, (flags & GEMM_ACC) ? *p + y[v] : y[v]);
         }
-      }
-      if (flags & GEMM_GELU) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) y[v] = gelu_tanh(y[v]);
-      }
-      // lane (h, r) holds rows 8q + 4h + e (e < 4) of column col
-      float *o = out + (size_t)(tg * RG + 4 * h) * n + col;
-      if (rows_full && (cg + 1) * RG <= n) {
-        if (flags & GEMM_ACC) {
-          float x[16];
-#pragma unroll
-          for (int v = 0; v < 16; ++v) x[v] = o[(size_t)(8 * (v >> 2) + (v & 3)) * n];
-#pragma unroll
-          for (int v = 0; v < 16; ++v) y[v] = x[v] + y[v];
-        }
-#pragma unroll
-        for (int v = 0; v < 16; ++v) stg_f(o + (size_t)(8 * (v >> 2) + (v & 3)) * n, y[v]);
-      } else if (col < n) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v)
-          if (tg * RG + 4 * h + 8 * (v >> 2) + (v & 3) < m) {
-            float *p = o + (size_t)(8 * (v >> 2) + (v & 3)) * n;
-            stg_f(p, (flags & GEMM_ACC) ? *p + y[v] : y[v]);
-          }
-      }
     }
   }
 }

@@ -358,10 +358,27 @@ static int gemm_kw(size_t tiles, int nb) {
   return kw;
 }
 
+// Row groups per workgroup: 4, or 2 for inputs of at most 64 rows (so a
+// skinny input does not run MFMAs on repeated rows).  OFFS: some weight of
+// the launch has offset rows (the epilogue's extra term and loads).
+template <int DT, int KW, int TM, bool OFFS>
+static void launch_gemm_tm(const GemmSet &set, size_t tiles, const ActView &av, int m, hipStream_t s) {
+  dim3 grid((unsigned)tiles, (unsigned)cdiv(av.mgroups, TM));
+  hipLaunchKernelGGL((k_gemm<DT, KW, TM, OFFS>), grid, dim3(64 * KW), 0, s, set, av, m);
+}
+
 template <int DT, int KW>
 static void launch_gemm_kw(const GemmSet &set, size_t tiles, const ActView &av, int m, hipStream_t s) {
-  dim3 grid((unsigned)tiles, (unsigned)cdiv(av.mgroups, GEMM_TM));
-  hipLaunchKernelGGL((k_gemm<DT, KW>), grid, dim3(64 * KW), 0, s, set, av, m);
+  bool offs = false;
+  for (int i = 0; i < set.count; ++i) offs = offs || set.it[i].gp.cm != nullptr;
+  const bool skinny = av.mgroups <= 2;
+  if (offs) {
+    if (skinny) launch_gemm_tm<DT, KW, 2, true>(set, tiles, av, m, s);
+    else launch_gemm_tm<DT, KW, 4, true>(set, tiles, av, m, s);
+  } else {
+    if (skinny) launch_gemm_tm<DT, KW, 2, false>(set, tiles, av, m, s);
+    else launch_gemm_tm<DT, KW, 4, false>(set, tiles, av, m, s);
+  }
 }
 
 template <int DT>
@@ -1234,6 +1251,14 @@ int rw_rocm_weight_upload(int dtype, size_t n, size_t k, const uint8_t *raw, siz
 #undef RW_REPACK
     e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+    if (e == hipSuccess) {
+      // a weight with no offset row skips the offset term in the GEMM
+      std::vector<float> cm(rows);
+      e = hipMemcpy(cm.data(), b + off_cm, rows * 4, hipMemcpyDeviceToHost);
+      bool any = false;
+      for (float v : cm) any = any || v != 0.0f;
+      if (!any) w->gemm.cm = nullptr;
+    }
   }
   if (tmp) (void)hipFree(tmp);
   if (e != hipSuccess) {
