@@ -1,23 +1,29 @@
 #!/usr/bin/env python3
 """Throughput of the quantized linear-layer matmul on one MI355X.
 
-Workload (one "step"): the linears of the Whisper large-v3 encoder at one
-30 s window, M = 1500 rows, weights in Q5_1 -- 32 layers x {q, k, v, out
-[1280x1280], fc1 [5120x1280], fc2 [1280x5120]}, with biases where Whisper has
-them (no bias on k).  Each layer quantizes its three distinct inputs (the
-attention-block input shared by q/k/v, the attention output, the MLP input)
-and the fc1 output, then runs the six products in four GEMM launches (q, k
-and v read one input and share a launch, as rw_rocm_matmul_prequant_multi_dev
-allows).  Weights are seeded N(0, 0.02)
+Headline workload (one "step"): the linears of the Whisper large-v3 encoder
+at one 30 s window, M = 1500 rows, weights in Q5_1 -- 32 layers x {q, k, v,
+out [1280x1280], fc1 [5120x1280], fc2 [1280x5120]}, with biases where
+Whisper has them (no bias on k).  Each layer quantizes its three distinct
+inputs (the attention-block input shared by q/k/v, the attention output, the
+MLP input) and the fc1 output, then runs the six products in four GEMM
+launches (q, k and v read one input and share a launch, as
+rw_rocm_matmul_prequant_multi_dev allows).  Weights are seeded N(0, 0.02)
 quantized to Q5_1 (472 MB resident, more than the 256 MB MALL); activations
-are seeded N(0, 1) and resident in HBM before timing starts.
+are seeded N(0, 1) and resident in HBM before timing starts.  `value` is the
+step with the same activation buffers for every layer (warm); `cold` gives
+each layer its own inputs, outputs and workspaces (2.6 GB touched per step,
+ten times the MALL).
 
-Reported: whole-step TOPS (2*M*N*K per linear), the GEMM kernel's own rate
-against the MI355X f16 MFMA peak (HIP events around bursts of back-to-back
-launches), the
-decode-GEMV bandwidth for the large-v3 decoder linear set at M = 5 in Q5_0,
-and the reference CPU path (oracle/cpu_baseline.c, AVX-512 VNNI / AVX2
-restatement of matmul_t_q) timed on this host on one encoder layer.
+Reported beside it: the GEMM kernel's own rate against the MI355X f16 MFMA
+peak (HIP events around bursts of back-to-back launches) with its HBM
+traffic from the committed rocprofv3 counter summary, one leg per benchmark
+configuration (tiny.en fc1; small.en Q8_0 with outliers; large-v3 Q4_0 and
+Q4_1 with scale spread; the large-v3 decoder set at M = 5 and M = 1; the
+turbo batch at M = 12000 and M = 40), the device encoder layers, attention
+and decoder steps, and the reference CPU path (oracle/cpu_baseline.c,
+AVX-512 VNNI / AVX2 restatement of matmul_t_q) timed on this host on one
+encoder layer (cold path) and on decoder shapes (packed cache).
 """
 from __future__ import annotations
 
@@ -41,59 +47,81 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def encoder_workload(A, synth, torch, dtype: int, m: int, seed0: int):
-    cfg = synth.LARGE_V3
+def encoder_workload(A, synth, torch, dtype: int, m: int, seed0: int, cfg=None, spread: bool = False,
+                     outliers: float = 0.0, layers_w=None, cold: bool = False):
+    """Weights (seeded N(0, 0.02), each 32-block scaled by 10**U(-1, 1) with
+    `spread`), per-launch inputs (N(0, 1), `outliers` of the channels x20),
+    biases, outputs and quantization workspaces for cfg's encoder linears.
+    `layers_w` reuses uploaded weights of the same shapes and dtype; `cold`
+    gives every layer its own inputs, outputs and workspaces."""
+    cfg = cfg or synth.LARGE_V3
     d, fc, layers = cfg["d"], cfg["fc"], cfg["layers"]
     shapes = synth.encoder_layer_shapes(d, fc)
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(seed0)
-    layers_w = []
-    t0 = time.time()
-    workers = min(16, os.cpu_count() or 1)
-    for layer in range(layers):
-        specs = [(dtype, n, k, seed0 + 100 * layer + i) for i, (_, n, k) in enumerate(shapes)]
-        raws = synth.normal_weights_many(specs, workers)
-        layers_w.append({name: A.DeviceWeight(dtype, n, k, raw) for (name, n, k), raw in zip(shapes, raws)})
-    log(f"encoder weights uploaded ({layers} layers, {time.time() - t0:.1f} s)")
-    inputs = {
-        "qkv": torch.randn(m, d, device=dev, generator=g),
-        "attn": torch.randn(m, d, device=dev, generator=g),
-        "mlp": torch.randn(m, d, device=dev, generator=g),
-        "h": torch.randn(m, fc, device=dev, generator=g),
-    }
+    if layers_w is None:
+        layers_w = []
+        t0 = time.time()
+        workers = min(16, os.cpu_count() or 1)
+        for layer in range(layers):
+            specs = [(dtype, n, k, seed0 + 100 * layer + i, 0.02, spread) for i, (_, n, k) in enumerate(shapes)]
+            raws = synth.normal_weights_many(specs, workers)
+            layers_w.append({name: A.DeviceWeight(dtype, n, k, raw) for (name, n, k), raw in zip(shapes, raws)})
+        log(f"encoder weights uploaded ({layers} layers of {synth.NAMES[dtype]}, d={d}, {time.time() - t0:.1f} s)")
+    widths = {"qkv": d, "attn": d, "mlp": d, "h": fc}
+    ch = {}
+    if outliers > 0:
+        for key, k in widths.items():
+            idx = torch.randperm(k, generator=g, device=dev)[:max(1, int(round(outliers * k)))]
+            ch[key] = idx
+
+    def make_inputs():
+        t = {key: torch.randn(m, k, device=dev, generator=g) for key, k in widths.items()}
+        for key, idx in ch.items():
+            t[key][:, idx] *= 20.0
+        return t
+
+    wsz = {key: A.workspace_size(m, k) for key, k in widths.items()}
+
+    def make_set():
+        return dict(inputs=make_inputs(), wsp={key: torch.empty(wsz[key], dtype=torch.uint8, device=dev)
+                                               for key in widths},
+                    outs={name: torch.empty(m, n, device=dev) for name, n, _ in shapes})
+
     bias = {name: (None if name == "k" else torch.randn(n, device=dev, generator=g) * 0.1)
             for name, n, _ in shapes}
-    outs = {name: torch.empty(m, n, device=dev) for name, n, _ in shapes}
-    wsz = {key: A.workspace_size(m, t.shape[1]) for key, t in inputs.items()}
-    wsp = {key: torch.empty(wsz[key], dtype=torch.uint8, device=dev) for key in inputs}
+    sets = [make_set() for _ in range(layers if cold else 1)]
     ops = layers * sum(2 * m * n * k for _, n, k in shapes)
-    return dict(layers=layers_w, inputs=inputs, bias=bias, outs=outs, wsz=wsz, wsp=wsp, ops=ops, shapes=shapes,
-                m=m, d=d, fc=fc)
+    return dict(layers=layers_w, sets=sets, bias=bias, wsz=wsz, ops=ops, shapes=shapes, m=m, d=d, fc=fc,
+                inputs=sets[0]["inputs"], wsp=sets[0]["wsp"], outs=sets[0]["outs"])
+
 
 SRC = {"q": "qkv", "k": "qkv", "v": "qkv", "out": "attn", "fc1": "mlp", "fc2": "h"}
 # the launches of one layer: q, k and v read one input and share a launch
 LAUNCHES = [("qkv", ("q", "k", "v")), ("out", ("out",)), ("fc1", ("fc1",)), ("fc2", ("fc2",))]
 
 
-def product(A, W, lw, names, stream):
+def product(A, W, lw, names, stream, bufs=None):
+    bufs = bufs or W["sets"][0]
     m = W["m"]
-    src = W["wsp"][SRC[names[0]]]
+    src = bufs["wsp"][SRC[names[0]]]
     if len(names) == 1:
-        lw[names[0]].matmul_prequant_dev(src, m, W["outs"][names[0]], W["bias"][names[0]], stream)
+        lw[names[0]].matmul_prequant_dev(src, m, bufs["outs"][names[0]], W["bias"][names[0]], stream)
     else:
-        A.matmul_prequant_multi_dev([lw[x] for x in names], src, m, [W["outs"][x] for x in names],
+        A.matmul_prequant_multi_dev([lw[x] for x in names], src, m, [bufs["outs"][x] for x in names],
                                     [W["bias"][x] for x in names], stream)
 
 
 def encoder_step(A, W, stream):
-    m = W["m"]
-    for lw in W["layers"]:
+    m, sets = W["m"], W["sets"]
+    for i, lw in enumerate(W["layers"]):
+        bufs = sets[i % len(sets)]
         for key in ("qkv", "attn", "mlp", "h"):
-            t = W["inputs"][key]
-            A.quantize_dev(t, m, t.shape[1], W["wsp"][key], W["wsz"][key], stream)
+            t = bufs["inputs"][key]
+            A.quantize_dev(t, m, t.shape[1], bufs["wsp"][key], W["wsz"][key], stream)
         for _, names in LAUNCHES:
-            product(A, W, lw, names, stream)
+            product(A, W, lw, names, stream, bufs)
 
 
 def time_encoder(A, torch, W, steps: int, warmup: int, stream):
@@ -113,19 +141,19 @@ def time_encoder(A, torch, W, steps: int, warmup: int, stream):
     return ms, wall
 
 
-def time_encoder_graph(A, torch, W, steps: int, warmup: int):
-    """The same step captured once in a HIP graph (torch.cuda.CUDAGraph over
-    the library's launches) and replayed: launches without host overhead,
-    as an encoder runs window after window."""
+def time_graph(torch, fn, steps: int, warmup: int):
+    """fn(stream) captured once in a HIP graph (torch.cuda.CUDAGraph over the
+    library's launches) and replayed: launches without host overhead, as an
+    encoder runs window after window.  Returns ms per replay."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        encoder_step(A, W, side.cuda_stream)
+        fn(side.cuda_stream)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        encoder_step(A, W, torch.cuda.current_stream().cuda_stream)
+        fn(torch.cuda.current_stream().cuda_stream)
     for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
@@ -141,15 +169,19 @@ def time_encoder_graph(A, torch, W, steps: int, warmup: int):
     return ms
 
 
+def time_encoder_graph(A, torch, W, steps: int, warmup: int):
+    return time_graph(torch, lambda st: encoder_step(A, W, st), steps, warmup)
+
+
 def time_gemm_kernel(A, torch, W, stream, reps: int = 3):
-    """Average k_gemm launch duration: per launch of the layer (q/k/v
-    together, out, fc1, fc2), the launches of every layer back to back
-    between two HIP events on torch's current stream (the stream the kernels
-    run on), so each weight is read once per pass as in the step.  An event
-    pair around every single launch would add the event packets' own latency
-    to each launch; back-to-back launches on one stream leave no measurable
-    gap, so the burst average is the kernel's duration.  Returns (mean launch
-    ms, ops per launch, launches, per-launch mean us)."""
+    """Average k_gemm launch duration: per launch type of the layer (q/k/v
+    together, out, fc1, fc2), the launches of every layer back to back,
+    captured in one HIP graph and replayed `reps` times between two HIP
+    events, so each weight is read once per pass as in the step and no host
+    launch overhead sits between them (an 11 us launch is shorter than a
+    launch from Python).  Back-to-back launches on one stream leave no
+    measurable gap, so the burst average is the kernel's duration.  Returns
+    (mean launch ms, ops per launch, launches, per-launch mean us)."""
     m = W["m"]
     for key in ("qkv", "attn", "mlp", "h"):
         t = W["inputs"][key]
@@ -158,19 +190,11 @@ def time_gemm_kernel(A, torch, W, stream, reps: int = 3):
     dims = {name: (n, k) for name, n, k in W["shapes"]}
     total_ms, ops, launches, per_launch = 0.0, 0, 0, {}
     for label, names in LAUNCHES:
-        def burst():
+        def burst(st, names=names):
             for lw in W["layers"]:
-                product(A, W, lw, names, stream)
-        burst()  # warm
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            burst()
-        e1.record()
-        torch.cuda.synchronize()
+                product(A, W, lw, names, st)
+        ms = time_graph(torch, burst, reps, 1) * reps
         cnt = reps * len(W["layers"])
-        ms = e0.elapsed_time(e1)
         per_launch[label] = round(1e3 * ms / cnt, 2)
         total_ms += ms
         ops += cnt * sum(2 * m * dims[x][0] * dims[x][1] for x in names)
@@ -178,8 +202,11 @@ def time_gemm_kernel(A, torch, W, stream, reps: int = 3):
     return total_ms / launches, ops / launches, launches, per_launch
 
 
-def decode_workload(A, synth, torch, dtype: int, m: int, seed0: int):
-    cfg = synth.LARGE_V3
+def decode_workload(A, synth, torch, dtype: int, m: int, seed0: int, cfg=None):
+    """cfg's decoder linears (10 per layer) plus the [n_vocab x d] logits,
+    each with its own m-row input, output and bias (none on the k
+    projections and the logits)."""
+    cfg = cfg or synth.LARGE_V3
     d, fc, layers, vocab = cfg["d"], cfg["fc"], cfg["layers"], cfg["n_vocab"]
     shapes = synth.decoder_layer_shapes(d, fc) * layers + [("logits", vocab, d)]
     dev = torch.device("cuda:0")
@@ -198,11 +225,8 @@ def decode_workload(A, synth, torch, dtype: int, m: int, seed0: int):
             items.append(_decode_item(A, torch, dev, g, dtype, name, n, k, raw, m, keep))
             wbytes += n * (k // 32) * synth.BLOCK_BYTES[dtype]
             io_bytes += 4 * m * k + 4 * m * n
-    arr = A.make_linears(items)
-    wsz = A.grouped_workspace_size(arr)
-    ws = torch.empty(wsz, dtype=torch.uint8, device=dev)
     log(f"decoder weights uploaded ({len(shapes)} linears, {wbytes / 1e6:.1f} MB, {time.time() - t0:.1f} s)")
-    return dict(arr=arr, ws=ws, wsz=wsz, keep=keep, bytes=wbytes + io_bytes, wbytes=wbytes, count=len(shapes))
+    return decode_rows(A, torch, dict(items=items, keep=keep, wbytes=wbytes, count=len(shapes), m=m), m)
 
 
 def _decode_item(A, torch, dev, g, dtype, name, n, k, raw, m, keep):
@@ -212,6 +236,16 @@ def _decode_item(A, torch, dev, g, dtype, name, n, k, raw, m, keep):
     o = torch.empty(m, n, device=dev)
     keep += [w, a, b, o]
     return (w, a, b, o, m)
+
+
+def decode_rows(A, torch, D, m: int):
+    """The workload's linears on the first m of their rows (m <= D's own)."""
+    items = [(w, a[:m], b, o[:m], m) for (w, a, b, o, _) in D["items"]]
+    arr = A.make_linears(items)
+    wsz = A.grouped_workspace_size(arr)
+    io = sum(4 * m * (w.k + w.n) for (w, _, _, _, _) in D["items"])
+    return dict(D, arr=arr, ws=torch.empty(wsz, dtype=torch.uint8, device="cuda:0"), wsz=wsz, rows=m,
+                bytes=D["wbytes"] + io, row_items=items)
 
 
 def time_decode(A, torch, D, steps: int, warmup: int, stream):
@@ -351,35 +385,42 @@ def time_decoder_tokens(A, synth, torch, D, stream, steps: int):
         L["fc1_b"] = vec(4 * d)
         lay.append(L)
     emb = keep[4 * per * layers]
-    dec = A.Decoder(d // 64, 448, 1500, lay, emb, vec(448 * d), vec(d, 1.0), vec(d))
+    n_ctx = 448
+    dec = A.Decoder(d // 64, n_ctx, 1500, lay, emb, vec(n_ctx * d), vec(d, 1.0), vec(d))
     enc = torch.randn(1500, d, device="cuda:0", generator=g)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     dec.set_audio(enc, stream)
     torch.cuda.synchronize()
     t_audio = (time.perf_counter() - t0) * 1e3
-    hid = torch.empty(4, d, device="cuda:0")
+    hid = torch.empty(n_ctx, d, device="cuda:0")
     logits = torch.empty(1, vocab, device="cuda:0")
-    dec.forward_hidden([50258, 50259, 50359], hid[:3], stream)
     tok = 50363
 
     def one():
         dec.forward_hidden([tok], hid[:1], stream)
         emb.matmul_dev(hid[:1], 1, logits, stream=stream)
 
-    one()
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        one()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    # per token at three cache lengths: the steps end at n_past = `end`
+    per_len = {}
+    for end, timed in ((24, steps), (224, 4), (440, 4)):
+        dec.reset()
+        prompt = [50258, 50259, 50359] + [(440 + 37 * i) % 50000 for i in range(end - timed - 4)]
+        dec.forward_hidden(prompt, hid[:len(prompt)], stream)
+        one()  # warm
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(timed):
+            one()
+        e1.record()
+        torch.cuda.synchronize()
+        assert dec.n_past == end
+        per_len[end] = e0.elapsed_time(e1) / timed
     ok = bool(torch.isfinite(logits).all().item())
     dec.free()
-    return t_audio, ms, ok
+    return t_audio, per_len, ok
 
 
 def time_model_load(A, synth, dtype: int, path: str, reps: int = 2):
@@ -422,6 +463,34 @@ def time_model_load(A, synth, dtype: int, path: str, reps: int = 2):
     return min(times), size, len(shapes)
 
 
+def cpu_description():
+    """The host CPU: model name, and the logical and physical cores this
+    process may run on (its affinity mask)."""
+    allowed = os.sched_getaffinity(0) if hasattr(os, "sched_getaffinity") else set(range(os.cpu_count() or 1))
+    model, phys = "", set()
+    try:
+        for block in open("/proc/cpuinfo").read().split("\n\n"):
+            f = dict(line.split(":", 1) for line in block.splitlines() if ":" in line)
+            f = {k.strip(): v.strip() for k, v in f.items()}
+            if "processor" not in f or int(f["processor"]) not in allowed:
+                continue
+            model = model or f.get("model name", "")
+            phys.add((f.get("physical id", "0"), f.get("core id", f["processor"])))
+    except OSError:
+        pass
+    return {"cpu_model": model, "logical_cores": len(allowed), "physical_cores": len(phys) or None}
+
+
+def cpu_threads():
+    import oracle as O
+
+    threads = O.cpu_threads()
+    cap = os.environ.get("OMP_NUM_THREADS")
+    if cap and cap.isdigit():
+        threads = min(threads, int(cap))
+    return threads
+
+
 def cpu_baseline(synth, dtype: int, m: int, budget_s: float):
     """The reference CPU path (oracle/cpu_baseline.c) on one large-v3 encoder
     layer: each of the six linears on its first call (cold path, as the
@@ -432,10 +501,7 @@ def cpu_baseline(synth, dtype: int, m: int, budget_s: float):
 
     cfg = synth.LARGE_V3
     shapes = synth.encoder_layer_shapes(cfg["d"], cfg["fc"])
-    threads = O.cpu_threads()
-    cap = os.environ.get("OMP_NUM_THREADS")
-    if cap and cap.isdigit():
-        threads = min(threads, int(cap))
+    threads = cpu_threads()
     rng = np.random.default_rng(7)
     raws = [synth.normal_weights(dtype, n, k, seed=900 + i) for i, (_, n, k) in enumerate(shapes)]
     acts = {k: rng.standard_normal((m, k)).astype(np.float32) for k in {k for _, _, k in shapes}}
@@ -454,15 +520,172 @@ def cpu_baseline(synth, dtype: int, m: int, budget_s: float):
     layer_s = sum(statistics.median(v) for v in per_linear)
     ops = sum(2 * m * n * k for _, n, k in shapes)
     tier_name = {0: "avx512-vnni", 1: "avx2", 2: "f32"}[tier]
-    return {
+    return dict({
         "value": round(ops / layer_s / 1e12, 4),
         "unit": "TOPS",
         "cores": threads,
         "kind": "port",
-        "sample": f"one large-v3 encoder layer (6 Q5_1 linears, M={m}), cold path, median of {reps} runs "
-                  f"per linear, tier {tier_name}, {threads} threads",
+        "sample": f"one large-v3 encoder layer (6 {synth.NAMES[dtype]} linears, M={m}), cold path, median of {reps} "
+                  f"runs per linear, tier {tier_name}, {threads} threads",
         "layer_ms": round(layer_s * 1e3, 2),
+    }, **cpu_description())
+
+
+def cpu_baseline_decode(synth, dtype: int, m: int, budget_s: float):
+    """The reference CPU path on the decoder shapes at steady state: one
+    large-v3 decoder layer's ten linears and the logits projection, each
+    timed from its third call on (the packed int8 cache, src/quant.rs:589-639),
+    median of repeated runs; the set's time is 32 layers plus the logits."""
+    import numpy as np
+
+    import oracle as O
+
+    cfg = synth.LARGE_V3
+    d, fc, vocab = cfg["d"], cfg["fc"], cfg["n_vocab"]
+    shapes = synth.decoder_layer_shapes(d, fc) + [("logits", vocab, d)]
+    threads = cpu_threads()
+    rng = np.random.default_rng(8)
+    times = []
+    t_start = time.time()
+    for i, (_, n, k) in enumerate(shapes):
+        t = O.CpuQTensor(dtype, n, k, synth.normal_weights(dtype, n, k, seed=950 + i))
+        a = rng.standard_normal((m, k)).astype(np.float32)
+        t.matmul(a, threads=threads)
+        t.matmul(a, threads=threads)  # the second call builds the packed cache
+        runs = []
+        while len(runs) < 5 or (len(runs) < 50 and time.time() - t_start < budget_s * (i + 1) / len(shapes)):
+            t0 = time.perf_counter()
+            t.matmul(a, threads=threads)
+            runs.append(time.perf_counter() - t0)
+        times.append(statistics.median(runs))
+        t.close()
+    set_s = cfg["layers"] * sum(times[:-1]) + times[-1]
+    wbytes = sum(n * (k // 32) * synth.BLOCK_BYTES[dtype] for _, n, k in shapes[:-1]) * cfg["layers"] + \
+        vocab * (d // 32) * synth.BLOCK_BYTES[dtype]
+    io = cfg["layers"] * sum(4 * m * (n + k) for _, n, k in shapes[:-1]) + 4 * m * (vocab + d)
+    return {
+        "value": round((wbytes + io) / set_s / 1e9, 2),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"one large-v3 decoder layer's 10 {synth.NAMES[dtype]} linears and the [51866x1280] logits at "
+                  f"M={m}, packed cache (third call on), median of >= 5 runs each; set = 32 layers + logits",
+        "set_ms": round(set_s * 1e3, 3),
+        "layer_ms": round(sum(times[:-1]) * 1e3, 3),
+        "logits_ms": round(times[-1] * 1e3, 3),
     }
+
+
+def leg_encoder(A, synth, torch, dtype: int, m: int, steps: int, warmup: int, seed0: int, cfg=None,
+                spread: bool = False, outliers: float = 0.0, layers_w=None, name: str = ""):
+    """One encoder-linears step of a configuration (graph replay)."""
+    W = encoder_workload(A, synth, torch, dtype, m, seed0, cfg=cfg, spread=spread, outliers=outliers,
+                         layers_w=layers_w)
+    ms = time_encoder_graph(A, torch, W, steps, warmup)
+    tops = W["ops"] / (ms * 1e-3) / 1e12
+    cfg = cfg or synth.LARGE_V3
+    log(f"{name}: {ms:.3f} ms per step ({tops:.1f} TOPS)")
+    res = {"workload": f"{cfg['layers']} encoder layers' linears (d={cfg['d']}, fc {cfg['fc']}), "
+                       f"{synth.NAMES[dtype]}, M={m}" + (", block scales spread 10**U(-1,1)" if spread else "")
+                       + (f", {outliers:.0%} of input channels x20" if outliers else ""),
+           "value": round(tops, 3), "unit": "TOPS", "ms_per_step": round(ms, 4), "peak": F16_PEAK_TFLOPS,
+           "frac": round(tops / F16_PEAK_TFLOPS, 4), "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+    return res, W
+
+
+def leg_single(A, synth, torch, dtype: int, n: int, k: int, m: int, steps: int, seed: int):
+    """One matmul_t_q call (quantize + product) on resident inputs, 20 calls
+    per graph replay."""
+    dev = "cuda:0"
+    w = A.DeviceWeight(dtype, n, k, synth.normal_weights(dtype, n, k, seed=seed))
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    a = torch.randn(m, k, device=dev, generator=g)
+    b = torch.randn(n, device=dev, generator=g) * 0.1
+    o = torch.empty(m, n, device=dev)
+    wsz = A.workspace_size(m, k)
+    ws = torch.empty(wsz, dtype=torch.uint8, device=dev)
+    reps = 20
+    ms = time_graph(torch, lambda st: [w.matmul_dev(a, m, o, b, ws, wsz, st) for _ in range(reps)], steps, 2) / reps
+    tops = 2 * m * n * k / (ms * 1e-3) / 1e12
+    w.free()
+    return {"workload": f"one {synth.NAMES[dtype]} matmul_t_q [{m}x{k}] x [{n}x{k}]^T + bias, quantization "
+                        f"included", "value": round(tops, 3), "unit": "TOPS", "us_per_call": round(ms * 1e3, 2),
+            "peak": F16_PEAK_TFLOPS, "frac": round(tops / F16_PEAK_TFLOPS, 4)}
+
+
+def leg_turbo_decoder(A, synth, torch, layers_w, steps: int, seed0: int):
+    """large-v3-turbo's 4-layer decoder over 8 stacked windows, Q5_1: the
+    cross K/V projections of the 8 x 1500 encoder rows (once per window
+    batch), then per step the 8 per-token linears of every layer and the
+    logits at M = 8 x 5 beam rows (quantization + product per linear)."""
+    dev = "cuda:0"
+    dtype, d, fc, vocab, nl = synth.BY_NAME["Q5_1"], 1280, 5120, 51866, 4
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed0)
+    # cross K/V: the encoder's q/k weights stand in (same shapes and dtype)
+    M = 8 * 1500
+    enc = torch.randn(M, d, device=dev, generator=g)
+    kv = [[torch.empty(M, d, device=dev) for _ in range(2)] for _ in range(nl)]
+    kv_b = torch.randn(d, device=dev, generator=g) * 0.1
+    wsz = A.workspace_size(M, d)
+    ws = torch.empty(wsz, dtype=torch.uint8, device=dev)
+
+    def cross(st):
+        A.quantize_dev(enc, M, d, ws, wsz, st)
+        for l in range(nl):
+            A.matmul_prequant_multi_dev([layers_w[l]["q"], layers_w[l]["k"]], ws, M, kv[l], [None, kv_b], st)
+
+    ms_cross = time_graph(torch, cross, max(2, steps // 2), 1)
+    ops_cross = nl * 2 * 2 * M * d * d
+    # per-token linears at m = 40
+    m = 40
+    per = [("q", d, d), ("k", d, d), ("v", d, d), ("out", d, d), ("cq", d, d), ("cout", d, d), ("fc1", fc, d),
+           ("fc2", d, fc)]
+    raws = synth.normal_weights_many([(dtype, n, k, seed0 + i) for i, (_, n, k) in enumerate(per * nl)]
+                                     + [(dtype, vocab, d, seed0 + 99)], min(16, os.cpu_count() or 1))
+    ws_ = [A.DeviceWeight(dtype, n, k, r) for (_, n, k), r in zip(per * nl + [("logits", vocab, d)], raws)]
+    ins = [torch.randn(m, w.k, device=dev, generator=g) for w in ws_]
+    outs = [torch.empty(m, w.n, device=dev) for w in ws_]
+    bs = [None if i % 8 == 1 or i == len(ws_) - 1 else torch.randn(w.n, device=dev, generator=g) * 0.1
+          for i, w in enumerate(ws_)]
+    wk = {k: (A.workspace_size(m, k), torch.empty(A.workspace_size(m, k), dtype=torch.uint8, device=dev))
+          for k in (d, fc)}
+
+    def step(st):
+        for w, a, o, b in zip(ws_, ins, outs, bs):
+            w.matmul_dev(a, m, o, b, wk[w.k][1], wk[w.k][0], st)
+
+    ms_step = time_graph(torch, step, steps, 2)
+    ops_step = sum(2 * m * w.n * w.k for w in ws_)
+    wbytes = sum(w.n * (w.k // 32) * synth.BLOCK_BYTES[dtype] for w in ws_)
+    for w in ws_:
+        w.free()
+    return {
+        "cross_kv": {"workload": "cross-attention K and V of 4 decoder layers over 8 stacked windows (M=12000, "
+                                 "1280x1280 Q5_1): one quantization, one two-weight GEMM launch per layer",
+                     "value": round(ops_cross / (ms_cross * 1e-3) / 1e12, 3), "unit": "TOPS",
+                     "ms": round(ms_cross, 4)},
+        "step_m40": {"workload": "per decoder step at M=40 (8 windows x 5 beams): 4 layers x (self q,k,v,out, "
+                                 "cross q,out, fc1, fc2) + logits [51866x1280], Q5_1, each a quantization and a "
+                                 "64-row-tile GEMM launch",
+                     "value": round(ops_step / (ms_step * 1e-3) / 1e12, 3), "unit": "TOPS",
+                     "ms": round(ms_step, 4),
+                     "weight_GB_per_s": round(wbytes / (ms_step * 1e-3) / 1e9, 1)},
+    }
+
+
+def profile_traffic(root: str):
+    """HBM bytes per k_gemm launch of the headline workload, from the
+    committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (the json block of
+    profiles/k_gemm_q5_1_large_v3_encoder_m1500.md); None when absent."""
+    path = os.path.join(root, "profiles", "k_gemm_q5_1_large_v3_encoder_m1500.md")
+    try:
+        text = open(path).read()
+        blob = text.split("```json", 1)[1].split("```", 1)[0]
+        return json.loads(blob), os.path.relpath(path, root)
+    except (OSError, IndexError, ValueError):
+        return None, None
 
 
 def main() -> int:
@@ -478,6 +701,12 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
     ap.add_argument("--no-layers", action="store_true")
+    ap.add_argument("--no-legs", action="store_true", help="skip the other configurations' legs")
+    ap.add_argument("--no-cold", action="store_true")
+    ap.add_argument("--no-kernel-timing", action="store_true",
+                    help="skip the per-launch k_gemm bursts (graph replays), e.g. under a counter profiler")
+    ap.add_argument("--eager", action="store_true",
+                    help="report the eager step (no graph capture), e.g. under a counter profiler")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--load-model", default="",
                     help="also time the model loader on a large-v3-shaped ggml file written to this path")
@@ -512,14 +741,22 @@ def main() -> int:
     eager_ms, wall = time_encoder(A, torch, W, args.steps, args.warmup, stream)
     eager_tops = W["ops"] / (eager_ms * 1e-3) / 1e12
     log(f"encoder step, eager launches {eager_ms:.3f} ms  ({eager_tops:.1f} TOPS, wall {wall:.2f} s)")
-    ms = time_encoder_graph(A, torch, W, args.steps, args.warmup)
+    ms = eager_ms if args.eager else time_encoder_graph(A, torch, W, args.steps, args.warmup)
     tops = W["ops"] / (ms * 1e-3) / 1e12
-    log(f"encoder step, graph replay {ms:.3f} ms  ({tops:.1f} TOPS)")
+    log(f"encoder step, {'eager' if args.eager else 'graph replay'} {ms:.3f} ms  ({tops:.1f} TOPS)")
 
-    gemm_ms, gemm_ops, launches, per_shape = time_gemm_kernel(A, torch, W, stream)
+    if args.no_kernel_timing:
+        gemm_ms, gemm_ops, launches, per_shape = ms / (4 * len(W["layers"])), W["ops"] / (4 * len(W["layers"])), 0, {}
+    else:
+        gemm_ms, gemm_ops, launches, per_shape = time_gemm_kernel(A, torch, W, stream)
     gemm_tops = gemm_ops / (gemm_ms * 1e-3) / 1e12
     log(f"k_gemm average launch {gemm_ms * 1e3:.1f} us over {launches} launches -> {gemm_tops:.1f} TOPS "
         f"(per launch, us: {per_shape})")
+    prof, prof_path = profile_traffic(ROOT)
+    traffic = None
+    if prof and args.quant == "Q5_1" and args.m == 1500:
+        # the same launch mix as `achieved`: one of each launch type per layer
+        traffic = int(sum(prof["fetch_bytes"][k] + prof["write_bytes"][k] for k, _ in LAUNCHES) / len(LAUNCHES))
 
     result = {
         "metric": METRIC,
@@ -554,13 +791,27 @@ def main() -> int:
             "peak": F16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(gemm_tops / F16_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": prof_path if traffic is not None else None,
             "kernel": f"k_gemm<{args.quant}> on v_mfma_f32_32x32x16_f16 (2*M*N*K per launch)",
+            "limiter": "operand delivery from L2 into the CUs: MFMA busy about a quarter of the kernel's time, "
+                       "L2->CU operand traffic 10-25x the unique bytes (rocprofv3 counters in "
+                       "profiles/k_gemm_q5_1_large_v3_encoder_m1500.md)",
             "avg_launch_us": round(gemm_ms * 1e3, 2),
             "launch_us_by_launch": per_shape,
             "frac_of_int8_peak": round(gemm_tops / INT8_PEAK_TOPS, 4),
         },
     }
+    if not args.no_cold:
+        Wc = encoder_workload(A, synth, torch, dtype, args.m, seed0=1, layers_w=W["layers"], cold=True)
+        cms = time_encoder_graph(A, torch, Wc, max(3, args.steps // 2), 1)
+        ctops = W["ops"] / (cms * 1e-3) / 1e12
+        log(f"encoder step, cold (every layer its own buffers): {cms:.3f} ms ({ctops:.1f} TOPS)")
+        result["cold"] = {"workload": "the headline step with every layer's inputs, outputs and workspaces its "
+                                      "own (2.6 GB of buffers, more than ten MALLs), graph replay",
+                          "value": round(ctops, 3), "unit": "TOPS", "ms_per_step": round(cms, 4)}
+        del Wc
+        torch.cuda.empty_cache()
     if not args.no_layers:
         eager_l, lms, finite = time_encoder_layers(A, torch, W, stream, max(3, args.steps // 2), 1)
         log(f"32 encoder layers on the device: graph replay {lms:.3f} ms ({lms * 1e3 / 32:.1f} us per layer), "
@@ -575,6 +826,31 @@ def main() -> int:
             "finite_and_replay_equal": finite,
         }
 
+    legs = {}
+    if not args.no_legs:
+        steps = max(3, args.steps // 2)
+        legs["c1_tiny_fc1_q5_1"] = leg_single(A, synth, torch, synth.BY_NAME["Q5_1"], 1536, 384, 1500, steps, 43)
+        log(f"tiny.en fc1: {legs['c1_tiny_fc1_q5_1']['us_per_call']} us per call "
+            f"({legs['c1_tiny_fc1_q5_1']['value']} TOPS)")
+        legs["c2_small_encoder_q8_0"], _ = leg_encoder(A, synth, torch, synth.BY_NAME["Q8_0"], 1500, steps, 1, 2,
+                                                       cfg=synth.SMALL, outliers=0.01, name="small.en Q8_0")
+        for q in ("Q4_0", "Q4_1"):
+            legs[f"c4_large_v3_encoder_{q.lower()}"], Wq = leg_encoder(A, synth, torch, synth.BY_NAME[q], 1500,
+                                                                      steps, 1, 4, spread=True,
+                                                                      name=f"large-v3 {q} spread")
+            del Wq
+            torch.cuda.empty_cache()
+        legs["c5_turbo_encoder_m12000_q5_1"], Wt = leg_encoder(A, synth, torch, dtype, 12000, 2, 1, 5,
+                                                               layers_w=W["layers"], name="turbo M=12000")
+        del Wt
+        torch.cuda.empty_cache()
+        t = leg_turbo_decoder(A, synth, torch, W["layers"], steps, 6)
+        legs["c5_turbo_cross_kv_m12000_q5_1"] = t["cross_kv"]
+        legs["c5_turbo_decoder_m40_q5_1"] = t["step_m40"]
+        log(f"turbo cross K/V {t['cross_kv']['ms']} ms ({t['cross_kv']['value']} TOPS); M=40 step "
+            f"{t['step_m40']['ms']} ms ({t['step_m40']['value']} TOPS)")
+        torch.cuda.empty_cache()
+
     del W
     torch.cuda.empty_cache()
 
@@ -582,7 +858,8 @@ def main() -> int:
         D = decode_workload(A, synth, torch, synth.BY_NAME[args.decode_quant], args.decode_m, seed0=5000)
         dms, dms_call = time_decode(A, torch, D, max(3, args.steps), 2, stream)
         gbs = D["bytes"] / (dms * 1e-3) / 1e9
-        log(f"decode set {dms:.3f} ms ({gbs:.1f} GB/s); with per-call table upload {dms_call:.3f} ms")
+        log(f"decode set M={args.decode_m}: {dms:.3f} ms ({gbs:.1f} GB/s); with per-call table upload "
+            f"{dms_call:.3f} ms")
         result["decode"] = {
             "metric": f"decode GEMV HBM GB/s @M={args.decode_m}",
             "workload": f"large-v3 decoder linears, {args.decode_quant}, M={args.decode_m}: 32 layers x 10 "
@@ -592,24 +869,40 @@ def main() -> int:
             "ms_per_step": round(dms, 4),
             "ms_per_step_with_table_upload": round(dms_call, 4),
             "bytes_per_step": D["bytes"],
-            "launch": "prepared group (rw_rocm_group_run): one k_gemv_records launch (each linear's activation quantized once) and one k_gemv launch for the set",
+            "launch": "prepared group (rw_rocm_group_run): one k_gemv_records launch (each linear's activation "
+                      "quantized once) and one k_gemv launch for the set",
             "peak": HBM_PEAK_GBS,
             "frac": round(gbs / HBM_PEAK_GBS, 4),
         }
+        if args.decode_m > 1:
+            D1 = decode_rows(A, torch, D, 1)
+            d1, _ = time_decode(A, torch, D1, max(3, args.steps), 2, stream)
+            g1 = D1["bytes"] / (d1 * 1e-3) / 1e9
+            log(f"decode set M=1: {d1:.3f} ms ({g1:.1f} GB/s)")
+            legs["c3_decode_m1_" + args.decode_quant.lower()] = {
+                "workload": f"the decode set at M=1 (greedy), {args.decode_quant}", "value": round(g1, 2),
+                "unit": "GB/s", "ms_per_step": round(d1, 4), "bytes_per_step": D1["bytes"],
+                "peak": HBM_PEAK_GBS, "frac": round(g1 / HBM_PEAK_GBS, 4)}
+            del D1
         if not args.no_layers:
-            t_audio, tok_ms, finite = time_decoder_tokens(A, synth, torch, D, stream, 20)
-            log(f"decoder on the device: set_audio {t_audio:.2f} ms, {tok_ms:.3f} ms per token with logits "
-                f"(finite={finite})")
+            t_audio, per_len, finite = time_decoder_tokens(A, synth, torch, D, stream, 20)
+            log(f"decoder on the device: set_audio {t_audio:.2f} ms, ms per token with logits by cache length "
+                f"{ {k: round(v, 3) for k, v in per_len.items()} } (finite={finite})")
             result["decoder_tokens"] = {
                 "workload": "large-v3 decoder, one beam, Q5_0: per token the embedding, 32 layers (causal "
                             "self-attention over the cache, cross-attention to 1500 positions, MLP), final "
                             "layernorm and the [51866 x 1280] logits product, all on the device (rw_decoder)",
-                "ms_per_token": round(tok_ms, 4),
+                "ms_per_token": round(per_len[24], 4),
+                "ms_per_token_by_cache_length": {str(k): round(v, 4) for k, v in per_len.items()},
+                "note": "ms_per_token: steps 5..24 of the cache (3-token prompt, one warm step, 20 timed); the "
+                        "other lengths time 4 steps ending at that many cached rows",
                 "set_audio_ms": round(t_audio, 3),
                 "finite": finite,
             }
         del D
         torch.cuda.empty_cache()
+    if legs:
+        result["legs"] = legs
 
     if not args.no_attention:
         ams, aflops = time_attention(A, torch, stream, max(5, args.steps), 2)
@@ -638,7 +931,10 @@ def main() -> int:
 
     if not args.no_cpu:
         cb = cpu_baseline(synth, dtype, args.m, args.cpu_seconds)
-        log(f"cpu baseline {cb['value']} TOPS ({cb['sample']})")
+        log(f"cpu baseline {cb['value']} TOPS ({cb['sample']}; {cb['cpu_model']})")
+        cd = cpu_baseline_decode(synth, synth.BY_NAME[args.decode_quant], args.decode_m, args.cpu_seconds)
+        log(f"cpu baseline, decoder shapes {cd['value']} GB/s ({cd['sample']})")
+        cb["decode"] = cd
         result["cpu_baseline"] = cb
 
     print(json.dumps(result), flush=True)
