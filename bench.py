@@ -419,8 +419,44 @@ def time_decoder_tokens(A, synth, torch, D, stream, steps: int):
         assert dec.n_past == end
         per_len[end] = e0.elapsed_time(e1) / timed
     ok = bool(torch.isfinite(logits).all().item())
+    # beam search: 5 forks at one cache length step together
+    # (rw_rocm_decoder_forward_beams_dev), then the stacked logits [5 x 51866]
+    # and their log_softmax + top-5 on the device
+    nb, k = 5, 5
+    dec.reset()
+    dec.forward_hidden([50258, 50259, 50359], hid[:3], stream)
+    beams = [dec] + [dec.fork(stream) for _ in range(nb - 1)]
+    hb = torch.empty(nb, d, device="cuda:0")
+    lb = torch.empty(nb, vocab, device="cuda:0")
+    ids = torch.empty(nb, k, dtype=torch.int32, device="cuda:0")
+    lps = torch.empty(nb, k, device="cuda:0")
+    toks = [440, 3111, 50257, 13, 1029]
+
+    def beam_step():
+        A.decoder_forward_beams(beams, toks, hb, stream)
+        emb.matmul_dev(hb, nb, lb, stream=stream)
+        A.logits_topk_dev(lb, nb, vocab, k, ids, lps, stream)
+
+    beam_step()  # warm
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        beam_step()
+    e1.record()
+    torch.cuda.synchronize()
+    beam_ms = e0.elapsed_time(e1) / steps
+    ok = ok and bool(torch.isfinite(lps).all().item())
+    t0 = time.perf_counter()
+    extra = [beams[1].fork(stream) for _ in range(4)]
+    torch.cuda.synchronize()
+    fork_ms = (time.perf_counter() - t0) * 1e3 / 4
+    for b in extra + beams[1:]:
+        b.free()
     dec.free()
-    return t_audio, per_len, ok
+    return t_audio, per_len, ok, {"beams": nb, "ms_per_step": beam_ms, "cache_rows": f"5..{4 + steps}",
+                                  "fork_ms": fork_ms}
 
 
 def time_model_load(A, synth, dtype: int, path: str, reps: int = 2):
@@ -885,7 +921,7 @@ def main() -> int:
                 "peak": HBM_PEAK_GBS, "frac": round(g1 / HBM_PEAK_GBS, 4)}
             del D1
         if not args.no_layers:
-            t_audio, per_len, finite = time_decoder_tokens(A, synth, torch, D, stream, 20)
+            t_audio, per_len, finite, beam = time_decoder_tokens(A, synth, torch, D, stream, 20)
             log(f"decoder on the device: set_audio {t_audio:.2f} ms, ms per token with logits by cache length "
                 f"{ {k: round(v, 3) for k, v in per_len.items()} } (finite={finite})")
             result["decoder_tokens"] = {
@@ -898,7 +934,21 @@ def main() -> int:
                         "other lengths time 4 steps ending at that many cached rows",
                 "set_audio_ms": round(t_audio, 3),
                 "finite": finite,
+                "beams": {
+                    "workload": f"beam search step, {beam['beams']} beams forked from one decoder: "
+                                "rw_rocm_decoder_forward_beams_dev (every linear over the 5 rows, the beams' "
+                                "self-attentions in one launch), the stacked [5 x 51866] logits product, and "
+                                "log_softmax + top-5 per beam on the device (rw_rocm_logits_topk_dev)",
+                    "ms_per_step": round(beam["ms_per_step"], 4),
+                    "ms_per_token_per_beam": round(beam["ms_per_step"] / beam["beams"], 4),
+                    "cache_rows": beam["cache_rows"],
+                    "fork_ms": round(beam["fork_ms"], 3),
+                    "note": "fork_ms: one rw_rocm_decoder_fork at 24 cached rows (the beam search forks the "
+                            "surviving candidates every step), host wall time",
+                },
             }
+            log(f"beam step ({beam['beams']} beams): {beam['ms_per_step']:.3f} ms, "
+                f"{beam['ms_per_step'] / beam['beams']:.3f} ms per token per beam; fork {beam['fork_ms']:.3f} ms")
         del D
         torch.cuda.empty_cache()
     if legs:

@@ -337,6 +337,39 @@ int rw_rocm_decoder_fork(const rw_decoder *d, void *stream, rw_decoder **out);
 int rw_rocm_decoder_forward_hidden_dev(rw_decoder *d, const uint32_t *tokens, size_t n_tok, float *hidden,
                                        void *stream);
 
+/* One step of a beam search for up to RW_MAX_BEAMS beams at once: beam i
+ * forwards its one new token tokens[i] (host array) and hidden row i (device
+ * [n_beams, n_state]) receives its final hidden state, as n_beams separate
+ * rw_rocm_decoder_forward_hidden_dev calls of one token would (within f32
+ * rounding: the products see n_beams rows, and the attention's kv split is
+ * chosen for all beams together).  Replaces the per-beam forward_hidden calls
+ * of the beam search (src/transcribe.rs:931-949); the beams' logits are then
+ * one rw_rocm_matmul_t_q_dev of the token embedding on the n_beams hidden
+ * rows, as the reference's stacked project_logits (src/transcribe.rs:965-978).
+ * The beams are distinct decoders forked from one decoder (they share its
+ * cross K/V) with equal n_past; every linear runs once over the n_beams rows,
+ * and the beams' self-attentions run as one launch, each over its own cache.
+ * Each beam's n_past grows by one.  The step uses beam 0's scratch, so steps
+ * that involve one decoder must not overlap. */
+#define RW_MAX_BEAMS 8
+int rw_rocm_decoder_forward_beams_dev(rw_decoder *const *beams, size_t n_beams, const uint32_t *tokens,
+                                      float *hidden, void *stream);
+
+/* log_softmax (src/transcribe.rs:482-486) and top_k (src/transcribe.rs:672-
+ * 685) of every row of logits [rows, n_vocab] (device): ids[rows * k] and
+ * logprobs[rows * k] (device) get each row's k largest log-probs, with the
+ * reference's rules: exactly -inf is skipped, equal log-probs keep the
+ * earlier ids and are listed later id first; NaN is never picked.  A row
+ * with fewer than k candidates ends with id 0xFFFFFFFF and -inf.  1 <= k <=
+ * 16, n_vocab <= 131072, rows <= 65535.  The log-sum-exp is summed in tree
+ * order, so a log-prob can differ from the reference's in its last bit.
+ * `workspace` (>= rw_rocm_logits_topk_workspace_size bytes; NULL = a buffer
+ * of the library's own for this stream) holds per-chunk partial results.  On
+ * the current device, asynchronous on `stream`. */
+int rw_rocm_logits_topk_dev(const float *logits, size_t rows, size_t n_vocab, size_t k, uint32_t *ids,
+                            float *logprobs, void *workspace, size_t workspace_len, void *stream);
+size_t rw_rocm_logits_topk_workspace_size(size_t rows, size_t n_vocab, size_t k);
+
 /* ---- Model files straight to resident weights ----
  *
  * rw_rocm_model_load reads a whisper model in either container the reference

@@ -64,3 +64,33 @@ class Decoder:
             x = (x + linear(gelu(linear(cur, L["fc1"], L["fc1_b"])), L["fc2"], L["fc2_b"])).astype(np.float32)
         self.n_past += len(tokens)
         return layernorm(x, self.p["ln_w"], self.p["ln_b"])
+
+
+def log_softmax(row: np.ndarray) -> np.ndarray:
+    """src/transcribe.rs:482-486 in float32: the maximum (a fold from -inf),
+    lse = max + ln(sum of exp(v - max)) summed in index order, lp = v - lse."""
+    row = np.asarray(row, dtype=np.float32)
+    mx = np.float32(-np.inf)
+    for v in row[~np.isnan(row)]:
+        mx = max(mx, v)
+    terms = np.exp((row - mx).astype(np.float32)).astype(np.float32)
+    s = np.cumsum(terms, dtype=np.float32)[-1] if len(terms) else np.float32(0.0)
+    lse = np.float32(mx + np.float32(np.log(s)))
+    return (row - lse).astype(np.float32)
+
+
+def top_k(lps: np.ndarray, k: int):
+    """src/transcribe.rs:672-685: scan the log-probs in id order, skip
+    exactly -inf, insert (lp, id) at partition_point(b > lp) of the list kept
+    sorted by lp while it has fewer than k entries or lp beats its last."""
+    best = []
+    for i, lp in enumerate(np.asarray(lps, dtype=np.float32).tolist()):
+        if lp == float("-inf"):
+            continue
+        if len(best) < k or lp > best[-1][0]:
+            pos = 0
+            while pos < len(best) and best[pos][0] > lp:
+                pos += 1
+            best.insert(pos, (lp, i))
+            del best[k:]
+    return best

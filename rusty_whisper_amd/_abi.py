@@ -94,6 +94,11 @@ _SIGNATURES = {
     "rw_rocm_decoder_fork": (C.c_int, [C.c_void_p, C.c_void_p, C.POINTER(C.c_void_p)]),
     "rw_rocm_decoder_forward_hidden_dev": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p,
                                                      C.c_void_p]),
+    "rw_rocm_decoder_forward_beams_dev": (C.c_int, [C.POINTER(C.c_void_p), C.c_size_t, C.c_void_p, C.c_void_p,
+                                                    C.c_void_p]),
+    "rw_rocm_logits_topk_dev": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_void_p, C.c_void_p,
+                                          C.c_void_p, C.c_size_t, C.c_void_p]),
+    "rw_rocm_logits_topk_workspace_size": (C.c_size_t, [C.c_size_t, C.c_size_t, C.c_size_t]),
     "rw_rocm_model_load": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(C.c_void_p)]),
     "rw_rocm_model_free": (None, [C.c_void_p]),
     "rw_rocm_model_hparams": (C.c_int, [C.c_void_p, C.POINTER(C.c_int32)]),
@@ -452,6 +457,26 @@ class Decoder:
         if getattr(self, "handle", None):
             lib().rw_rocm_decoder_free(self.handle)
             self.handle = None
+
+
+def decoder_forward_beams(beams, tokens, hidden, stream: int | None = None) -> None:
+    """One beam-search step: beam i (a Decoder forked from one decoder)
+    forwards tokens[i]; hidden: device [len(beams), n_state]."""
+    t = np.ascontiguousarray(tokens, dtype=np.uint32)
+    arr = (C.c_void_p * max(len(beams), 1))(*[b.handle for b in beams])
+    check(lib().rw_rocm_decoder_forward_beams_dev(arr, len(beams), t.ctypes.data, _ptr(hidden), stream))
+
+
+def logits_topk_dev(logits, rows: int, n_vocab: int, k: int, ids, logprobs, stream: int | None = None,
+                    workspace=None, workspace_len: int = 0) -> None:
+    """log_softmax + top_k of each row of device logits into device ids
+    (uint32 [rows, k]) and logprobs (f32 [rows, k])."""
+    check(lib().rw_rocm_logits_topk_dev(_ptr(logits), rows, n_vocab, k, _ptr(ids), _ptr(logprobs),
+                                        _ptr(workspace), workspace_len, stream))
+
+
+def logits_topk_workspace_size(rows: int, n_vocab: int, k: int) -> int:
+    return lib().rw_rocm_logits_topk_workspace_size(rows, n_vocab, k)
 
     def __del__(self):
         try:

@@ -135,6 +135,87 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ q,
   }
 }
 
+// Several decoding states' one-token steps in one self-attention: plane
+// "head" b * n_head + h is head h of beam b, so one k_attn launch over
+// n_beams * n_head heads serves every beam (each attends to its own cache).
+constexpr int ATT_MAX_BEAMS = 8;
+struct BeamCaches {
+  float *k[ATT_MAX_BEAMS];  // beam b's f32 key cache [n_ctx][n]
+  float *v[ATT_MAX_BEAMS];  // and value cache
+};
+
+// The beams' planes in one launch: workgroups [0, wq) split q (the beams'
+// new rows, q [nb][n], scaled by 1/8; one query row per beam), [wq, wq + wk)
+// the keys, the rest v^T.  Key / value row r < n_past comes from beam b's
+// cache, row n_past from the step's new rows (kn, vn [nb][n]), which are also
+// stored into the caches at row n_past (each value by one thread).
+__global__ __launch_bounds__(256) void k_attn_split_beams(const float *__restrict__ q, const float *__restrict__ kn,
+                                                          const float *__restrict__ vn, BeamCaches C, int nb,
+                                                          int n_head, int n_past, AttnPlanes P, int wq, int wk) {
+  const int bx = blockIdx.x;
+  const int n = n_head * ATT_DH, t_kv = n_past + 1, heads = nb * n_head;
+  if (bx < wq) {
+    // plane head' = b * n_head + h of row 0 is q + b * n + h * 64, which is
+    // where att_split_rows reads head' of a one-row input
+    const size_t idx = (size_t)bx * 256 + threadIdx.x;
+    if (idx < (size_t)heads * P.tq_pad * 8)
+      att_split_rows(idx, q, n, 1, P.tq_pad, 0.125f, const_cast<uint16_t *>(P.qh), const_cast<uint16_t *>(P.ql));
+  } else if (bx < wq + wk) {
+    const size_t idx = (size_t)(bx - wq) * 256 + threadIdx.x;
+    if (idx >= (size_t)heads * P.tkv_pad * 8) return;
+    const int c = (int)(idx & 7);
+    const size_t hr = idx >> 3;  // head' * tkv_pad + row
+    const int row = (int)(hr % P.tkv_pad), hd = (int)(hr / P.tkv_pad);
+    const int b = hd / n_head, h = hd % n_head;
+    float v[8];
+    if (row < t_kv) {
+      const float *src = row < n_past ? C.k[b] + (size_t)row * n : kn + (size_t)b * n;
+      const float4 *s4 = reinterpret_cast<const float4 *>(src + h * ATT_DH + c * 8);
+      const float4 a = s4[0], e = s4[1];
+      v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = e.x, v[5] = e.y, v[6] = e.z, v[7] = e.w;
+      if (row == n_past) {
+        float4 *d4 = reinterpret_cast<float4 *>(C.k[b] + (size_t)n_past * n + h * ATT_DH + c * 8);
+        d4[0] = a;
+        d4[1] = e;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+    }
+    uint16_t h8[8], l8[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) att_split(v[j], h8[j], l8[j]);
+    const size_t o = hr * ATT_DH + c * 8;
+    *reinterpret_cast<uint4 *>(const_cast<uint16_t *>(P.kh) + o) = *reinterpret_cast<const uint4 *>(h8);
+    *reinterpret_cast<uint4 *>(const_cast<uint16_t *>(P.kl) + o) = *reinterpret_cast<const uint4 *>(l8);
+  } else {
+    const size_t idx = (size_t)(bx - wq - wk) * 256 + threadIdx.x;
+    const int nc = P.tkv_pad / 8;
+    const int d = (int)(idx % ATT_DH);
+    const size_t hc = idx / ATT_DH;
+    const int cc = (int)(hc % nc), hd = (int)(hc / nc);
+    if (hd >= heads) return;
+    const int b = hd / n_head, h = hd % n_head;
+    uint16_t h8[8], l8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int p = cc * 8 + e;
+      const int kv = (p & ~15) | attn_vpos(p & 15);
+      float x = 0.0f;
+      if (kv < n_past) {
+        x = C.v[b][(size_t)kv * n + h * ATT_DH + d];
+      } else if (kv == n_past) {
+        x = vn[(size_t)b * n + h * ATT_DH + d];
+        C.v[b][(size_t)n_past * n + h * ATT_DH + d] = x;
+      }
+      att_split(x, h8[e], l8[e]);
+    }
+    const size_t o = ((size_t)hd * ATT_DH + d) * P.tkv_pad + cc * 8;
+    *reinterpret_cast<uint4 *>(const_cast<uint16_t *>(P.vh) + o) = *reinterpret_cast<const uint4 *>(h8);
+    *reinterpret_cast<uint4 *>(const_cast<uint16_t *>(P.vl) + o) = *reinterpret_cast<const uint4 *>(l8);
+  }
+}
+
 // out rows [0, t) x columns [0, cols) = 0 (attention over no keys)
 __global__ __launch_bounds__(256) void k_attn_zero(float *__restrict__ out, int ld, int t, int cols) {
   const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;

@@ -12,12 +12,15 @@ namespace rw {
 
 #if defined(__HIPCC__)
 
-// x[i] = token_embedding.row_f32(tok[i]) + positional[n_past + i]
+// x[i] = token_embedding.row_f32(tok[i]) + positional[n_past + i * pos_step]
 // (src/decoder.rs:122-135): the quantized row dequantized as d * q + m (two
-// roundings), then the position added.  One thread per (token, block).
+// roundings), then the position added.  pos_step is 1 for a prompt's
+// consecutive tokens and 0 for one token of each of several beams.  One
+// thread per (token, block).
 template <int DT>
 __global__ __launch_bounds__(256) void k_embed(WeightView w, const int *__restrict__ tok, int n_tok,
-                                               const float *__restrict__ pos, int n_past, float *__restrict__ x) {
+                                               const float *__restrict__ pos, int n_past, int pos_step,
+                                               float *__restrict__ x) {
   const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= (size_t)n_tok * w.nb) return;
   const int bl = (int)(t % w.nb), i = (int)(t / w.nb);
@@ -28,7 +31,7 @@ __global__ __launch_bounds__(256) void k_embed(WeightView w, const int *__restri
   const float m = has_min(DT) ? h2f_exact(w.m[si]) : 0.0f;
   const size_t n = (size_t)w.nb * QK;
   float *o = x + (size_t)i * n + (size_t)bl * QK;
-  const float *p = pos + (size_t)(n_past + i) * n + (size_t)bl * QK;
+  const float *p = pos + (size_t)(n_past + i * pos_step) * n + (size_t)bl * QK;
   for (int e = 0; e < QK; ++e) o[e] = __fadd_rn(__fadd_rn(__fmul_rn(d, (float)weight_q<DT>(w, g, bl, r, e)), m), p[e]);
 }
 
@@ -75,6 +78,182 @@ __global__ __launch_bounds__(256) void k_gelu(float *__restrict__ h, size_t n) {
     const float v = h[t];
     const float inner = 0.7978846f * (v + 0.044715f * v * v * v);
     h[t] = 0.5f * v * (1.0f + tanhf(inner));
+  }
+}
+
+constexpr int TOPK_MAX = 16;  // candidates per row of the top-k kernels
+
+// Block-wide reductions of one value per thread (256 threads, 4 wavefronts)
+__device__ inline float block_fmax(float v, float *scratch) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
+  __syncthreads();  // scratch may hold the previous reduction's values
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(scratch[0], scratch[1]), fmaxf(scratch[2], scratch[3]));
+}
+__device__ inline float block_fsum(float v, float *scratch) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (scratch[0] + scratch[1]) + (scratch[2] + scratch[3]);
+}
+// (v, i) beats (bv, bi): larger v, or equal v and smaller i
+__device__ inline bool topk_before(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
+
+// log_softmax of each row (src/transcribe.rs:482-486: the maximum, lse =
+// max + ln(sum exp(v - max)), lp = v - lse) and its top_k
+// (src/transcribe.rs:672-685).  top_k keeps the k largest log-probs, skips
+// exactly -inf, and among equal log-probs keeps the earlier ids; it lists
+// them by log-prob, equal ones later id first (its insertion order).  The
+// selection order is therefore (lp desc, id asc), and NaN is never picked.
+// Three launches over chunks of TOPK_CHUNK logits (rows x chunks
+// workgroups): k_topk_stats (each chunk's maximum and sum of exp(v - max)),
+// k_topk_chunk (the row's lse from those partials, in one fixed order, then
+// the chunk's k first entries in the selection order, from registers) and
+// k_topk_merge (per row, the k first of all chunks' picks, reordered for
+// the output).  Every chunk's picks hold that chunk's members of the row's
+// answer, so the merge is exact.  The sum runs in tree order, so lse (and
+// every lp) can differ from the reference's sequential sum in its last bit.
+constexpr int TOPK_CHUNK = 2048;  // logits per workgroup (8 per thread)
+constexpr int TOPK_MAX_CHUNKS = 64;
+
+__global__ __launch_bounds__(256) void k_topk_stats(const float *__restrict__ logits, int n, float *__restrict__ pm,
+                                                    float *__restrict__ ps) {
+  __shared__ float sf[4];
+  const int c = blockIdx.x, row = blockIdx.y, nc = gridDim.x, t = threadIdx.x;
+  const float *x = logits + (size_t)row * n;
+  const int e0 = c * TOPK_CHUNK, e1 = min(n, e0 + TOPK_CHUNK);
+  float v[TOPK_CHUNK / 256];
+  float mx = -__builtin_huge_valf();
+#pragma unroll
+  for (int j = 0; j < TOPK_CHUNK / 256; ++j) {
+    const int e = e0 + j * 256 + t;
+    v[j] = e < e1 ? x[e] : -__builtin_huge_valf();
+    mx = fmaxf(mx, v[j]);
+  }
+  mx = block_fmax(mx, sf);
+  float sum = 0.0f;  // an all -inf chunk (suppressed tokens) adds nothing
+#pragma unroll
+  for (int j = 0; j < TOPK_CHUNK / 256; ++j)
+    if (e0 + j * 256 + t < e1 && v[j] > -__builtin_huge_valf()) sum += expf(v[j] - mx);
+  sum = block_fsum(sum, sf);
+  if (t == 0) {
+    pm[(size_t)row * nc + c] = mx;
+    ps[(size_t)row * nc + c] = sum;
+  }
+}
+
+// the row's lse from its chunks' (maximum, sum) pairs: the maximum of the
+// maxima, then sum_c s_c exp(m_c - M) in chunk order
+__device__ inline float topk_lse(const float *pm, const float *ps, int nc) {
+  float M = -__builtin_huge_valf();
+  for (int c = 0; c < nc; ++c) M = fmaxf(M, pm[c]);
+  float S = 0.0f;
+  for (int c = 0; c < nc; ++c)
+    if (pm[c] > -__builtin_huge_valf()) S += ps[c] * expf(pm[c] - M);
+  return M + logf(S);
+}
+
+// the block-wide first (v, i) in the selection order (lp desc, id asc)
+__device__ inline void block_topk_argmax(float &bv, int &bi, float *rv, int *ri) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int oi = __shfl_xor(bi, o);
+    if (topk_before(ov, oi, bv, bi)) bv = ov, bi = oi;
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) rv[threadIdx.x >> 6] = bv, ri[threadIdx.x >> 6] = bi;
+  __syncthreads();
+  bv = rv[0], bi = ri[0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w)
+    if (topk_before(rv[w], ri[w], bv, bi)) bv = rv[w], bi = ri[w];
+}
+
+// k rounds over the values a thread holds (`cnt` of them): each round picks
+// the block's first entry after the previous pick; picks go to (ov, oi)[0, k),
+// padded with (-inf, INT32_MAX).  Returns the number picked.
+template <int PER>
+__device__ inline int topk_rounds(const float (&lp)[PER], const int (&id)[PER], int k, float *ov, int *oi,
+                                  float *rv, int *ri) {
+  constexpr float NEG_INF = -__builtin_huge_valf();
+  float pv = __builtin_huge_valf();
+  int pi = -1, got = 0;
+  for (int r = 0; r < k; ++r) {
+    float bv = NEG_INF;
+    int bi = INT32_MAX;
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (lp[j] > NEG_INF && topk_before(pv, pi, lp[j], id[j]) && topk_before(lp[j], id[j], bv, bi))
+        bv = lp[j], bi = id[j];
+    block_topk_argmax(bv, bi, rv, ri);
+    if (bi == INT32_MAX) break;  // no candidate left (uniform)
+    if (threadIdx.x == 0) ov[r] = bv, oi[r] = bi;
+    pv = bv, pi = bi;
+    got = r + 1;
+  }
+  if (threadIdx.x == 0)
+    for (int r = got; r < k; ++r) ov[r] = NEG_INF, oi[r] = INT32_MAX;
+  return got;
+}
+
+__global__ __launch_bounds__(256) void k_topk_chunk(const float *__restrict__ logits, int n, int k,
+                                                    const float *__restrict__ pm, const float *__restrict__ ps,
+                                                    float *__restrict__ cv, int *__restrict__ ci) {
+  __shared__ float rv[4];
+  __shared__ int ri[4];
+  const int c = blockIdx.x, row = blockIdx.y, nc = gridDim.x, t = threadIdx.x;
+  const float lse = topk_lse(pm + (size_t)row * nc, ps + (size_t)row * nc, nc);
+  const float *x = logits + (size_t)row * n;
+  const int e0 = c * TOPK_CHUNK, e1 = min(n, e0 + TOPK_CHUNK);
+  constexpr int PER = TOPK_CHUNK / 256;
+  float lp[PER];
+  int id[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int e = e0 + j * 256 + t;
+    id[j] = e;
+    lp[j] = e < e1 ? x[e] - lse : -__builtin_huge_valf();  // NaN stays NaN and is never picked
+  }
+  const size_t o = ((size_t)row * nc + c) * k;
+  topk_rounds<PER>(lp, id, k, cv + o, ci + o, rv, ri);
+}
+
+__global__ __launch_bounds__(256) void k_topk_merge(int nc, int k, const float *__restrict__ cv,
+                                                    const int *__restrict__ ci, uint32_t *__restrict__ ids,
+                                                    float *__restrict__ lps) {
+  __shared__ float rv[4];
+  __shared__ int ri[4];
+  __shared__ float pick_v[TOPK_MAX];
+  __shared__ int pick_i[TOPK_MAX];
+  const int row = blockIdx.x, t = threadIdx.x;
+  constexpr int PER = TOPK_MAX_CHUNKS * TOPK_MAX / 256;
+  float lp[PER];
+  int id[PER];
+  const int total = nc * k;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int e = j * 256 + t;
+    lp[j] = e < total ? cv[(size_t)row * total + e] : -__builtin_huge_valf();
+    id[j] = e < total ? ci[(size_t)row * total + e] : INT32_MAX;
+  }
+  const int got = topk_rounds<PER>(lp, id, k, pick_v, pick_i, rv, ri);
+  __syncthreads();
+  if (t == 0) {
+    // equal log-probs: later id first
+    for (int a = 1; a < got; ++a)
+      for (int b = a; b > 0 && pick_v[b] == pick_v[b - 1] && pick_i[b] > pick_i[b - 1]; --b) {
+        const int ti = pick_i[b];
+        pick_i[b] = pick_i[b - 1], pick_i[b - 1] = ti;
+      }
+    for (int r = 0; r < k; ++r) {
+      ids[(size_t)row * k + r] = r < got ? (uint32_t)pick_i[r] : 0xFFFFFFFFu;
+      lps[(size_t)row * k + r] = r < got ? pick_v[r] : -__builtin_huge_valf();
+    }
   }
 }
 

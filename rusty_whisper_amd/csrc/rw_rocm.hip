@@ -963,15 +963,17 @@ static int check_decoder_params(const rw_decoder_params *P) {
   return RW_OK;
 }
 
-// the per-call scratch of forward_hidden for n_tok tokens
+// the per-call scratch of forward_hidden for n_tok tokens (beams: n_tok beams
+// of one token each, whose self-attention runs as n_tok * n_head heads and
+// whose new key / value rows pass through kn, vn)
 struct DecScratch {
-  size_t off_tok, off_x, off_cur, off_q, off_a, off_h, off_act, off_att, bytes;
+  size_t off_tok, off_x, off_cur, off_q, off_a, off_h, off_kn, off_vn, off_act, off_att, bytes;
   AttnLayout self_att, cross_att;
 };
-static DecScratch dec_scratch(const rw_decoder *d, size_t n_tok) {
+static DecScratch dec_scratch(const rw_decoder *d, size_t n_tok, bool beams = false) {
   DecScratch S{};
   const size_t row = n_tok * d->n * 4;
-  S.self_att = attn_layout(n_tok, d->p.n_ctx, d->n);
+  S.self_att = beams ? attn_layout(1, d->p.n_ctx, n_tok * d->n) : attn_layout(n_tok, d->p.n_ctx, d->n);
   S.cross_att = attn_layout(n_tok, d->n_audio, d->n, false);  // K/V: the window's kept planes
   S.off_tok = 0;
   S.off_x = align_up(n_tok * 4, 256);
@@ -979,10 +981,46 @@ static DecScratch dec_scratch(const rw_decoder *d, size_t n_tok) {
   S.off_q = align_up(S.off_cur + row, 256);
   S.off_a = align_up(S.off_q + row, 256);
   S.off_h = align_up(S.off_a + row, 256);
-  S.off_act = align_up(S.off_h + n_tok * d->f * 4, 256);
+  S.off_kn = align_up(S.off_h + n_tok * d->f * 4, 256);
+  S.off_vn = align_up(S.off_kn + (beams ? row : 0), 256);
+  S.off_act = align_up(S.off_vn + (beams ? row : 0), 256);
   S.off_att = align_up(S.off_act + act_layout(n_tok, std::max(d->n, d->f)).bytes, 256);
   S.bytes = align_up(S.off_att + std::max(S.self_att.bytes, S.cross_att.bytes), 256);
   return S;
+}
+
+// One self-attention over several beams' caches (one new row each): the
+// planes of beam b, head h are head b * n_head + h of one k_attn launch.
+static int run_beam_self_attention(rw_decoder *const *beams, size_t nb, int l, const float *q, const float *kn,
+                                   const float *vn, float *att, const AttnLayout &L, void *ws, hipStream_t s) {
+  const rw_decoder *d = beams[0];
+  const int n_head = d->p.n_head, heads = (int)nb * n_head;
+  const size_t n_past = d->n_past, t_kv = n_past + 1;
+  char *b = (char *)ws;
+  AttnPlanes P{(uint16_t *)(b + L.off_qh), (uint16_t *)(b + L.off_ql), (uint16_t *)(b + L.off_kh),
+               (uint16_t *)(b + L.off_kl), (uint16_t *)(b + L.off_vh), (uint16_t *)(b + L.off_vl), L.tq_pad,
+               (int)std::min<size_t>(align_up(t_kv, ATT_KVB), L.tkv_pad)};
+  BeamCaches C{};
+  for (size_t i = 0; i < nb; ++i) {
+    C.k[i] = beams[i]->self_k(l);
+    C.v[i] = beams[i]->self_v(l);
+  }
+  const size_t nq = (size_t)heads * L.tq_pad * 8, nk = (size_t)heads * P.tkv_pad * 8;
+  const int wq = (int)cdiv(nq, 256), wk = (int)cdiv(nk, 256);
+  hipLaunchKernelGGL(k_attn_split_beams, dim3((unsigned)(wq + 2 * wk)), dim3(256), 0, s, q, kn, vn, C, (int)nb,
+                     n_head, (int)n_past, P, wq, wk);
+  LAUNCH_TRY("k_attn_split_beams");
+  const int nsplit = std::min(L.nsplit, attn_nsplit((size_t)(L.tq_pad / ATT_QB) * heads, cdiv(t_kv, ATT_KVB)));
+  float *part = nsplit > 1 ? (float *)(b + L.off_part) : nullptr;
+  hipLaunchKernelGGL(k_attn, dim3((unsigned)(L.tq_pad / ATT_QB), (unsigned)heads, (unsigned)nsplit), dim3(128), 0, s,
+                     P, 1, (int)t_kv, 1, att, (int)d->n, part, nullptr, 0);
+  LAUNCH_TRY("k_attn");
+  if (part) {
+    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)cdiv((size_t)heads * ATT_DH, 256)), dim3(256), 0, s, part, nsplit,
+                       heads, L.tq_pad, 1, att, (int)d->n);
+    LAUNCH_TRY("k_attn_combine");
+  }
+  return RW_OK;
 }
 
 // y = layernorm(x (+= r first when r is given))
@@ -993,17 +1031,23 @@ static int launch_layernorm(float *x, size_t rows, size_t n, const float *w, con
   return RW_OK;
 }
 
-static int decoder_forward(rw_decoder *d, size_t n_tok, float *hidden, char *b, const DecScratch &S, hipStream_t s) {
+// One forward pass: n_tok tokens of one decoder (nb = 1, beams = false), or
+// one token for each of nb beams (forks sharing the cross K/V at one n_past,
+// n_tok = nb, beams = true).
+static int decoder_forward(rw_decoder *const *dec, size_t nb, bool beams, size_t n_tok, float *hidden, char *b,
+                           const DecScratch &S, hipStream_t s) {
+  rw_decoder *d = dec[0];
   const size_t n = d->n;
   const int *tok = (const int *)(b + S.off_tok);
   float *x = (float *)(b + S.off_x), *cur = (float *)(b + S.off_cur), *q = (float *)(b + S.off_q);
   float *att = (float *)(b + S.off_a), *h = (float *)(b + S.off_h);
+  float *kn = (float *)(b + S.off_kn), *vn = (float *)(b + S.off_vn);
   void *act = b + S.off_act, *aws = b + S.off_att;
   const rw_weight *E = d->p.token_embedding;
   const size_t items = n_tok * (size_t)E->nb;
 #define RW_EMB(DT)                                                                                           \
   hipLaunchKernelGGL(k_embed<DT>, dim3((unsigned)cdiv(items, 256)), dim3(256), 0, s, E->view, tok, (int)n_tok, \
-                     d->p.positional, (int)d->n_past, x)
+                     d->p.positional, (int)d->n_past, beams ? 0 : 1, x)
   switch (E->dtype) {
     case RW_Q4_0: RW_EMB(RW_Q4_0); break;
     case RW_Q4_1: RW_EMB(RW_Q4_1); break;
@@ -1021,10 +1065,11 @@ static int decoder_forward(rw_decoder *d, size_t n_tok, float *hidden, char *b, 
     const rw_decoder_layer &L = d->layers[l];
     // causal self-attention over the cache and the new rows
     {
-      // q, k and v in one launch; k and v land in the cache rows
+      // q, k and v in one launch; k and v land in the cache rows (beams: in
+      // kn, vn, which the beams' split stores into each beam's cache)
       const rw_weight *w3[3] = {L.q, L.k, L.v};
       const float *b3[3] = {L.q_b, nullptr, L.v_b};
-      float *o3[3] = {q, d->self_k(l) + d->n_past * n, d->self_v(l) + d->n_past * n};
+      float *o3[3] = {q, beams ? kn : d->self_k(l) + d->n_past * n, beams ? vn : d->self_v(l) + d->n_past * n};
       if (L.q->dtype == L.k->dtype && L.q->dtype == L.v->dtype) {
         RW_TRY(run_matmul_set(w3, 3, x, n_tok, b3, o3, act, s, L.attn_ln_w, L.attn_ln_b, 0, cur));
       } else {
@@ -1032,8 +1077,11 @@ static int decoder_forward(rw_decoder *d, size_t n_tok, float *hidden, char *b, 
         for (int i = 0; i < 3; ++i) RW_TRY(run_matmul(w3[i], cur, n_tok, b3[i], o3[i], act, s));
       }
     }
-    RW_TRY(run_attention(q, n, d->self_k(l), n, d->self_v(l), n, n_tok, t_kv, d->p.n_head, 1, att, n, S.self_att,
-                         aws, s));
+    if (beams)
+      RW_TRY(run_beam_self_attention(dec, nb, l, q, kn, vn, att, S.self_att, aws, s));
+    else
+      RW_TRY(run_attention(q, n, d->self_k(l), n, d->self_v(l), n, n_tok, t_kv, d->p.n_head, 1, att, n, S.self_att,
+                           aws, s));
     RW_TRY(run_linear(L.out, att, n_tok, L.out_b, x, act, s, nullptr, nullptr, GEMM_ACC, nullptr));
     // cross-attention to the window's K/V
     RW_TRY(run_linear(L.cq, x, n_tok, L.cq_b, q, act, s, L.cross_ln_w, L.cross_ln_b, 0, cur));
@@ -1829,9 +1877,99 @@ int rw_rocm_decoder_forward_hidden_dev(rw_decoder *d, const uint32_t *tokens, si
   char *b = (char *)d->scratch;
   hipStream_t s = (hipStream_t)stream;
   HIP_TRY(hipMemcpyAsync(b + S.off_tok, tokens, n_tok * 4, hipMemcpyHostToDevice, s));
-  rc = decoder_forward(d, n_tok, hidden, b, S, s);
+  rc = decoder_forward(&d, 1, false, n_tok, hidden, b, S, s);
   if (rc) return rc;
   d->n_past += n_tok;
+  return RW_OK;
+}
+
+int rw_rocm_decoder_forward_beams_dev(rw_decoder *const *beams, size_t n_beams, const uint32_t *tokens,
+                                      float *hidden, void *stream) {
+  if (!beams || !tokens || !hidden) return fail(RW_EINVAL, "beams, tokens or hidden is NULL");
+  if (n_beams < 1 || n_beams > (size_t)ATT_MAX_BEAMS)
+    return fail(RW_EINVAL, "n_beams = %zu: between 1 and %d beams per step", n_beams, ATT_MAX_BEAMS);
+  rw_decoder *d = beams[0];
+  for (size_t i = 0; i < n_beams; ++i) {
+    const rw_decoder *e = beams[i];
+    if (!e) return fail(RW_EINVAL, "beam %zu is NULL", i);
+    if (!e->audio) return fail(RW_EINVAL, "beam %zu: no audio window: call rw_rocm_decoder_set_audio_dev first", i);
+    if (e->cross != d->cross || e->p.token_embedding != d->p.token_embedding)
+      return fail(RW_EINVAL, "beam %zu is not a fork of beam 0's decoder (another model or audio window)", i);
+    if (e->n_past != d->n_past)
+      return fail(RW_EINVAL, "beam %zu has %zu cached tokens, beam 0 has %zu", i, e->n_past, d->n_past);
+    for (size_t j = 0; j < i; ++j)
+      if (beams[j] == e) return fail(RW_EINVAL, "beam %zu is listed twice", i);
+  }
+  if (d->n_past + 1 > (size_t)d->p.n_ctx)
+    return fail(RW_EINVAL, "decoder context overflow: %zu + 1 > %d", d->n_past, d->p.n_ctx);
+  const size_t n_vocab = d->p.token_embedding->n;
+  for (size_t i = 0; i < n_beams; ++i)
+    if (tokens[i] >= n_vocab) return fail(RW_EINVAL, "token id %u out of range", tokens[i]);
+  HIP_TRY(hipSetDevice(d->device));
+  const DecScratch S = dec_scratch(d, n_beams, true);
+  int rc = dec_reserve(d, S.bytes);
+  if (rc) return rc;
+  char *b = (char *)d->scratch;
+  hipStream_t s = (hipStream_t)stream;
+  HIP_TRY(hipMemcpyAsync(b + S.off_tok, tokens, n_beams * 4, hipMemcpyHostToDevice, s));
+  rc = decoder_forward(beams, n_beams, true, n_beams, hidden, b, S, s);
+  if (rc) return rc;
+  for (size_t i = 0; i < n_beams; ++i) beams[i]->n_past += 1;
+  return RW_OK;
+}
+
+struct TopkLayout {
+  int nc;
+  size_t off_pm, off_ps, off_cv, off_ci, bytes;
+};
+static TopkLayout topk_layout(size_t rows, size_t n_vocab, size_t k) {
+  TopkLayout L{};
+  L.nc = (int)cdiv(n_vocab, TOPK_CHUNK);
+  const size_t np = rows * L.nc, nk = np * k;
+  L.off_pm = 0;
+  L.off_ps = align_up(np * 4, 256);
+  L.off_cv = align_up(L.off_ps + np * 4, 256);
+  L.off_ci = align_up(L.off_cv + nk * 4, 256);
+  L.bytes = align_up(L.off_ci + nk * 4, 256);
+  return L;
+}
+
+size_t rw_rocm_logits_topk_workspace_size(size_t rows, size_t n_vocab, size_t k) {
+  if (rows == 0 || n_vocab == 0 || k == 0) return 0;
+  return topk_layout(rows, n_vocab, k).bytes;
+}
+
+int rw_rocm_logits_topk_dev(const float *logits, size_t rows, size_t n_vocab, size_t k, uint32_t *ids,
+                            float *logprobs, void *workspace, size_t workspace_len, void *stream) {
+  if (rows == 0) return RW_OK;
+  if (!logits || !ids || !logprobs) return fail(RW_EINVAL, "logits, ids or logprobs is NULL");
+  if (k < 1 || k > (size_t)TOPK_MAX) return fail(RW_EINVAL, "k = %zu: between 1 and %d", k, TOPK_MAX);
+  if (n_vocab == 0 || n_vocab > (size_t)TOPK_CHUNK * TOPK_MAX_CHUNKS)
+    return fail(RW_EINVAL, "n_vocab = %zu: between 1 and %d", n_vocab, TOPK_CHUNK * TOPK_MAX_CHUNKS);
+  if (rows > 65535) return fail(RW_EINVAL, "rows = %zu: at most 65535", rows);
+  int dev;
+  int rc = current_device(&dev);
+  if (rc) return rc;
+  const TopkLayout L = topk_layout(rows, n_vocab, k);
+  void *ws = workspace;
+  WsHold hold;
+  if (ws) {
+    if (workspace_len < L.bytes) return fail(RW_EINVAL, "workspace of %zu bytes < %zu needed", workspace_len, L.bytes);
+  } else {
+    rc = stream_workspace(dev, stream, L.bytes, hold, &ws);
+    if (rc) return rc;
+  }
+  char *b = (char *)ws;
+  float *pm = (float *)(b + L.off_pm), *ps = (float *)(b + L.off_ps), *cv = (float *)(b + L.off_cv);
+  int *ci = (int *)(b + L.off_ci);
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)L.nc, (unsigned)rows);
+  hipLaunchKernelGGL(k_topk_stats, grid, dim3(256), 0, s, logits, (int)n_vocab, pm, ps);
+  LAUNCH_TRY("k_topk_stats");
+  hipLaunchKernelGGL(k_topk_chunk, grid, dim3(256), 0, s, logits, (int)n_vocab, (int)k, pm, ps, cv, ci);
+  LAUNCH_TRY("k_topk_chunk");
+  hipLaunchKernelGGL(k_topk_merge, dim3((unsigned)rows), dim3(256), 0, s, L.nc, (int)k, cv, ci, ids, logprobs);
+  LAUNCH_TRY("k_topk_merge");
   return RW_OK;
 }
 
