@@ -367,16 +367,29 @@ static void launch_gemm_tm(const GemmSet &set, size_t tiles, const ActView &av, 
   hipLaunchKernelGGL((k_gemm<DT, KW, TM, OFFS>), grid, dim3(64 * KW), 0, s, set, av, m);
 }
 
+// A single-wavefront launch whose 128-row tiles leave SIMDs idle takes
+// 96-row tiles when those still fit one wavefront per SIMD (q/k/v of a
+// 1500-row input: 720 wavefronts of 128 rows, or 960 of 96, on 1024 SIMDs)
+constexpr size_t GEMM_SIMDS = 1024;
+static int gemm_rows(int kw, size_t tiles, int mgroups) {
+  if (mgroups <= 2) return 2;
+  if (kw == 1 && cdiv(mgroups, 3) * tiles <= GEMM_SIMDS && cdiv(mgroups, 4) * tiles < cdiv(mgroups, 3) * tiles)
+    return 3;
+  return 4;
+}
+
 template <int DT, int KW>
 static void launch_gemm_kw(const GemmSet &set, size_t tiles, const ActView &av, int m, hipStream_t s) {
   bool offs = false;
   for (int i = 0; i < set.count; ++i) offs = offs || set.it[i].gp.cm != nullptr;
-  const bool skinny = av.mgroups <= 2;
+  const int tm = gemm_rows(KW, tiles, av.mgroups);
   if (offs) {
-    if (skinny) launch_gemm_tm<DT, KW, 2, true>(set, tiles, av, m, s);
+    if (tm == 2) launch_gemm_tm<DT, KW, 2, true>(set, tiles, av, m, s);
+    else if (KW == 1 && tm == 3) launch_gemm_tm<DT, 1, 3, true>(set, tiles, av, m, s);
     else launch_gemm_tm<DT, KW, 4, true>(set, tiles, av, m, s);
   } else {
-    if (skinny) launch_gemm_tm<DT, KW, 2, false>(set, tiles, av, m, s);
+    if (tm == 2) launch_gemm_tm<DT, KW, 2, false>(set, tiles, av, m, s);
+    else if (KW == 1 && tm == 3) launch_gemm_tm<DT, 1, 3, false>(set, tiles, av, m, s);
     else launch_gemm_tm<DT, KW, 4, false>(set, tiles, av, m, s);
   }
 }

@@ -205,3 +205,31 @@ def test_turbo_q5_1_m40(torch, n, k):
         check_sampled(torch, A.Q5_1, n, k, 40, seed=300, with_bias=False)
     else:
         check_whole(torch, A.Q5_1, n, k, 40, seed=310 + n // 640 + k // 640)
+
+
+@pytest.mark.parametrize("m", [1500, 12000])
+def test_large_v3_qkv_one_launch_rows_independent_of_m(torch, m):
+    """q, k and v of a large-v3 layer in one launch (96-row tiles at
+    M = 1500, 128-row tiles at M = 12000): the sampled rows run alone (64-row
+    tiles) give the same bits, and match the oracle."""
+    d = 1280
+    a = activations(m, d, 61)
+    raws = [weights(A.Q5_1, d, d, 62 + i) for i in range(3)]
+    ws_w = [A.DeviceWeight(A.Q5_1, d, d, r) for r in raws]
+    rows = sample_rows(m, 63)
+
+    def run(x):
+        mm = x.shape[0]
+        ws_len = A.workspace_size(mm, d)
+        ws = torch.empty(ws_len, dtype=torch.uint8, device="cuda:0")
+        A.quantize_dev(torch.from_numpy(np.ascontiguousarray(x)).to("cuda:0"), mm, d, ws, ws_len)
+        outs = [torch.empty(mm, d, device="cuda:0") for _ in range(3)]
+        A.matmul_prequant_multi_dev(ws_w, ws, mm, outs)
+        torch.cuda.synchronize()
+        return [o.cpu().numpy() for o in outs]
+
+    full, alone = run(a), run(a[rows])
+    for raw, f, s in zip(raws, full, alone):
+        assert np.all(np.isfinite(f))
+        assert np.array_equal(f[rows].view(np.uint32), s.view(np.uint32)), "a row depends on m"
+        assert rel_row_l2(s, O.matmul_emul(a[rows], A.Q5_1, raw, d)) <= TOL
