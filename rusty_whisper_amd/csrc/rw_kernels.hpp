@@ -997,48 +997,56 @@ __device__ inline void gemv_fold_oct(const uint8_t *orec, int a_off, int h, int 
 // depends on its weight row and activation row alone.  Blocks past nb in the
 // last octet meet zero weight planes (the upload writes the padding as
 // zeros) and zero activation records: they add exactly +0.
-// y + bias, then GELU (flag 1) and accumulation into the output (flag 2):
-// the epilogue options the GEMM takes (GEMM_GELU, GEMM_ACC)
-__device__ inline void gemv_store(const GemvItem &I, size_t idx, int col, float y) {
-  if (I.bias) y = y + ldg_f(I.bias + col);
-  if (I.flags & 1) {
-    const float inner = 0.7978846f * (y + 0.044715f * y * y * y);
-    y = 0.5f * y * (1.0f + tanhf(inner));
+// The epilogue of one lane: y + bias, then GELU (flag 1) and accumulation
+// into the output (flag 2), the options the GEMM takes (GEMM_GELU,
+// GEMM_ACC).  With PRE, `bv` holds the lane's columns' bias (loaded when
+// the tile started); otherwise the bias is loaded here.  Every value the
+// epilogue reads is requested before any store, so it costs one memory
+// round trip at most.
+template <bool PRE>
+__device__ inline void gemv_epilogue(const GemvItem &I, int gw, int h, int r, int mr,
+                                     const float (&y)[GEMV_NG][4], const float (&bv_in)[GEMV_NG]) {
+  const int n = I.n;
+  float bv[GEMV_NG], x[GEMV_NG][4];
+#pragma unroll
+  for (int j = 0; j < GEMV_NG; ++j)
+    bv[j] = PRE ? bv_in[j] : I.bias ? ldg_f(I.bias + min((gw + j) * RG + r, n - 1)) : 0.0f;
+  if (I.flags & 2) {
+#pragma unroll
+    for (int j = 0; j < GEMV_NG; ++j) {
+      const int col = (gw + j) * RG + r;
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        x[j][v] = gw + j < I.w.ngroups && col < n && 4 * h + v < mr ? ldg_f(I.out + (size_t)(4 * h + v) * n + col)
+                                                                     : 0.0f;
+    }
   }
-  if (I.flags & 2) y = I.out[idx] + y;
-  stg_f(I.out + idx, y);
+#pragma unroll
+  for (int j = 0; j < GEMV_NG; ++j) {
+    const int col = (gw + j) * RG + r;
+    if (gw + j < I.w.ngroups && col < n)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        if (4 * h + v < mr) {
+          float t = y[j][v];
+          if (I.bias) t = t + bv[j];
+          if (I.flags & 1) {
+            const float inner = 0.7978846f * (t + 0.044715f * t * t * t);
+            t = 0.5f * t * (1.0f + tanhf(inner));
+          }
+          if (I.flags & 2) t = x[j][v] + t;
+          stg_f(I.out + (size_t)(4 * h + v) * n + col, t);
+        }
+  }
 }
 
+// One tile of k_gemv: item I's tile wt.y (every wavefront of the workgroup
+// calls it; LDS is free on entry and in use on return).
 template <int DT, int MR, bool GROUPED>
-__global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restrict__ items, const int2 *__restrict__ wg_item,
-                                              GemvSet one, int cap_oct) {
-  extern __shared__ __align__(16) uint8_t lds[];
+__device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I, int2 wt, int cap_oct,
+                                                                uint8_t *lds) {
   constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR;
   constexpr int QB = DT == 8 ? 32 : 16;                // qs bytes per row-block
-  // the descriptor is wave-uniform: scalar loads from the table or kernarg
-  int2 wt;  // (item, tile)
-  if constexpr (GROUPED) {
-    wt = wg_item[blockIdx.x];
-  } else {  // the set's item by uniform compares (no runtime index into the argument)
-    int ii = 0;
-#pragma unroll
-    for (int t = 0; t + 1 < GEMV_SET; ++t)
-      if (t + 1 < one.count && (int)blockIdx.x >= one.end[t]) ii = t + 1;
-    int first = 0;
-#pragma unroll
-    for (int t = 0; t + 1 < GEMV_SET; ++t)
-      if (ii == t + 1) first = one.end[t];
-    wt = make_int2(ii, (int)blockIdx.x - first);
-  }
-  if (wt.x < 0) return;  // a slot no item uses (the whole workgroup)
-  GemvItem I = one.it[0];
-  if constexpr (GROUPED) {
-    I = items[wt.x];
-  } else {
-#pragma unroll
-    for (int t = 1; t < GEMV_SET; ++t)
-      if (wt.x == t) I = one.it[t];
-  }
   const WeightView &w = I.w;
   const int nb = w.nb;
   const int lks = I.lks, KS = 1 << lks;
@@ -1079,6 +1087,13 @@ __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restri
   constexpr bool EARLY = GROUPED || DT == 2 || (MR == 1 && (DT == 3 || DT == 6));
   GemvOct<DT> cur;
   if (EARLY && o0 < min(o1, o0 + ch)) gemv_load_oct<DT>(w, gw, o0, rq, rd, rm, rh, vq, vs, vh, cur);
+  // grouped launches: this lane's columns' bias, in flight with the first
+  // octet (the others, and Q5_1, load it in the epilogue: registers)
+  constexpr bool PRE = GROUPED && DT != 7;
+  float bv[GEMV_NG];
+#pragma unroll
+  for (int j = 0; j < GEMV_NG; ++j)
+    bv[j] = PRE && I.bias && part == 0 ? ldg_f(I.bias + min((gw + j) * RG + r, I.n - 1)) : 0.0f;
 
   // layernorm statistics of the m activation rows (single / set launches
   // with I.lnw): every workgroup computes them, in the same tree order, and
@@ -1158,9 +1173,20 @@ __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restri
       if (c0 >= c1) continue;
       uint8_t *base = lds + pp * ch * OCT * REC;
       if constexpr (GROUPED) {
+        // RB loads per thread in flight at a time (as many as the
+        // registers beside the first octet's allow)
+        constexpr int RB = DT == 2 || DT == 6 ? 4 : DT == 7 ? 1 : 2;
         const uint4 *src = reinterpret_cast<const uint4 *>(I.rec + (size_t)c0 * OCT * REC);
-        for (int z = t; z < (c1 - c0) * OCT * (REC / 16); z += 256)
-          reinterpret_cast<uint4 *>(base)[z] = ldg_u4(src + z);
+        const int total = (c1 - c0) * OCT * (REC / 16);
+        for (int z0 = t; z0 < total; z0 += RB * 256) {
+          uint4 rv[RB];
+#pragma unroll
+          for (int u = 0; u < RB; ++u)
+            if (z0 + 256 * u < total) rv[u] = ldg_u4(src + z0 + 256 * u);
+#pragma unroll
+          for (int u = 0; u < RB; ++u)
+            if (z0 + 256 * u < total) reinterpret_cast<uint4 *>(base)[z0 + 256 * u] = rv[u];
+        }
       } else {
         gemv_fill<DT, MR>(I, nb, c0, c1, base, t, ln_s);
       }
@@ -1185,17 +1211,8 @@ __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restri
 #pragma unroll
     for (int v = 0; v < 4; ++v) y[j][v] = has_min(DT) ? acc[j][v] + accm[j][v] : acc[j][v];
 
-  const int n = I.n;
   if (KS == 1) {
-#pragma unroll
-    for (int j = 0; j < GEMV_NG; ++j) {
-      const int g = gw + j, col = g * RG + r;
-      if (g < w.ngroups && col < n)
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-          if (4 * h + v < MR)
-            gemv_store(I, (size_t)(4 * h + v) * n + col, col, y[j][v]);
-    }
+    gemv_epilogue<PRE>(I, gw, h, r, MR, y, bv);
     return;
   }
   __syncthreads();  // the activation LDS is reused for the partial sums
@@ -1207,17 +1224,43 @@ __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restri
   __syncthreads();
   if (part == 0) {
 #pragma unroll
-    for (int j = 0; j < GEMV_NG; ++j) {
-      const int g = gw + j, col = g * RG + r;
-      if (g < w.ngroups && col < n)
+    for (int j = 0; j < GEMV_NG; ++j)
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
-          if (4 * h + v < MR) {
-            float tt = red[(wv * 4 * GEMV_NG + 4 * j + v) * 64 + l];
-            for (int p = 1; p < KS; ++p) tt = tt + red[((wv + p) * 4 * GEMV_NG + 4 * j + v) * 64 + l];
-            gemv_store(I, (size_t)(4 * h + v) * n + col, col, tt);
-          }
-    }
+      for (int v = 0; v < 4; ++v) {
+        float tt = red[(wv * 4 * GEMV_NG + 4 * j + v) * 64 + l];
+        for (int p = 1; p < KS; ++p) tt = tt + red[((wv + p) * 4 * GEMV_NG + 4 * j + v) * 64 + l];
+        y[j][v] = tt;
+      }
+    gemv_epilogue<PRE>(I, gw, h, r, MR, y, bv);
+  }
+}
+
+// One launch: workgroup -> (item, tile) through `wg_item` (grouped; item -1
+// = an unused slot) or, for a single or set launch, the set's item by
+// uniform compares (no runtime index into the argument).
+template <int DT, int MR, bool GROUPED>
+__global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restrict__ items, const int2 *__restrict__ wg_item,
+                                              GemvSet one, int cap_oct) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  // the descriptor is wave-uniform: scalar loads from the table or kernarg
+  if constexpr (GROUPED) {
+    const int2 wt = wg_item[blockIdx.x];  // (item, tile)
+    if (wt.x < 0) return;                 // a slot no item uses (the whole workgroup)
+    gemv_tile<DT, MR, true>(items[wt.x], wt, cap_oct, lds);
+  } else {
+    int ii = 0;
+#pragma unroll
+    for (int t = 0; t + 1 < GEMV_SET; ++t)
+      if (t + 1 < one.count && (int)blockIdx.x >= one.end[t]) ii = t + 1;
+    int first = 0;
+#pragma unroll
+    for (int t = 0; t + 1 < GEMV_SET; ++t)
+      if (ii == t + 1) first = one.end[t];
+    GemvItem I = one.it[0];
+#pragma unroll
+    for (int t = 1; t < GEMV_SET; ++t)
+      if (ii == t) I = one.it[t];
+    gemv_tile<DT, MR, false>(I, make_int2(ii, (int)blockIdx.x - first), cap_oct, lds);
   }
 }
 

@@ -484,12 +484,12 @@ static GemvItem gemv_item(const rw_weight *w, const float *a, const float *bias,
 template <int DT, int MR>
 static void launch_gemv_mr(const GemvItem *items, const int2 *wg_item, const GemvSet &one, int wgs, int cap_oct,
                            hipStream_t s) {
+  const size_t lds = gemv_lds_bytes(MR, cap_oct);
   if (items)
-    hipLaunchKernelGGL((k_gemv<DT, MR, true>), dim3((unsigned)wgs), dim3(256), gemv_lds_bytes(MR, cap_oct), s,
-                       items, wg_item, one, cap_oct);
+    hipLaunchKernelGGL((k_gemv<DT, MR, true>), dim3((unsigned)wgs), dim3(256), lds, s, items, wg_item, one, cap_oct);
   else
-    hipLaunchKernelGGL((k_gemv<DT, MR, false>), dim3((unsigned)wgs), dim3(256), gemv_lds_bytes(MR, cap_oct), s,
-                       items, wg_item, one, cap_oct);
+    hipLaunchKernelGGL((k_gemv<DT, MR, false>), dim3((unsigned)wgs), dim3(256), lds, s, items, wg_item, one,
+                       cap_oct);
 }
 
 // one k_gemv launch: `items` (device) + `wg_item` (device) for a group, or
