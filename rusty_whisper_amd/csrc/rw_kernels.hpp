@@ -1041,8 +1041,13 @@ __device__ inline void gemv_epilogue(const GemvItem &I, int gw, int h, int r, in
 }
 
 // One tile of k_gemv: item I's tile wt.y (every wavefront of the workgroup
-// calls it; LDS is free on entry and in use on return).
-template <int DT, int MR, bool GROUPED>
+// calls it; LDS is free on entry and in use on return).  PD > 1: the
+// latency form for launches of at most one wavefront per SIMD, whose
+// records fit LDS at once: the first PD octets of a wavefront's part are
+// requested before the statistics and the fill, and each octet's slot is
+// refilled PD octets ahead as soon as it is folded.  The octets are folded
+// in the same order whatever PD, so the results do not depend on it.
+template <int DT, int MR, bool GROUPED, int PD>
 __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I, int2 wt, int cap_oct,
                                                                 uint8_t *lds) {
   constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR;
@@ -1084,9 +1089,14 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
   // registers fit beside the fill's: grouped launches copy records and
   // always can; fills can for Q4_0, and for Q4_1 and Q5_0 at one row (the
   // other forms would spill)
-  constexpr bool EARLY = GROUPED || DT == 2 || (MR == 1 && (DT == 3 || DT == 6));
-  GemvOct<DT> cur;
-  if (EARLY && o0 < min(o1, o0 + ch)) gemv_load_oct<DT>(w, gw, o0, rq, rd, rm, rh, vq, vs, vh, cur);
+  constexpr bool EARLY = PD > 1 || GROUPED || DT == 2 || (MR == 1 && (DT == 3 || DT == 6));
+  GemvOct<DT> ring[PD];
+  GemvOct<DT> &cur = ring[0];
+  if (EARLY) {
+#pragma unroll
+    for (int u = 0; u < PD; ++u)
+      if (o0 + u < min(o1, o0 + ch)) gemv_load_oct<DT>(w, gw, o0 + u, rq, rd, rm, rh, vq, vs, vh, ring[u]);
+  }
   // grouped launches: this lane's columns' bias, in flight with the first
   // octet (the others, and Q5_1, load it in the epilogue: registers)
   constexpr bool PRE = GROUPED && DT != 7;
@@ -1196,11 +1206,22 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
     // --- weights: each octet loaded whole for all row groups (the planes
     // are padded to whole octets), then folded in
     if (p0 < p1) {
-      if (!EARLY) gemv_load_oct<DT>(w, gw, p0, rq, rd, rm, rh, vq, vs, vh, cur);
-      gemv_fold_oct<DT, MR>(lds + part * ch * OCT * REC, a_off, h, rot, cur, acc, accm);
-      for (int o = p0 + 1; o < p1; ++o) {
-        gemv_load_oct<DT>(w, gw, o, rq, rd, rm, rh, vq, vs, vh, cur);
-        gemv_fold_oct<DT, MR>(lds + (part * ch + o - p0) * OCT * REC, a_off, h, rot, cur, acc, accm);
+      if constexpr (PD > 1) {  // one chunk: octets p0 .. p0 + PD - 1 are in flight
+        for (int o = p0; o < p1; o += PD) {
+#pragma unroll
+          for (int u = 0; u < PD; ++u)
+            if (o + u < p1) {
+              gemv_fold_oct<DT, MR>(lds + (part * ch + o + u - p0) * OCT * REC, a_off, h, rot, ring[u], acc, accm);
+              if (o + u + PD < p1) gemv_load_oct<DT>(w, gw, o + u + PD, rq, rd, rm, rh, vq, vs, vh, ring[u]);
+            }
+        }
+      } else {
+        if (!EARLY) gemv_load_oct<DT>(w, gw, p0, rq, rd, rm, rh, vq, vs, vh, cur);
+        gemv_fold_oct<DT, MR>(lds + part * ch * OCT * REC, a_off, h, rot, cur, acc, accm);
+        for (int o = p0 + 1; o < p1; ++o) {
+          gemv_load_oct<DT>(w, gw, o, rq, rd, rm, rh, vq, vs, vh, cur);
+          gemv_fold_oct<DT, MR>(lds + (part * ch + o - p0) * OCT * REC, a_off, h, rot, cur, acc, accm);
+        }
       }
     }
   }
@@ -1238,15 +1259,16 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
 // One launch: workgroup -> (item, tile) through `wg_item` (grouped; item -1
 // = an unused slot) or, for a single or set launch, the set's item by
 // uniform compares (no runtime index into the argument).
-template <int DT, int MR, bool GROUPED>
-__global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restrict__ items, const int2 *__restrict__ wg_item,
-                                              GemvSet one, int cap_oct) {
+template <int DT, int MR, bool GROUPED, int PD = 1>
+__global__ __launch_bounds__(256, PD > 1 ? 1 : GEMV_WPE) void k_gemv(const GemvItem *__restrict__ items,
+                                                                   const int2 *__restrict__ wg_item, GemvSet one,
+                                                                   int cap_oct) {
   extern __shared__ __align__(16) uint8_t lds[];
   // the descriptor is wave-uniform: scalar loads from the table or kernarg
   if constexpr (GROUPED) {
     const int2 wt = wg_item[blockIdx.x];  // (item, tile)
     if (wt.x < 0) return;                 // a slot no item uses (the whole workgroup)
-    gemv_tile<DT, MR, true>(items[wt.x], wt, cap_oct, lds);
+    gemv_tile<DT, MR, true, PD>(items[wt.x], wt, cap_oct, lds);
   } else {
     int ii = 0;
 #pragma unroll
@@ -1260,7 +1282,7 @@ __global__ __launch_bounds__(256, GEMV_WPE) void k_gemv(const GemvItem *__restri
 #pragma unroll
     for (int t = 1; t < GEMV_SET; ++t)
       if (ii == t) I = one.it[t];
-    gemv_tile<DT, MR, false>(I, make_int2(ii, (int)blockIdx.x - first), cap_oct, lds);
+    gemv_tile<DT, MR, false, PD>(I, make_int2(ii, (int)blockIdx.x - first), cap_oct, lds);
   }
 }
 

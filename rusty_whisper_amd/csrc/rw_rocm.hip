@@ -481,12 +481,30 @@ static GemvItem gemv_item(const rw_weight *w, const float *a, const float *bias,
   return it;
 }
 
+// A single or set launch of at most one wavefront per SIMD whose records fit
+// LDS at once takes k_gemv's latency form: every wavefront keeps up to
+// GEMV_PD weight octets in flight (it has the registers of a whole SIMD; a
+// third octet measured slower).
+constexpr int GEMV_PD = 2;
+constexpr int GEMV_LAT_WGS = 256;  // 4 wavefronts each: one per SIMD of 256 CUs
+static bool gemv_latency_form(const GemvSet &one, int wgs, int cap_oct) {
+  if (wgs > GEMV_LAT_WGS) return false;
+  for (int i = 0; i < one.count; ++i) {
+    const int lks = one.it[i].lks, span = (one.it[i].w.noct + (1 << lks) - 1) >> lks;
+    if ((cap_oct >> lks) < span) return false;  // the records would come in chunks
+  }
+  return true;
+}
+
 template <int DT, int MR>
 static void launch_gemv_mr(const GemvItem *items, const int2 *wg_item, const GemvSet &one, int wgs, int cap_oct,
                            hipStream_t s) {
   const size_t lds = gemv_lds_bytes(MR, cap_oct);
   if (items)
     hipLaunchKernelGGL((k_gemv<DT, MR, true>), dim3((unsigned)wgs), dim3(256), lds, s, items, wg_item, one, cap_oct);
+  else if (gemv_latency_form(one, wgs, cap_oct))
+    hipLaunchKernelGGL((k_gemv<DT, MR, false, GEMV_PD>), dim3((unsigned)wgs), dim3(256), lds, s, items,
+                       wg_item, one, cap_oct);
   else
     hipLaunchKernelGGL((k_gemv<DT, MR, false>), dim3((unsigned)wgs), dim3(256), lds, s, items, wg_item, one,
                        cap_oct);
