@@ -434,15 +434,6 @@ __global__ __launch_bounds__(256) void k_quantize(const float *__restrict__ a, i
   }
 }
 
-// quantize_acts_i8's q for v = x * inv as a float: round half away from
-// zero, clamp to +-127 (an infinite v, from an infinite inv, included),
-// NaN -> 0, and +0 (never -0) for zero
-__device__ inline float quant_q(float v) {
-  const float r = roundf(fminf(fabsf(v), 127.0f));
-  if (v != v) return 0.0f;
-  return v <= -0.5f ? -r : r;
-}
-
 // Activations for the encoder GEMM: WPR wavefronts per row (4 / WPR rows
 // per workgroup; rows >= m of the padded row groups are written as zeros).
 // A row's blocks go in passes of 8 (1 KB of f32), pass P to wavefront
@@ -624,13 +615,13 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
       const float inv = bcast8<p & 7>(iv[p >> 3], lt);
       const float da = bcast8<p & 7>(dv[p >> 3], lt);
       const float dd = da * down;
-      const float q0 = quant_q(__fmul_rn(v[p].x, inv)), q1 = quant_q(__fmul_rn(v[p].y, inv));
-      const float q2 = quant_q(__fmul_rn(v[p].z, inv)), q3 = quant_q(__fmul_rn(v[p].w, inv));
+      const int q0 = round_clamp_i8(__fmul_rn(v[p].x, inv)), q1 = round_clamp_i8(__fmul_rn(v[p].y, inv));
+      const int q2 = round_clamp_i8(__fmul_rn(v[p].z, inv)), q3 = round_clamp_i8(__fmul_rn(v[p].w, inv));
       // the block's sum(q_a) (exact integers), times d_a, counted once
-      const int bsum = sum8((int)q0 + (int)q1 + (int)q2 + (int)q3);
+      const int bsum = sum8(q0 + q1 + q2 + q3);
       if (lt == 0) ptot += __fmul_rn(da, (float)bsum);
-      const h2v lo2 = {(_Float16)__fmul_rn(q0, dd), (_Float16)__fmul_rn(q1, dd)};
-      const h2v hi2 = {(_Float16)__fmul_rn(q2, dd), (_Float16)__fmul_rn(q3, dd)};
+      const h2v lo2 = {(_Float16)__fmul_rn((float)q0, dd), (_Float16)__fmul_rn((float)q1, dd)};
+      const h2v hi2 = {(_Float16)__fmul_rn((float)q2, dd), (_Float16)__fmul_rn((float)q3, dd)};
       if (b0 + lb < nb) {
         __builtin_amdgcn_raw_buffer_store_b64(
             (rw_u32x2){__builtin_bit_cast(uint32_t, lo2), __builtin_bit_cast(uint32_t, hi2)}, ro, voff,

@@ -285,8 +285,9 @@ def _a16_index(m, k):
 
 @pytest.mark.parametrize("k", [32, 96, 416, 1024, 1280, 2048, 5120, 8224, 16384])
 def test_gemm_activation_plane_bit_exact(torch, k):
-    # one, two and four wavefronts per row (416: two; 1024 and up: four);
-    # 8224 and 16384 take the long-row path (the row is read twice)
+    # one, two and four wavefronts per row (416: two of one pass; 1280: two
+    # of three passes; 1024, 2048 and 5120: four); 8224 and 16384 take the
+    # long-row path (the row is read twice)
     a = np.concatenate([activations(21, k, seed=k, outliers=0.01), edge_activation_rows(k), _scale_rows(k)])
     m = a.shape[0]
     assert m > 8  # the encoder (f16) layout
