@@ -140,13 +140,23 @@ template <int CTRL>
 __device__ inline float dpp_f(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
 }
-// the maximum over each 8-lane group, in every lane of it
-__device__ inline float max8(float b) {
-  b = fmaxf(b, dpp_f<0xB1>(b));   // quad_perm [1,0,3,2]: lane i ^ 1
-  b = fmaxf(b, dpp_f<0x4E>(b));   // quad_perm [2,3,0,1]: lane i ^ 2
-  b = fmaxf(b, dpp_f<0x141>(b));  // row_half_mirror: lane 7 - i of the 8
-  return b;
+// The maximum over each 8-lane group of values that are >= +0 and not NaN,
+// in every lane of it.  Such floats order as their bit patterns do, so the
+// maxima are integer DPP maxima (no NaN quieting around each move).
+__device__ inline float max8_nn(float b) {
+  int v = __float_as_int(b);
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]: lane i ^ 1
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false));   // quad_perm [2,3,0,1]: lane i ^ 2
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false));  // row_half_mirror: lane 7 - i
+  return __int_as_float(v);
 }
+// max(0, |x|, |y|, |z|, |w|), NaN skipped: the amax fold of
+// quantize_acts_i8, which starts at 0 (src/quant.rs:701), over one lane's four
+// values (a block's eight lanes then meet in max8_nn)
+__device__ inline float amax4(float4 x) {
+  return fmaxf(fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))), 0.0f);
+}
+__device__ inline float max_nn(float a, float b) { return __int_as_float(max(__float_as_int(a), __float_as_int(b))); }
 // the sum over each 8-lane group, in every lane of it
 __device__ inline int sum8(int v) {
   v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);
@@ -390,7 +400,7 @@ struct BlockQuant {
 };
 
 __device__ inline BlockQuant quantize_block8(float4 x) {
-  const float amax = max8(fmaxf(fmaxf(fabsf(x.x), fabsf(x.y)), fmaxf(fabsf(x.z), fabsf(x.w))));
+  const float amax = max8_nn(amax4(x));
   BlockQuant b;
   b.d = __fdiv_rn(amax, 127.0f);
   const float inv = b.d > 0.0f ? __fdiv_rn(1.0f, b.d) : 0.0f;
@@ -502,8 +512,8 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
     float amax = 0.0f;
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-      bam[p] = max8(fmaxf(fmaxf(fabsf(v[p].x), fabsf(v[p].y)), fmaxf(fabsf(v[p].z), fabsf(v[p].w))));
-      amax = fmaxf(amax, bam[p]);
+      bam[p] = max8_nn(amax4(v[p]));
+      amax = max_nn(amax, bam[p]);
     }
     return amax;
   };
@@ -554,21 +564,21 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
       }
     }
   }
-  float amax = 0.0f;  // fmaxf drops NaN, in any order of combination
+  float amax = 0.0f;  // the block maxima are >= 0 and never NaN: integer maxima
   if (live) {
     for (int c = 0; c < nch; ++c) {
       if (!LN) load(c);
-      amax = fmaxf(amax, block_max());
+      amax = max_nn(amax, block_max());
     }
-    amax = fmaxf(amax, __shfl_xor(amax, 8));
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
-    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    amax = max_nn(amax, __shfl_xor(amax, 8));
+    amax = max_nn(amax, __shfl_xor(amax, 16));
+    amax = max_nn(amax, __shfl_xor(amax, 32));
   }
   if (WPR > 1) {  // every wavefront reaches the barrier
     if (lane == 0) part_max[wv] = amax;
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < WPR; ++j) amax = fmaxf(amax, part_max[wv - part + j]);
+    for (int j = 0; j < WPR; ++j) amax = max_nn(amax, part_max[wv - part + j]);
   }
   if (!live) {
     for (int c = 0; c < nch; ++c)

@@ -67,6 +67,11 @@ def edge_activation_rows(k: int) -> np.ndarray:
     n = np.ones(k, np.float32)
     n[3] = np.nan  # NaN ignored by the amax fold, quantizes to 0
     rows.append(n)
+    nn = np.ones(k, np.float32)
+    nn[:32] = np.nan  # a block of NaN: the fold from 0 gives amax = 0 -> d = 0, q = 0
+    if k >= 64:
+        nn[36:40] = np.nan  # one 4-value lane of a block all NaN
+    rows.append(nn)
     i = np.ones(k, np.float32)
     i[5] = np.inf  # amax = inf -> inv = 0 -> q = 0 (inf*0 = NaN -> 0)
     rows.append(i)
