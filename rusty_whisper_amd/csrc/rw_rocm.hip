@@ -312,10 +312,8 @@ static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &
     // The shape follows k alone, so a row's bits never depend on m.  The
     // kernel is VALU-bound (every lane of a wavefront runs a pass, live
     // blocks or not): rows of 5-6 passes (k = 1280) take 2 wavefronts of 3
-    // passes (48 block slots for 40, against 64 with 4 wavefronts of 2:
-    // 4.8 against 5.6 us at m = 1500); 9-32 passes take 4 wavefronts of 8,
-    // whose passes past the row's end are skipped whole (k = 5120: 11.3 us,
-    // against 11.9 with 5 passes, same bytes).
+    // passes (48 block slots for 40, against 64 with 4 wavefronts of 2: 4.5
+    // against 4.9 us per launch at m = 1500 in a replayed graph).
     const int passes = (L.nb + 7) / 8;
     if (lnw) {
       if (passes <= 1) RW_QF16(1, 1, true);
@@ -323,6 +321,7 @@ static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &
       else if (passes <= 4) RW_QF16(1, 4, true);
       else if (passes <= 6) RW_QF16(3, 2, true);
       else if (passes <= 8) RW_QF16(2, 4, true);
+      else if (passes <= 20) RW_QF16(5, 4, true);
       else RW_QF16(8, 4, true);
     } else {
       if (passes <= 1) RW_QF16(1, 1, false);
@@ -330,6 +329,7 @@ static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &
       else if (passes <= 4) RW_QF16(1, 4, false);
       else if (passes <= 6) RW_QF16(3, 2, false);
       else if (passes <= 8) RW_QF16(2, 4, false);
+      else if (passes <= 20) RW_QF16(5, 4, false);
       else RW_QF16(8, 4, false);
     }
 #undef RW_QF16
