@@ -164,13 +164,12 @@ __device__ inline int sum8(int v) {
   v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false);
   return v;
 }
-// lane T's value of each 8-lane group, in every lane of it (lt = lane % 8)
+// lane T's value of each 8-lane group, in every lane of it: ds_swizzle in
+// bit-mask mode (lane i reads lane (i & 0x18) | T of its 32), one instruction
+// on the LDS pipe instead of DPP moves and a select on the VALU
 template <int T>
-__device__ inline float bcast8(float v, int lt) {
-  constexpr int Q = T & 3;
-  const float x1 = dpp_f<Q | (Q << 2) | (Q << 4) | (Q << 6)>(v);  // quad_perm [Q,Q,Q,Q]
-  const float x2 = dpp_f<0x141>(x1);                             // the other quad's copy
-  return (lt >> 2) == (T >> 2) ? x1 : x2;
+__device__ inline float bcast8(float v) {
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x18 | (T << 5)));
 }
 
 // --------------------------------------------------------------- k_repack
@@ -622,8 +621,8 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
       constexpr int p = decltype(pc)::value;
       const int b0 = first(c, p);
       if (b0 >= nb) return;  // uniform
-      const float inv = bcast8<p & 7>(iv[p >> 3], lt);
-      const float da = bcast8<p & 7>(dv[p >> 3], lt);
+      const float inv = bcast8<p & 7>(iv[p >> 3]);
+      const float da = bcast8<p & 7>(dv[p >> 3]);
       const float dd = da * down;
       const int q0 = round_clamp_i8(__fmul_rn(v[p].x, inv)), q1 = round_clamp_i8(__fmul_rn(v[p].y, inv));
       const int q2 = round_clamp_i8(__fmul_rn(v[p].z, inv)), q3 = round_clamp_i8(__fmul_rn(v[p].w, inv));
