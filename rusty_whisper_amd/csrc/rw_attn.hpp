@@ -92,30 +92,50 @@ __device__ inline void att_split_rows(size_t idx, const float *__restrict__ x, i
   *reinterpret_cast<uint4 *>(lo + o) = *reinterpret_cast<const uint4 *>(l8);
 }
 
-// v -> v^T [head][64][t_pad] f16 pairs, kv positions permuted by attn_vpos
-// within each 16-block; kv >= t are zeros.  Item idx covers (head, 8
-// positions, d): a wavefront reads 64 consecutive d of one kv row.
-__device__ inline void att_split_vt(size_t idx, const float *__restrict__ v, int ld, int t, int t_pad,
-                                    uint16_t *__restrict__ hi, uint16_t *__restrict__ lo) {
-  const int nc = t_pad / 8;
-  const int d = (int)(idx % ATT_DH);
-  const size_t hc = idx / ATT_DH;
-  const int c = (int)(hc % nc), head = (int)(hc / nc);
-  uint16_t h8[8], l8[8];
+// v^T [head][64][t_pad] f16 pairs: kv positions permuted by attn_vpos within
+// each 16-block; kv >= t are zeros.
+// v -> v^T pairs, one workgroup per (head, 64 kv positions): the 64 x 64
+// values are read as row-contiguous 16-byte loads, split, and transposed
+// through LDS (each position at its attn_vpos place, an involution), then
+// written as 128-byte runs of positions per d and plane.  `sh` holds 2 x 64
+// rows of ATT_VT_LD halves.
+constexpr int ATT_VT_KV = 64, ATT_VT_LD = ATT_VT_KV + 8;
+__device__ inline int att_vt_tiles(int t_pad) { return (t_pad + ATT_VT_KV - 1) / ATT_VT_KV; }
+__device__ inline void att_split_vt_tile(int tile, const float *__restrict__ v, int ld, int t, int t_pad,
+                                         uint16_t *__restrict__ hi, uint16_t *__restrict__ lo, uint16_t *sh) {
+  const int nt = att_vt_tiles(t_pad);
+  const int head = tile / nt, kv0 = (tile % nt) * ATT_VT_KV;
+  const int th = threadIdx.x, d4 = th & 15;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int p = c * 8 + e;
-    const int kv = (p & ~15) | attn_vpos(p & 15);
-    const float x = kv < t ? v[(size_t)kv * ld + head * ATT_DH + d] : 0.0f;
-    att_split(x, h8[e], l8[e]);
+  for (int u = 0; u < 4; ++u) {
+    const int row = (th >> 4) + 16 * u, kv = kv0 + row;
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (kv < t) x = *reinterpret_cast<const float4 *>(v + (size_t)kv * ld + head * ATT_DH + 4 * d4);
+    const int pos = (row & ~15) | attn_vpos(row & 15);
+    const float xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint16_t hb, lb;
+      att_split(xs[e], hb, lb);
+      sh[(4 * d4 + e) * ATT_VT_LD + pos] = hb;
+      sh[(ATT_DH + 4 * d4 + e) * ATT_VT_LD + pos] = lb;
+    }
   }
-  const size_t o = ((size_t)head * ATT_DH + d) * t_pad + c * 8;
-  *reinterpret_cast<uint4 *>(hi + o) = *reinterpret_cast<const uint4 *>(h8);
-  *reinterpret_cast<uint4 *>(lo + o) = *reinterpret_cast<const uint4 *>(l8);
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int c = th + 256 * u;  // (plane, d, 8 positions)
+    const int pl = c >> 9, d = (c >> 3) & 63, ch = c & 7;
+    if (kv0 + 8 * ch < t_pad) {
+      const uint4 w = *reinterpret_cast<const uint4 *>(sh + (pl * ATT_DH + d) * ATT_VT_LD + 8 * ch);
+      *reinterpret_cast<uint4 *>((pl ? lo : hi) + ((size_t)head * ATT_DH + d) * t_pad + kv0 + 8 * ch) = w;
+    }
+  }
 }
 
 // All three splits in one launch: workgroups [0, wq) split q (scaled by
-// 1/8, exact), [wq, wq + wk) split k, the rest split v into v^T.
+// 1/8, exact), [wq, wq + wk) split k, the rest split v into v^T
+// (n_head * att_vt_tiles(tkv_pad) workgroups).
 __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ q, int ldq, int t_q,
                                                     const float *__restrict__ k, int ldk, const float *__restrict__ v,
                                                     int ldv, int t_kv, AttnPlanes P, int n_head, int wq, int wk) {
@@ -129,9 +149,11 @@ __global__ __launch_bounds__(256) void k_attn_split(const float *__restrict__ q,
     if (idx < (size_t)n_head * P.tkv_pad * 8)
       att_split_rows(idx, k, ldk, t_kv, P.tkv_pad, 1.0f, const_cast<uint16_t *>(P.kh), const_cast<uint16_t *>(P.kl));
   } else {
-    const size_t idx = (size_t)(bx - wq - wk) * 256 + threadIdx.x;
-    if (idx < (size_t)n_head * (P.tkv_pad / 8) * ATT_DH)
-      att_split_vt(idx, v, ldv, t_kv, P.tkv_pad, const_cast<uint16_t *>(P.vh), const_cast<uint16_t *>(P.vl));
+    __shared__ __align__(16) uint16_t sh[2 * ATT_DH * ATT_VT_LD];
+    const int tile = bx - wq - wk;
+    if (tile < n_head * att_vt_tiles(P.tkv_pad))  // uniform: the whole workgroup
+      att_split_vt_tile(tile, v, ldv, t_kv, P.tkv_pad, const_cast<uint16_t *>(P.vh), const_cast<uint16_t *>(P.vl),
+                        sh);
   }
 }
 

@@ -927,7 +927,8 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
   }
   if (!kv_split) {
     const size_t nq = (size_t)n_head * L.tq_pad * 8, nk = (size_t)n_head * P.tkv_pad * 8;
-    const int wq = (int)cdiv(nq, 256), wk = (int)cdiv(nk, 256), wv = wk;  // v^T: as many items as k
+    const int wq = (int)cdiv(nq, 256), wk = (int)cdiv(nk, 256);
+    const int wv = n_head * (int)cdiv(P.tkv_pad, ATT_VT_KV);  // v^T: one workgroup per (head, 64 positions)
     hipLaunchKernelGGL(k_attn_split, dim3((unsigned)(wq + wk + wv)), dim3(256), 0, s, q, (int)ldq, (int)t_q, k,
                        (int)ldk, v, (int)ldv, (int)t_kv, P, n_head, wq, wk);
     LAUNCH_TRY("k_attn_split");
@@ -1852,8 +1853,8 @@ int rw_rocm_decoder_set_audio_dev(rw_decoder *d, const float *enc_out, void *str
     const AttnPlanes cp = d->cross->planes(l);
     AttnPlanes P{nullptr, nullptr, cp.kh, cp.kl, cp.vh, cp.vl, A.tq_pad, cp.tkv_pad};
     const size_t nk = (size_t)d->p.n_head * cp.tkv_pad * 8;
-    const int wk = (int)cdiv(nk, 256);
-    hipLaunchKernelGGL(k_attn_split, dim3((unsigned)(2 * wk)), dim3(256), 0, s, nullptr, (int)n, 0, kf, (int)n, vf,
+    const int wk = (int)cdiv(nk, 256), wv = d->p.n_head * (int)cdiv(cp.tkv_pad, ATT_VT_KV);
+    hipLaunchKernelGGL(k_attn_split, dim3((unsigned)(wk + wv)), dim3(256), 0, s, nullptr, (int)n, 0, kf, (int)n, vf,
                        (int)n, (int)T, P, d->p.n_head, 0, wk);
     LAUNCH_TRY("k_attn_split");
   }
