@@ -916,8 +916,8 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
     LAUNCH_TRY("k_attn_zero");
     return RW_OK;
   }
-  // kv_split: K and v^T already split (the decoder's cross-attention); only q
-  // needs splitting, which k_attn does as it loads it
+  // k_attn splits q (f32, scaled by 1/8) as it loads it; K and v^T are split
+  // here, or were split before (kv_split: the decoder's cross-attention)
   // planes padded to this call's t_kv (the layout may be sized for a longer
   // one, e.g. a decoder's n_ctx)
   AttnPlanes P{qh, ql, kh, kl, vh, vl, L.tq_pad, (int)std::min<size_t>(align_up(t_kv, ATT_KVB), L.tkv_pad)};
@@ -925,12 +925,12 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
     P.kh = kv_split->kh, P.kl = kv_split->kl, P.vh = kv_split->vh, P.vl = kv_split->vl;
     P.tkv_pad = kv_split->tkv_pad;
   }
-  if (!kv_split) {
-    const size_t nq = (size_t)n_head * L.tq_pad * 8, nk = (size_t)n_head * P.tkv_pad * 8;
-    const int wq = (int)cdiv(nq, 256), wk = (int)cdiv(nk, 256);
+  if (!kv_split) {  // k and v only: k_attn splits q as it loads it
+    const size_t nk = (size_t)n_head * P.tkv_pad * 8;
+    const int wk = (int)cdiv(nk, 256);
     const int wv = n_head * (int)cdiv(P.tkv_pad, ATT_VT_KV);  // v^T: one workgroup per (head, 64 positions)
-    hipLaunchKernelGGL(k_attn_split, dim3((unsigned)(wq + wk + wv)), dim3(256), 0, s, q, (int)ldq, (int)t_q, k,
-                       (int)ldk, v, (int)ldv, (int)t_kv, P, n_head, wq, wk);
+    hipLaunchKernelGGL(k_attn_split, dim3((unsigned)(wk + wv)), dim3(256), 0, s, q, (int)ldq, (int)t_q, k,
+                       (int)ldk, v, (int)ldv, (int)t_kv, P, n_head, 0, wk);
     LAUNCH_TRY("k_attn_split");
   }
   // this call's split (the layout's is for its longest kv; the rule grows
@@ -938,7 +938,7 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
   const int nsplit = std::min(L.nsplit, attn_nsplit((size_t)(L.tq_pad / ATT_QB) * n_head, cdiv(t_kv, ATT_KVB)));
   float *part = nsplit > 1 ? (float *)(b + L.off_part) : nullptr;
   hipLaunchKernelGGL(k_attn, dim3((unsigned)(L.tq_pad / ATT_QB), (unsigned)n_head, (unsigned)nsplit), dim3(128), 0, s,
-                     P, (int)t_q, (int)t_kv, causal ? 1 : 0, out, (int)ldo, part, kv_split ? q : nullptr, (int)ldq);
+                     P, (int)t_q, (int)t_kv, causal ? 1 : 0, out, (int)ldo, part, q, (int)ldq);
   LAUNCH_TRY("k_attn");
   if (part) {
     const size_t nz = t_q * (size_t)n_head * ATT_DH;
