@@ -871,31 +871,33 @@ __global__ __launch_bounds__(256) void k_gemv_records(const GemvItem *__restrict
   }
 }
 
-// row groups (of 32 weight rows) per k_gemv wavefront
-#ifndef GEMV_NG
-#define GEMV_NG 2
-#endif
+// row groups (of 32 weight rows) per k_gemv wavefront: two in grouped
+// launches (records shared by more rows), one in single and set launches,
+// which are short of workgroups at decode sizes (twice the wavefronts, each
+// with half the weight stream, halve their latency)
+RW_HD constexpr int gemv_ng(bool grouped) { return grouped ? 2 : 1; }
+constexpr int GEMV_NG_MAX = 2;
 #ifndef GEMV_WPE
 #define GEMV_WPE 4
 #endif
 
-// One octet of a wavefront's GEMV_NG row groups, as loaded: quants (8
-// bytes, Q8_0 16, per lane and block), scales, mins and (Q5) high-bit words.
-template <int DT>
+// One octet of a wavefront's NG row groups, as loaded: quants (8 bytes,
+// Q8_0 16, per lane and block), scales, mins and (Q5) high-bit words.
+template <int DT, int NG>
 struct GemvOct {
-  std::conditional_t<DT == 8, uint4, uint2> q[GEMV_NG][8];
-  uint4 d[GEMV_NG], m[GEMV_NG], h0[GEMV_NG], h1[GEMV_NG];
+  std::conditional_t<DT == 8, uint4, uint2> q[NG][8];
+  uint4 d[NG], m[NG], h0[NG], h1[NG];
 };
 
 // (every weight byte is read once per launch: streaming loads)
-template <int DT>
+template <int DT, int NG>
 __device__ inline void gemv_load_oct(const WeightView &w, int gw, int o, __amdgpu_buffer_rsrc_t rq,
                                      __amdgpu_buffer_rsrc_t rd, __amdgpu_buffer_rsrc_t rm,
                                      __amdgpu_buffer_rsrc_t rh, uint32_t vq, uint32_t vs, uint32_t vh,
-                                     GemvOct<DT> &x) {
+                                     GemvOct<DT, NG> &x) {
   constexpr int QB = DT == 8 ? 32 : 16;
 #pragma unroll
-  for (int j = 0; j < GEMV_NG; ++j) {
+  for (int j = 0; j < NG; ++j) {
     const int g = min(gw + j, w.ngroups - 1);
     const uint32_t sq = (uint32_t)(g * w.nb_pad + o * OCT) * (RG * QB);
     const uint32_t ss = (uint32_t)(g * w.noct + o) * (RG * 16);
@@ -919,9 +921,9 @@ __device__ inline void gemv_load_oct(const WeightView &w, int gw, int o, __amdgp
 // v_mfma_i32_32x32x32_i8 (exact sums S of weight rows x activation rows),
 // then acc += (d_a*d_b) * S and accm += m_b * (d_a*sum(q_a)) for the
 // activation rows 4h..4h+3 this lane holds.  `orec` = the octet's records.
-template <int DT, int MR>
-__device__ inline void gemv_fold_oct(const uint8_t *orec, int a_off, int h, int rot, const GemvOct<DT> &x,
-                                     float (&acc)[GEMV_NG][4], float (&accm)[GEMV_NG][4]) {
+template <int DT, int MR, int NG>
+__device__ inline void gemv_fold_oct(const uint8_t *orec, int a_off, int h, int rot, const GemvOct<DT, NG> &x,
+                                     float (&acc)[NG][4], float (&accm)[NG][4]) {
   constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR, SO = ZO + 16, DO = SO + 32, PO = DO + 32;
   constexpr int OFF = DT == 2 ? 8 : DT == 6 ? 16 : 0;
 #pragma unroll
@@ -935,7 +937,7 @@ __device__ inline void gemv_fold_oct(const uint8_t *orec, int a_off, int h, int 
     float4 pa = make_float4(0.f, 0.f, 0.f, 0.f);
     if (has_min(DT)) pa = *reinterpret_cast<const float4 *>(rec + PO + 16 * h);
 #pragma unroll
-    for (int j = 0; j < GEMV_NG; ++j) {
+    for (int j = 0; j < NG; ++j) {
       v4i bop;
       if constexpr (DT == 8) {
         const uint4 v = x.q[j][b8];
@@ -1003,17 +1005,17 @@ __device__ inline void gemv_fold_oct(const uint8_t *orec, int a_off, int h, int 
 // the tile started); otherwise the bias is loaded here.  Every value the
 // epilogue reads is requested before any store, so it costs one memory
 // round trip at most.
-template <bool PRE>
-__device__ inline void gemv_epilogue(const GemvItem &I, int gw, int h, int r, int mr,
-                                     const float (&y)[GEMV_NG][4], const float (&bv_in)[GEMV_NG]) {
+template <bool PRE, int NG>
+__device__ inline void gemv_epilogue(const GemvItem &I, int gw, int h, int r, int mr, const float (&y)[NG][4],
+                                     const float (&bv_in)[NG]) {
   const int n = I.n;
-  float bv[GEMV_NG], x[GEMV_NG][4];
+  float bv[NG], x[NG][4];
 #pragma unroll
-  for (int j = 0; j < GEMV_NG; ++j)
+  for (int j = 0; j < NG; ++j)
     bv[j] = PRE ? bv_in[j] : I.bias ? ldg_f(I.bias + min((gw + j) * RG + r, n - 1)) : 0.0f;
   if (I.flags & 2) {
 #pragma unroll
-    for (int j = 0; j < GEMV_NG; ++j) {
+    for (int j = 0; j < NG; ++j) {
       const int col = (gw + j) * RG + r;
 #pragma unroll
       for (int v = 0; v < 4; ++v)
@@ -1022,7 +1024,7 @@ __device__ inline void gemv_epilogue(const GemvItem &I, int gw, int h, int r, in
     }
   }
 #pragma unroll
-  for (int j = 0; j < GEMV_NG; ++j) {
+  for (int j = 0; j < NG; ++j) {
     const int col = (gw + j) * RG + r;
     if (gw + j < I.w.ngroups && col < n)
 #pragma unroll
@@ -1051,14 +1053,15 @@ template <int DT, int MR, bool GROUPED, int PD>
 __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I, int2 wt, int cap_oct,
                                                                 uint8_t *lds) {
   constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR;
-  constexpr int QB = DT == 8 ? 32 : 16;                // qs bytes per row-block
+  constexpr int QB = DT == 8 ? 32 : 16;  // qs bytes per row-block
+  constexpr int NG = gemv_ng(GROUPED);
   const WeightView &w = I.w;
   const int nb = w.nb;
   const int lks = I.lks, KS = 1 << lks;
   const int t = threadIdx.x, l = t & 63, h = l >> 5, r = l & 31;
   const int wv = __builtin_amdgcn_readfirstlane(t >> 6);  // wave-uniform: scalar offsets, uniform loops
   const int set = wv >> lks, part = wv & (KS - 1);
-  const int gw = (wt.y * (4 >> lks) + set) * GEMV_NG;  // first row group
+  const int gw = (wt.y * (4 >> lks) + set) * NG;  // first row group
   const int o0 = (w.noct * part) >> lks, o1 = (w.noct * (part + 1)) >> lks;
 
   // plane buffers (the upload keeps every plane below 4 GiB) and this lane's
@@ -1073,9 +1076,9 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
   const int a_off = r < MR ? 32 * r + 16 * h : ZO;
   const int rot = (32 - 2 * h) & 31;  // rotr by this = rotl by 2h
 
-  float acc[GEMV_NG][4], accm[GEMV_NG][4];
+  float acc[NG][4], accm[NG][4];
 #pragma unroll
-  for (int j = 0; j < GEMV_NG; ++j)
+  for (int j = 0; j < NG; ++j)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       acc[j][v] = 0.0f;
@@ -1090,19 +1093,19 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
   // always can; fills can for Q4_0, and for Q4_1 and Q5_0 at one row (the
   // other forms would spill)
   constexpr bool EARLY = PD > 1 || GROUPED || DT == 2 || (MR == 1 && (DT == 3 || DT == 6));
-  GemvOct<DT> ring[PD];
-  GemvOct<DT> &cur = ring[0];
+  GemvOct<DT, NG> ring[PD];
+  GemvOct<DT, NG> &cur = ring[0];
   if (EARLY) {
 #pragma unroll
     for (int u = 0; u < PD; ++u)
-      if (o0 + u < min(o1, o0 + ch)) gemv_load_oct<DT>(w, gw, o0 + u, rq, rd, rm, rh, vq, vs, vh, ring[u]);
+      if (o0 + u < min(o1, o0 + ch)) gemv_load_oct<DT, NG>(w, gw, o0 + u, rq, rd, rm, rh, vq, vs, vh, ring[u]);
   }
   // grouped launches: this lane's columns' bias, in flight with the first
   // octet (the others, and Q5_1, load it in the epilogue: registers)
   constexpr bool PRE = GROUPED && DT != 7;
-  float bv[GEMV_NG];
+  float bv[NG];
 #pragma unroll
-  for (int j = 0; j < GEMV_NG; ++j)
+  for (int j = 0; j < NG; ++j)
     bv[j] = PRE && I.bias && part == 0 ? ldg_f(I.bias + min((gw + j) * RG + r, I.n - 1)) : 0.0f;
 
   // layernorm statistics of the m activation rows (single / set launches
@@ -1176,7 +1179,7 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
   for (int cc = 0; cc < span; cc += ch) {
     // this part's octets in the chunk
     const int p0 = o0 + cc, p1 = min(o1, p0 + ch);
-    if (EARLY && cc && p0 < p1) gemv_load_oct<DT>(w, gw, p0, rq, rd, rm, rh, vq, vs, vh, cur);
+    if (EARLY && cc && p0 < p1) gemv_load_oct<DT, NG>(w, gw, p0, rq, rd, rm, rh, vq, vs, vh, cur);
     if (cc) __syncthreads();  // every wavefront is done with the previous chunk
     for (int pp = 0; pp < KS; ++pp) {
       const int c0 = ((w.noct * pp) >> lks) + cc, c1 = min((w.noct * (pp + 1)) >> lks, c0 + ch);
@@ -1211,48 +1214,48 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
 #pragma unroll
           for (int u = 0; u < PD; ++u)
             if (o + u < p1) {
-              gemv_fold_oct<DT, MR>(lds + (part * ch + o + u - p0) * OCT * REC, a_off, h, rot, ring[u], acc, accm);
-              if (o + u + PD < p1) gemv_load_oct<DT>(w, gw, o + u + PD, rq, rd, rm, rh, vq, vs, vh, ring[u]);
+              gemv_fold_oct<DT, MR, NG>(lds + (part * ch + o + u - p0) * OCT * REC, a_off, h, rot, ring[u], acc, accm);
+              if (o + u + PD < p1) gemv_load_oct<DT, NG>(w, gw, o + u + PD, rq, rd, rm, rh, vq, vs, vh, ring[u]);
             }
         }
       } else {
-        if (!EARLY) gemv_load_oct<DT>(w, gw, p0, rq, rd, rm, rh, vq, vs, vh, cur);
-        gemv_fold_oct<DT, MR>(lds + part * ch * OCT * REC, a_off, h, rot, cur, acc, accm);
+        if (!EARLY) gemv_load_oct<DT, NG>(w, gw, p0, rq, rd, rm, rh, vq, vs, vh, cur);
+        gemv_fold_oct<DT, MR, NG>(lds + part * ch * OCT * REC, a_off, h, rot, cur, acc, accm);
         for (int o = p0 + 1; o < p1; ++o) {
-          gemv_load_oct<DT>(w, gw, o, rq, rd, rm, rh, vq, vs, vh, cur);
-          gemv_fold_oct<DT, MR>(lds + (part * ch + o - p0) * OCT * REC, a_off, h, rot, cur, acc, accm);
+          gemv_load_oct<DT, NG>(w, gw, o, rq, rd, rm, rh, vq, vs, vh, cur);
+          gemv_fold_oct<DT, MR, NG>(lds + (part * ch + o - p0) * OCT * REC, a_off, h, rot, cur, acc, accm);
         }
       }
     }
   }
 
-  float y[GEMV_NG][4];
+  float y[NG][4];
 #pragma unroll
-  for (int j = 0; j < GEMV_NG; ++j)
+  for (int j = 0; j < NG; ++j)
 #pragma unroll
     for (int v = 0; v < 4; ++v) y[j][v] = has_min(DT) ? acc[j][v] + accm[j][v] : acc[j][v];
 
   if (KS == 1) {
-    gemv_epilogue<PRE>(I, gw, h, r, MR, y, bv);
+    gemv_epilogue<PRE, NG>(I, gw, h, r, MR, y, bv);
     return;
   }
   __syncthreads();  // the activation LDS is reused for the partial sums
-  float *red = reinterpret_cast<float *>(lds);  // [4 wavefronts][GEMV_NG groups x 4][64]
+  float *red = reinterpret_cast<float *>(lds);  // [4 wavefronts][NG groups x 4][64]
 #pragma unroll
-  for (int j = 0; j < GEMV_NG; ++j)
+  for (int j = 0; j < NG; ++j)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) red[(wv * 4 * GEMV_NG + 4 * j + v) * 64 + l] = y[j][v];
+    for (int v = 0; v < 4; ++v) red[(wv * 4 * NG + 4 * j + v) * 64 + l] = y[j][v];
   __syncthreads();
   if (part == 0) {
 #pragma unroll
-    for (int j = 0; j < GEMV_NG; ++j)
+    for (int j = 0; j < NG; ++j)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        float tt = red[(wv * 4 * GEMV_NG + 4 * j + v) * 64 + l];
-        for (int p = 1; p < KS; ++p) tt = tt + red[((wv + p) * 4 * GEMV_NG + 4 * j + v) * 64 + l];
+        float tt = red[(wv * 4 * NG + 4 * j + v) * 64 + l];
+        for (int p = 1; p < KS; ++p) tt = tt + red[((wv + p) * 4 * NG + 4 * j + v) * 64 + l];
         y[j][v] = tt;
       }
-    gemv_epilogue<PRE>(I, gw, h, r, MR, y, bv);
+    gemv_epilogue<PRE, NG>(I, gw, h, r, MR, y, bv);
   }
 }
 
@@ -1289,7 +1292,7 @@ __global__ __launch_bounds__(256, PD > 1 ? 1 : GEMV_WPE) void k_gemv(const GemvI
 // LDS bytes k_gemv needs for m rows and cap_oct octets of records
 RW_HD inline size_t gemv_lds_bytes(int m, int cap_oct) {
   const size_t act = (size_t)cap_oct * OCT * gemv_rec_bytes(m);
-  const size_t red = (size_t)4 * 4 * GEMV_NG * 64 * 4;
+  const size_t red = (size_t)4 * 4 * GEMV_NG_MAX * 64 * 4;
   return act > red ? act : red;
 }
 

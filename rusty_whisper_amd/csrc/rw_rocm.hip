@@ -447,16 +447,24 @@ static int run_gemm(const rw_weight *const *w, const float *const *bias, float *
 // The split of a row's octets over wavefronts depends on the weight and the
 // launch form only.  Grouped launches have workgroups to spare and split
 // while every wavefront keeps at least 4 octets; a single linear's launch
-// is short of workgroups at decode sizes (5 for a 1280-row weight) and
-// splits while every wavefront keeps 2, which halves its latency.  The two
-// forms then differ only by the f32 reassociation of the parts' sums.
+// is short of workgroups at decode sizes and splits while every wavefront
+// keeps 2, which halves its latency.  The two forms then differ only by the
+// f32 reassociation of the parts' sums.  Single and set launches also give
+// each wavefront one row group instead of two (gemv_ng): a 1280-row weight
+// at k = 1280 runs on 20 workgroups instead of 10 (decoder step 3.61 ->
+// 2.96 ms per token).
+#ifndef GEMV_SINGLE_KEEP
+#define GEMV_SINGLE_KEEP 2
+#endif
 static int gemv_ks(const rw_weight *w, bool single = false) {
-  const int keep = single ? 2 : 4;
+  const int keep = single ? GEMV_SINGLE_KEEP : 4;
   int ks = 1;
   while (ks < 4 && w->noct / (2 * ks) >= keep) ks *= 2;
   return ks;
 }
-static int gemv_wgs(const rw_weight *w, int ks) { return (int)cdiv(w->ngroups, GEMV_NG * (4 / ks)); }
+static int gemv_wgs(const rw_weight *w, int ks, bool grouped) {
+  return (int)cdiv(w->ngroups, gemv_ng(grouped) * (4 / ks));
+}
 
 // LDS per workgroup is held to GEMV_LDS_CAP bytes: activation records go
 // through LDS in chunks (the arithmetic does not depend on them).  A weight
@@ -556,7 +564,7 @@ static int run_product(const rw_weight *w, size_t m, const float *bias, float *o
     one.it[0].qpa = av.pa;
     one.it[0].qsa = av.sa;
     one.count = 1;
-    one.end[0] = gemv_wgs(w, gemv_ks(w, true));
+    one.end[0] = gemv_wgs(w, gemv_ks(w, true), false);
     RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, one.end[0], gemv_cap((int)m, gemv_need(w, true)), s);
     LAUNCH_TRY("k_gemv");
   } else {
@@ -574,7 +582,7 @@ static int run_matmul(const rw_weight *w, const float *a, size_t m, const float 
     GemvSet one{};
     one.it[0] = gemv_item(w, a, bias, out, true);
     one.count = 1;
-    one.end[0] = gemv_wgs(w, gemv_ks(w, true));
+    one.end[0] = gemv_wgs(w, gemv_ks(w, true), false);
     RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, one.end[0], gemv_cap((int)m, gemv_need(w, true)), s);
     LAUNCH_TRY("k_gemv");
     return RW_OK;
@@ -614,7 +622,7 @@ static int run_matmul_set(const rw_weight *const *w, size_t count, const float *
       set.it[i].lnw = lnw;
       set.it[i].lnb = lnb;
       set.it[i].flags = flags;
-      wgs += gemv_wgs(w[i], gemv_ks(w[i], true));
+      wgs += gemv_wgs(w[i], gemv_ks(w[i], true), false);
       set.end[i] = wgs;
       need = std::max(need, gemv_need(w[i], true));
     }
@@ -720,7 +728,7 @@ static GroupPlan group_plan(const rw_linear *items, size_t count) {
     for (size_t j = j0; j < j1; ++j) {
       const rw_weight *w = items[P.order[j]].w;
       const int m = (int)items[P.order[j]].m;
-      const int x0 = place_runs((int)j, gemv_wgs(w, gemv_ks(w)), pos, slots);
+      const int x0 = place_runs((int)j, gemv_wgs(w, gemv_ks(w), true), pos, slots);
       place_runs((int)j, (int)cdiv((size_t)m * w->noct * OCT, 32), qpos, qslots, x0);
       P.rec_off[j] = rec;
       rec += align_up((size_t)w->noct * OCT * gemv_rec_bytes(m), 256);
