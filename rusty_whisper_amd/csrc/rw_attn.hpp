@@ -40,7 +40,10 @@ constexpr int ATT_DH = 64;   // head size (every whisper model)
 constexpr int ATT_KVB = 32;  // kv rows per block
 constexpr int ATT_QT = 2;    // 32-query tiles per workgroup
 constexpr int ATT_QB = 32 * ATT_QT;
-constexpr int ATT_MAX_SPLIT = 16;  // kv runs of one (query block, head) at most
+#ifndef ATT_MAX_SPLIT_N
+#define ATT_MAX_SPLIT_N 32
+#endif
+constexpr int ATT_MAX_SPLIT = ATT_MAX_SPLIT_N;  // kv runs of one (query block, head) at most
 
 // kv index (within a 16-block) stored at position p of the v^T plane: the
 // middle quads swap (an involution)

@@ -498,9 +498,14 @@ static GemvItem gemv_item(const rw_weight *w, const float *a, const float *bias,
 
 // A single or set launch of at most one wavefront per SIMD whose records fit
 // LDS at once takes k_gemv's latency form: every wavefront keeps up to
-// GEMV_PD weight octets in flight (it has the registers of a whole SIMD; a
-// third octet measured slower).
-constexpr int GEMV_PD = 2;
+// GEMV_PD weight octets in flight (it has the registers of a whole SIMD).
+// With one row group per wavefront three octets fit without spilling and
+// cover a 1280-wide row's larger part (2 + 3 octets) in one round trip; a
+// fourth measured no better.
+#ifndef GEMV_PD_LAT
+#define GEMV_PD_LAT 3
+#endif
+constexpr int GEMV_PD = GEMV_PD_LAT;
 constexpr int GEMV_LAT_WGS = 256;  // 4 wavefronts each: one per SIMD of 256 CUs
 static bool gemv_latency_form(const GemvSet &one, int wgs, int cap_oct) {
   if (wgs > GEMV_LAT_WGS) return false;
@@ -861,9 +866,16 @@ struct AttnLayout {
 };
 
 // few (query block, head) workgroups -- a decoding step: split the kv
-// blocks over up to ATT_MAX_SPLIT workgroups each, merged by k_attn_combine
+// blocks over up to ATT_MAX_SPLIT workgroups each (down to one 32-row block
+// per run: each run is then one short chain of loads; the decoder step's
+// cross-attention, 47 blocks per head, runs 26 splits instead of 11: 2% per
+// token, 3% at 440 cached rows), merged by k_attn_combine
+#ifndef ATT_SPLIT_MINBLK
+#define ATT_SPLIT_MINBLK 1
+#endif
 static int attn_nsplit(size_t groups, size_t nblk) {
-  if (groups < 256 && nblk >= 8) return (int)std::min<size_t>(ATT_MAX_SPLIT, std::min(nblk / 4, cdiv(512, groups)));
+  if (groups < 256 && nblk >= 8)
+    return (int)std::min<size_t>(ATT_MAX_SPLIT, std::min<size_t>(nblk / ATT_SPLIT_MINBLK, cdiv(512, groups)));
   return 1;
 }
 
