@@ -695,6 +695,21 @@ def leg_turbo_decoder(A, synth, torch, layers_w, steps: int, seed0: int):
     ms_step = time_graph(torch, step, steps, 2)
     ops_step = sum(2 * m * w.n * w.k for w in ws_)
     wbytes = sum(w.n * (w.k // 32) * synth.BLOCK_BYTES[dtype] for w in ws_)
+    # the prompt's prefill: the same per-layer linears at M = 224 prompt rows
+    # (no logits; src/transcribe.rs:540-561 runs prompts of up to 224 tokens)
+    mp = 224
+    lin = ws_[:-1]
+    ins_p = [torch.randn(mp, w.k, device=dev, generator=g) for w in lin]
+    outs_p = [torch.empty(mp, w.n, device=dev) for w in lin]
+    wk_p = {k: (A.workspace_size(mp, k), torch.empty(A.workspace_size(mp, k), dtype=torch.uint8, device=dev))
+            for k in (d, fc)}
+
+    def prefill(st):
+        for w, a, o, b in zip(lin, ins_p, outs_p, bs):
+            w.matmul_dev(a, mp, o, b, wk_p[w.k][1], wk_p[w.k][0], st)
+
+    ms_pre = time_graph(torch, prefill, steps, 2)
+    ops_pre = sum(2 * mp * w.n * w.k for w in lin)
     for w in ws_:
         w.free()
     return {
@@ -708,6 +723,10 @@ def leg_turbo_decoder(A, synth, torch, layers_w, steps: int, seed0: int):
                      "value": round(ops_step / (ms_step * 1e-3) / 1e12, 3), "unit": "TOPS",
                      "ms": round(ms_step, 4),
                      "weight_GB_per_s": round(wbytes / (ms_step * 1e-3) / 1e9, 1)},
+        "prefill_m224": {"workload": "prompt prefill at M=224: 4 layers x (self q,k,v,out, cross q,out, fc1, fc2), "
+                                     "Q5_1, each a quantization and a GEMM launch",
+                         "value": round(ops_pre / (ms_pre * 1e-3) / 1e12, 3), "unit": "TOPS",
+                         "ms": round(ms_pre, 4)},
     }
 
 
@@ -883,8 +902,10 @@ def main() -> int:
         t = leg_turbo_decoder(A, synth, torch, W["layers"], steps, 6)
         legs["c5_turbo_cross_kv_m12000_q5_1"] = t["cross_kv"]
         legs["c5_turbo_decoder_m40_q5_1"] = t["step_m40"]
+        legs["c5_turbo_prefill_m224_q5_1"] = t["prefill_m224"]
         log(f"turbo cross K/V {t['cross_kv']['ms']} ms ({t['cross_kv']['value']} TOPS); M=40 step "
-            f"{t['step_m40']['ms']} ms ({t['step_m40']['value']} TOPS)")
+            f"{t['step_m40']['ms']} ms ({t['step_m40']['value']} TOPS); prefill M=224 "
+            f"{t['prefill_m224']['ms']} ms ({t['prefill_m224']['value']} TOPS)")
         torch.cuda.empty_cache()
 
     del W

@@ -376,10 +376,19 @@ static void launch_gemm_tm(const GemmSet &set, size_t tiles, const ActView &av, 
 
 // A single-wavefront launch whose 128-row tiles leave SIMDs idle takes
 // 96-row tiles when those still fit one wavefront per SIMD (q/k/v of a
-// 1500-row input: 720 wavefronts of 128 rows, or 960 of 96, on 1024 SIMDs)
+// 1500-row input: 720 wavefronts of 128 rows, or 960 of 96, on 1024 SIMDs).
+// A launch that 128-row tiles would give fewer than GEMM_TM2_BELOW
+// wavefronts (a skinny input: a 224-row prompt's products run 120-160)
+// takes 64-row tiles, twice the wavefronts (the 32 large-v3 layers'
+// linears at M = 200: 2.94 -> 2.43 ms).  Tile rows change which rows share
+// a workgroup, not how a row is summed.
 constexpr size_t GEMM_SIMDS = 1024;
+#ifndef GEMM_TM2_BELOW
+#define GEMM_TM2_BELOW 512
+#endif
 static int gemm_rows(int kw, size_t tiles, int mgroups) {
   if (mgroups <= 2) return 2;
+  if (cdiv(mgroups, 4) * tiles * kw < GEMM_TM2_BELOW) return 2;
   if (kw == 1 && cdiv(mgroups, 3) * tiles <= GEMM_SIMDS && cdiv(mgroups, 4) * tiles < cdiv(mgroups, 3) * tiles)
     return 3;
   return 4;
