@@ -1392,8 +1392,9 @@ struct GemmSet {
 // A launch covers up to GEMM_MAX_SET weights that share the activation (the
 // column tiles of the launch run through the weights in turn).  A
 // workgroup owns one tile of TM activation row groups x TN weight row
-// groups (32 TM x 64; TM = 4, or 2 for inputs of at most 64 rows) and has
-// KW wavefronts, each taking every KW-th block
+// groups (32 TM x 32 TN; TM = 4, 3 or 2, TN = 2, or 1 for skinny inputs,
+// whose launches are short of wavefronts) and has KW wavefronts, each
+// taking every KW-th block
 // (block kw, kw + KW, ...).  A wavefront loads its operands straight into
 // registers, P blocks ahead, and needs no other wavefront until the end: no
 // LDS and no barrier in the k loop.  Each step issues the loads of block
@@ -1403,9 +1404,9 @@ struct GemmSet {
 // 32 x 32 output tiles dealt to the wavefronts in turn.  KW comes from the
 // weights' shapes alone and TM changes which rows share a workgroup, not
 // how a row is summed, so a row's result never depends on m.
-template <int DT, int KW, int TM, bool OFFS>
+template <int DT, int KW, int TM, bool OFFS, int TN = GEMM_TN>
 __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int m) {
-  constexpr int TN = GEMM_TN, P = GEMM_P, S = P + 1;
+  constexpr int P = GEMM_P, S = P + 1;
   constexpr int RED = KW > 1 ? KW * TM * TN * 16 * 64 * 4 : 16;
   __shared__ __align__(16) uint8_t lds[RED];
   const int l = threadIdx.x & 63;

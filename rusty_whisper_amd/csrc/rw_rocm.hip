@@ -368,10 +368,29 @@ static int gemm_kw(size_t tiles, int nb) {
 // Row groups per workgroup: 4, or 2 for inputs of at most 64 rows (so a
 // skinny input does not run MFMAs on repeated rows).  OFFS: some weight of
 // the launch has offset rows (the epilogue's extra term and loads).
-template <int DT, int KW, int TM, bool OFFS>
+template <int DT, int KW, int TM, bool OFFS, int TN = GEMM_TN>
 static void launch_gemm_tm(const GemmSet &set, size_t tiles, const ActView &av, int m, hipStream_t s) {
   dim3 grid((unsigned)tiles, (unsigned)cdiv(av.mgroups, TM));
-  hipLaunchKernelGGL((k_gemm<DT, KW, TM, OFFS>), grid, dim3(64 * KW), 0, s, set, av, m);
+  hipLaunchKernelGGL((k_gemm<DT, KW, TM, OFFS, TN>), grid, dim3(64 * KW), 0, s, set, av, m);
+}
+
+// A skinny launch (64-row tiles that still give fewer than GEMM_TN1_BELOW
+// wavefronts: the M = 40 decoder products run 60-80) takes 32-column tiles,
+// twice the wavefronts.  The launch's column tiles are recounted for one
+// weight row group each; the k split stays the one chosen from the weights.
+#ifndef GEMM_TN1_BELOW
+#define GEMM_TN1_BELOW 512
+#endif
+template <int DT, int KW, bool OFFS>
+static bool launch_gemm_narrow(GemmSet set, size_t tiles, const ActView &av, int m, hipStream_t s) {
+  if (cdiv(av.mgroups, 2) * tiles * KW >= GEMM_TN1_BELOW) return false;
+  size_t t1 = 0;
+  for (int i = 0; i < set.count; ++i) {
+    set.it[i].tile0 = (int)t1;
+    t1 += (size_t)set.it[i].ngroups;
+  }
+  launch_gemm_tm<DT, KW, 2, OFFS, 1>(set, t1, av, m, s);
+  return true;
 }
 
 // A single-wavefront launch whose 128-row tiles leave SIMDs idle takes
@@ -399,6 +418,9 @@ static void launch_gemm_kw(const GemmSet &set, size_t tiles, const ActView &av, 
   bool offs = false;
   for (int i = 0; i < set.count; ++i) offs = offs || set.it[i].gp.cm != nullptr;
   const int tm = gemm_rows(KW, tiles, av.mgroups);
+  if (tm == 2 && (offs ? launch_gemm_narrow<DT, KW, true>(set, tiles, av, m, s)
+                      : launch_gemm_narrow<DT, KW, false>(set, tiles, av, m, s)))
+    return;
   if (offs) {
     if (tm == 2) launch_gemm_tm<DT, KW, 2, true>(set, tiles, av, m, s);
     else if (KW == 1 && tm == 3) launch_gemm_tm<DT, 1, 3, true>(set, tiles, av, m, s);
