@@ -289,6 +289,69 @@ __device__ inline void att_load_v(const AttnPlanes &P, int head, int blk, int h,
   }
 }
 
+// The same K and v^T operands straight from f32 rows (kf, vf with row
+// strides ldk, ldv; rows >= t_kv are zeros), for calls that do not split K
+// and V into planes first: the loads (raw) and the split (att_split, the
+// values k_attn_split stores) are separate, so the loads can run ahead.
+struct AttKRaw {
+  float4 x[4][2];
+};
+struct AttVRaw {
+  float x[2][2][8];
+};
+__device__ inline void att_load_k_raw(const float *kf, int ldk, int t_kv, int head, int blk, int h, int n,
+                                      AttKRaw &o) {
+  // lane (h, n): kv row 32 blk + n, values 8h + 16s .. + 7
+  const float *src = kf + (size_t)min(blk * ATT_KVB + n, t_kv - 1) * ldk + head * ATT_DH + 8 * h;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    o.x[s][0] = *reinterpret_cast<const float4 *>(src + 16 * s);
+    o.x[s][1] = *reinterpret_cast<const float4 *>(src + 16 * s + 4);
+  }
+}
+__device__ inline void att_split_k(const AttKRaw &x, bool live, AttK &o) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const float v[8] = {x.x[s][0].x, x.x[s][0].y, x.x[s][0].z, x.x[s][0].w,
+                        x.x[s][1].x, x.x[s][1].y, x.x[s][1].z, x.x[s][1].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      uint16_t hb, lb;
+      att_split(live ? v[e] : 0.0f, hb, lb);
+      o.kh[s][e] = __builtin_bit_cast(_Float16, hb);
+      o.kl[s][e] = __builtin_bit_cast(_Float16, lb);
+    }
+  }
+}
+__device__ inline void att_load_v_raw(const float *vf, int ldv, int t_kv, int head, int blk, int h, int n,
+                                      AttVRaw &o) {
+  // lane (h, n): value d = 32 dt + n of the kv rows that the v^T plane keeps
+  // at positions 32 blk + 16 s + 8 h + e (attn_vpos order within 16)
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int kv = blk * ATT_KVB + 16 * s + attn_vpos(8 * h + e);
+        const float x = vf[(size_t)min(kv, t_kv - 1) * ldv + head * ATT_DH + dt * 32 + n];
+        o.x[dt][s][e] = kv < t_kv ? x : 0.0f;
+      }
+}
+__device__ inline void att_split_v(const AttVRaw &x, AttV &o) {
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        uint16_t hb, lb;
+        att_split(x.x[dt][s][e], hb, lb);
+        o.vh[dt][s][e] = __builtin_bit_cast(_Float16, hb);
+        o.vl[dt][s][e] = __builtin_bit_cast(_Float16, lb);
+      }
+}
+
 // Workgroup (blockIdx.x, blockIdx.y) = (ATT_QB query rows from q0, head).
 // Wavefront w takes kv blocks w, w + 2, ...; a causal query row i (at
 // absolute position t_kv - t_q + i) sees kv rows up to its position.
@@ -301,10 +364,15 @@ __device__ inline void att_load_v(const AttnPlanes &P, int head, int blk, int h,
 // With qf != NULL the queries come as f32 rows (qf, ldq) and are scaled and
 // split here, exactly as k_attn_split would store them (P.qh, P.ql unused):
 // the decoder's cross-attention, whose K and v^T planes are kept, then needs
-// no split launch.
+// no split launch.  ROWS: K and V come as f32 rows too (kf, vf) and are split
+// here as well (the P planes are unused): calls of one query block (a
+// decoding step's self-attention over its cache) then need no split launch;
+// the operands are the planes' values, so the results are the same bits.
+template <bool ROWS>
 __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, int causal,
                                               float *__restrict__ out, int ld_out, float *__restrict__ part,
-                                              const float *__restrict__ qf, int ldq) {
+                                              const float *__restrict__ qf, int ldq, const float *__restrict__ kf,
+                                              int ldk, const float *__restrict__ vf, int ldv) {
   constexpr float LOG2E = 1.4426950408889634f;
   constexpr float NEG_INF = -__builtin_huge_valf();
   __shared__ __align__(16) float xo[ATT_QB * (ATT_DH + 4)];  // partial O^T exchange, then the output tile
@@ -375,10 +443,21 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
   // after the scores and the softmax
   AttK cur, nxt;
   AttV vb;
-  if (b_begin + wv < nblk) att_load_k(P, head, b_begin + wv, h, n, cur);
+  AttKRaw kr_cur, kr_nxt;  // ROWS: f32 K rows, split when their block comes
+  AttVRaw vr;
+  if (b_begin + wv < nblk) {
+    if constexpr (ROWS) att_load_k_raw(kf, ldk, t_kv, head, b_begin + wv, h, n, kr_cur);
+    else att_load_k(P, head, b_begin + wv, h, n, cur);
+  }
   for (int b = b_begin + wv; b < nblk; b += 2) {
-    att_load_v(P, head, b, h, n, vb);
-    if (b + 2 < nblk) att_load_k(P, head, b + 2, h, n, nxt);
+    if constexpr (ROWS) {
+      att_load_v_raw(vf, ldv, t_kv, head, b, h, n, vr);
+      if (b + 2 < nblk) att_load_k_raw(kf, ldk, t_kv, head, b + 2, h, n, kr_nxt);
+      att_split_k(kr_cur, b * ATT_KVB + n < t_kv, cur);
+    } else {
+      att_load_v(P, head, b, h, n, vb);
+      if (b + 2 < nblk) att_load_k(P, head, b + 2, h, n, nxt);
+    }
     // both query tiles' scores first, so the softmax of one tile can run on
     // the VALU while the matrix cores work on the other
     att_v16f s[ATT_QT];
@@ -388,6 +467,7 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
 #pragma unroll
       for (int k = 0; k < 4; ++k) att_mma3(cur.kh[k], cur.kl[k], qh[qt][k], ql[qt][k], s[qt]);
     }
+    if constexpr (ROWS) att_split_v(vr, vb);
 #pragma unroll
     for (int qt = 0; qt < ATT_QT; ++qt) {
       // lane (h, n): s[qt][i] = score of query q0 + 32 qt + n against kv
@@ -436,7 +516,8 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
 #pragma unroll
         for (int k = 0; k < 2; ++k) att_mma3(vb.vh[dt][k], vb.vl[dt][k], ph[k], pl[k], o[qt][dt]);
     }
-    cur = nxt;
+    if constexpr (ROWS) kr_cur = kr_nxt;
+    else cur = nxt;
   }
 
   // wavefront 1 hands its partial state to wavefront 0

@@ -976,7 +976,10 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
     P.kh = kv_split->kh, P.kl = kv_split->kl, P.vh = kv_split->vh, P.vl = kv_split->vl;
     P.tkv_pad = kv_split->tkv_pad;
   }
-  if (!kv_split) {  // k and v only: k_attn splits q as it loads it
+  // one query block against k and v rows (a decoding step's self-attention):
+  // k_attn splits q, K and V as it loads them
+  const bool rows = !kv_split && L.tq_pad == ATT_QB;
+  if (!kv_split && !rows) {  // k and v only: k_attn splits q as it loads it
     const size_t nk = (size_t)n_head * P.tkv_pad * 8;
     const int wk = (int)cdiv(nk, 256);
     const int wv = n_head * (int)cdiv(P.tkv_pad, ATT_VT_KV);  // v^T: one workgroup per (head, 64 positions)
@@ -988,8 +991,13 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
   // with the kv length, so this one fits the layout's part buffer)
   const int nsplit = std::min(L.nsplit, attn_nsplit((size_t)(L.tq_pad / ATT_QB) * n_head, cdiv(t_kv, ATT_KVB)));
   float *part = nsplit > 1 ? (float *)(b + L.off_part) : nullptr;
-  hipLaunchKernelGGL(k_attn, dim3((unsigned)(L.tq_pad / ATT_QB), (unsigned)n_head, (unsigned)nsplit), dim3(128), 0, s,
-                     P, (int)t_q, (int)t_kv, causal ? 1 : 0, out, (int)ldo, part, q, (int)ldq);
+  if (rows)
+    hipLaunchKernelGGL(k_attn<true>, dim3(1, (unsigned)n_head, (unsigned)nsplit), dim3(128), 0, s, P, (int)t_q,
+                       (int)t_kv, causal ? 1 : 0, out, (int)ldo, part, q, (int)ldq, k, (int)ldk, v, (int)ldv);
+  else
+    hipLaunchKernelGGL(k_attn<false>, dim3((unsigned)(L.tq_pad / ATT_QB), (unsigned)n_head, (unsigned)nsplit),
+                       dim3(128), 0, s, P, (int)t_q, (int)t_kv, causal ? 1 : 0, out, (int)ldo, part, q, (int)ldq,
+                       nullptr, 0, nullptr, 0);
   LAUNCH_TRY("k_attn");
   if (part) {
     const size_t nz = t_q * (size_t)n_head * ATT_DH;
@@ -1113,8 +1121,8 @@ static int run_beam_self_attention(rw_decoder *const *beams, size_t nb, int l, c
   LAUNCH_TRY("k_attn_split_beams");
   const int nsplit = std::min(L.nsplit, attn_nsplit((size_t)(L.tq_pad / ATT_QB) * heads, cdiv(t_kv, ATT_KVB)));
   float *part = nsplit > 1 ? (float *)(b + L.off_part) : nullptr;
-  hipLaunchKernelGGL(k_attn, dim3((unsigned)(L.tq_pad / ATT_QB), (unsigned)heads, (unsigned)nsplit), dim3(128), 0, s,
-                     P, 1, (int)t_kv, 1, att, (int)d->n, part, nullptr, 0);
+  hipLaunchKernelGGL(k_attn<false>, dim3((unsigned)(L.tq_pad / ATT_QB), (unsigned)heads, (unsigned)nsplit), dim3(128),
+                     0, s, P, 1, (int)t_kv, 1, att, (int)d->n, part, nullptr, 0, nullptr, 0, nullptr, 0);
   LAUNCH_TRY("k_attn");
   if (part) {
     hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)cdiv((size_t)heads * ATT_DH, 256)), dim3(256), 0, s, part, nsplit,
