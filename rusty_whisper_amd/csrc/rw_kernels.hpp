@@ -758,12 +758,14 @@ __device__ inline void gemv_zero_slots(uint8_t *lds, int nslots, int t) {
 // LDS at `base`: quantized here from f32 (I.a, the arithmetic of k_quantize,
 // so fused and separate quantization agree bit for bit)
 // or copied from an already quantized workspace (I.qa).  (block, row) pairs
-// block-major, 4 passes of 32 per batch so their global loads are in flight
-// together.  Records of the tail blocks past nb are zeroed.
+// block-major, U passes of 32 per batch (4, or 8 for one row in the latency
+// form: fc2's 160 blocks in one round of loads; 5-row sets measured slower
+// with 8) so their global loads are in flight together.  Records of the
+// tail blocks past nb are zeroed.
 // With I.lnw the rows are layernormed first (mean ln[i] and inverse deviation
 // ln[GEMV_MR_MAX + i] of row i, in LDS; then (x - mean) * inv * w + b,
 // src/tensor.rs:274-287) and the result quantized.
-template <int DT, int MR>
+template <int DT, int MR, int U = 4>
 __device__ inline void gemv_fill(const GemvItem &I, int nb, int c0, int c1, uint8_t *base, int t,
                                  const float *ln) {
   constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR, SO = ZO + 16, DO = SO + 32, PO = DO + 32;
@@ -771,10 +773,11 @@ __device__ inline void gemv_fill(const GemvItem &I, int nb, int c0, int c1, uint
   const int bb0 = c0 * OCT, cnb = min(nb, c1 * OCT) - bb0;
   const int total = MR * cnb;
   if (I.a) {
-    for (int rb0 = 0; rb0 < total; rb0 += 128) {
-      float4 x[4];
+    // U loads per thread in flight per round (32 U (row, block) pairs)
+    for (int rb0 = 0; rb0 < total; rb0 += 32 * U) {
+      float4 x[U];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < U; ++u) {
         const int rb = rb0 + 32 * u + (t >> 3), lt = t & 7;
         x[u] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (rb < total) {
@@ -792,7 +795,10 @@ __device__ inline void gemv_fill(const GemvItem &I, int nb, int c0, int c1, uint
         }
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < U; ++u) {
+        // a wavefront's 8 pairs of pass u start at rb0 + 32 u + 8 (t / 64):
+        // passes wholly past the end are skipped (uniform)
+        if (U > 4 && rb0 + 32 * u + 8 * (t >> 6) >= total) continue;
         const int rb = rb0 + 32 * u + (t >> 3), lt = t & 7;
         const BlockQuant bq = quantize_block8(x[u]);
         if (rb < total) {
@@ -1146,17 +1152,48 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
         }
         return a;
       };
-      float acc_s[MR];
+      float acc_s[MR], mean[MR];
+      if (K <= 8 * 256) {
+        // one round of 8 values per thread: kept in registers for the
+        // squared deviations (the same sums, in the same order, as below)
+        float xv[MR][8];
 #pragma unroll
-      for (int i = 0; i < MR; ++i) acc_s[i] = thread_sum(I.a + (size_t)i * K, 0.0f, false);
-      row_sums(acc_s);
-      float mean[MR];
+        for (int i = 0; i < MR; ++i)
 #pragma unroll
-      for (int i = 0; i < MR; ++i) {
-        mean[i] = __fdiv_rn(acc_s[i], (float)K);
-        acc_s[i] = thread_sum(I.a + (size_t)i * K, mean[i], true);
+          for (int u = 0; u < 8; ++u) xv[i][u] = t + 256 * u < K ? I.a[(size_t)i * K + t + 256 * u] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < MR; ++i) {
+          float a = 0.0f;
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            if (t + 256 * u < K) a += xv[i][u];
+          acc_s[i] = a;
+        }
+        row_sums(acc_s);
+#pragma unroll
+        for (int i = 0; i < MR; ++i) {
+          mean[i] = __fdiv_rn(acc_s[i], (float)K);
+          float a = 0.0f;
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            if (t + 256 * u < K) {
+              const float d = xv[i][u] - mean[i];
+              a += d * d;
+            }
+          acc_s[i] = a;
+        }
+        row_sums(acc_s);
+      } else {
+#pragma unroll
+        for (int i = 0; i < MR; ++i) acc_s[i] = thread_sum(I.a + (size_t)i * K, 0.0f, false);
+        row_sums(acc_s);
+#pragma unroll
+        for (int i = 0; i < MR; ++i) {
+          mean[i] = __fdiv_rn(acc_s[i], (float)K);
+          acc_s[i] = thread_sum(I.a + (size_t)i * K, mean[i], true);
+        }
+        row_sums(acc_s);
       }
-      row_sums(acc_s);
       if (t == 0) {
 #pragma unroll
         for (int i = 0; i < MR; ++i) {
@@ -1201,7 +1238,7 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
             if (z0 + 256 * u < total) reinterpret_cast<uint4 *>(base)[z0 + 256 * u] = rv[u];
         }
       } else {
-        gemv_fill<DT, MR>(I, nb, c0, c1, base, t, ln_s);
+        gemv_fill<DT, MR, (PD > 1 && MR == 1 ? 8 : 4)>(I, nb, c0, c1, base, t, ln_s);
       }
     }
     __syncthreads();
