@@ -1905,10 +1905,23 @@ int rw_rocm_decoder_set_audio_dev(rw_decoder *d, const float *enc_out, void *str
   if (rc) return rc;
   char *b = (char *)d->scratch;
   float *kf = (float *)(b + off_k), *vf = (float *)(b + off_v);
+  // every layer's K and V read the same encoder output: it is quantized
+  // once (quantize_acts_i8 of the same rows gives the same values each
+  // time), and a layer's K and V run as one two-weight launch where their
+  // dtypes and k agree
+  const ActLayout AL = act_layout(T, n);
+  RW_TRY(launch_quantize(enc_out, T, n, AL, b + off_act, s));
   for (int l = 0; l < d->p.n_layer; ++l) {
     const rw_decoder_layer &L = d->layers[l];
-    RW_TRY(run_matmul(L.ck, enc_out, T, nullptr, kf, b + off_act, s));  // the key has no bias
-    RW_TRY(run_matmul(L.cv, enc_out, T, L.cv_b, vf, b + off_act, s));
+    if (T > (size_t)GEMV_MAX_M && L.ck->dtype == L.cv->dtype && L.ck->k == L.cv->k) {
+      const rw_weight *w2[2] = {L.ck, L.cv};
+      const float *b2[2] = {nullptr, L.cv_b};  // the key has no bias
+      float *o2[2] = {kf, vf};
+      RW_TRY(run_gemm(w2, b2, o2, 2, act_view(AL, b + off_act), (int)T, s));
+    } else {
+      RW_TRY(run_product(L.ck, T, nullptr, kf, b + off_act, s));
+      RW_TRY(run_product(L.cv, T, L.cv_b, vf, b + off_act, s));
+    }
     const AttnPlanes cp = d->cross->planes(l);
     AttnPlanes P{nullptr, nullptr, cp.kh, cp.kl, cp.vh, cp.vl, A.tq_pad, cp.tkv_pad};
     const size_t nk = (size_t)d->p.n_head * cp.tkv_pad * 8;
