@@ -1010,24 +1010,35 @@ __device__ inline void gemv_fold_oct(const uint8_t *orec, int a_off, int h, int 
 // GEMM_ACC).  With PRE, `bv` holds the lane's columns' bias (loaded when
 // the tile started); otherwise the bias is loaded here.  Every value the
 // epilogue reads is requested before any store, so it costs one memory
-// round trip at most.
-template <bool PRE, int NG>
+// round trip at most.  With PREX the residual values were loaded when the
+// tile started as well (`x_in`), so the epilogue reads nothing.
+template <int NG>
+__device__ inline void gemv_load_residual(const GemvItem &I, int gw, int h, int r, int mr, float (&x)[NG][4]) {
+  const int n = I.n;
+#pragma unroll
+  for (int j = 0; j < NG; ++j) {
+    const int col = (gw + j) * RG + r;
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+      x[j][v] = gw + j < I.w.ngroups && col < n && 4 * h + v < mr ? ldg_f(I.out + (size_t)(4 * h + v) * n + col)
+                                                                   : 0.0f;
+  }
+}
+template <bool PRE, int NG, bool PREX = false>
 __device__ inline void gemv_epilogue(const GemvItem &I, int gw, int h, int r, int mr, const float (&y)[NG][4],
-                                     const float (&bv_in)[NG]) {
+                                     const float (&bv_in)[NG], const float (&x_in)[NG][4]) {
   const int n = I.n;
   float bv[NG], x[NG][4];
 #pragma unroll
   for (int j = 0; j < NG; ++j)
     bv[j] = PRE ? bv_in[j] : I.bias ? ldg_f(I.bias + min((gw + j) * RG + r, n - 1)) : 0.0f;
-  if (I.flags & 2) {
+  if (PREX) {
 #pragma unroll
-    for (int j = 0; j < NG; ++j) {
-      const int col = (gw + j) * RG + r;
+    for (int j = 0; j < NG; ++j)
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-        x[j][v] = gw + j < I.w.ngroups && col < n && 4 * h + v < mr ? ldg_f(I.out + (size_t)(4 * h + v) * n + col)
-                                                                     : 0.0f;
-    }
+      for (int v = 0; v < 4; ++v) x[j][v] = x_in[j][v];
+  } else if (I.flags & 2) {
+    gemv_load_residual<NG>(I, gw, h, r, mr, x);
   }
 #pragma unroll
   for (int j = 0; j < NG; ++j) {
@@ -1108,11 +1119,18 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
   }
   // grouped launches: this lane's columns' bias, in flight with the first
   // octet (the others, and Q5_1, load it in the epilogue: registers)
-  constexpr bool PRE = GROUPED && DT != 7;
-  float bv[NG];
+  // The latency form (PD > 1) also requests the residual values of the
+  // epilogue here (flag 2; nothing in the launch writes them before the
+  // epilogue), so its end costs no memory round trip.
+  constexpr bool PRE = (GROUPED && DT != 7) || PD > 1, PREX = PD > 1;
+  float bv[NG], xres[NG][4];
 #pragma unroll
-  for (int j = 0; j < NG; ++j)
+  for (int j = 0; j < NG; ++j) {
     bv[j] = PRE && I.bias && part == 0 ? ldg_f(I.bias + min((gw + j) * RG + r, I.n - 1)) : 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) xres[j][v] = 0.0f;
+  }
+  if (PREX && part == 0 && (I.flags & 2)) gemv_load_residual<NG>(I, gw, h, r, MR, xres);
 
   // layernorm statistics of the m activation rows (single / set launches
   // with I.lnw): every workgroup computes them, in the same tree order, and
@@ -1273,7 +1291,7 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
     for (int v = 0; v < 4; ++v) y[j][v] = has_min(DT) ? acc[j][v] + accm[j][v] : acc[j][v];
 
   if (KS == 1) {
-    gemv_epilogue<PRE, NG>(I, gw, h, r, MR, y, bv);
+    gemv_epilogue<PRE, NG, PREX>(I, gw, h, r, MR, y, bv, xres);
     return;
   }
   __syncthreads();  // the activation LDS is reused for the partial sums
@@ -1292,7 +1310,7 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
         for (int p = 1; p < KS; ++p) tt = tt + red[((wv + p) * 4 * NG + 4 * j + v) * 64 + l];
         y[j][v] = tt;
       }
-    gemv_epilogue<PRE, NG>(I, gw, h, r, MR, y, bv);
+    gemv_epilogue<PRE, NG, PREX>(I, gw, h, r, MR, y, bv, xres);
   }
 }
 
