@@ -364,19 +364,23 @@ __device__ inline void att_split_v(const AttVRaw &x, AttV &o) {
 // With qf != NULL the queries come as f32 rows (qf, ldq) and are scaled and
 // split here, exactly as k_attn_split would store them (P.qh, P.ql unused):
 // the decoder's cross-attention, whose K and v^T planes are kept, then needs
-// no split launch.  ROWS: K and V come as f32 rows too (kf, vf) and are split
+// no split launch.  QT: 32-query tiles per workgroup (2, or 1 for calls of at
+// most 32 query rows: a decoding step then does half the products and
+// softmax work; a query row's arithmetic does not depend on QT).
+// ROWS: K and V come as f32 rows too (kf, vf) and are split
 // here as well (the P planes are unused): calls of one query block (a
 // decoding step's self-attention over its cache) then need no split launch;
 // the operands are the planes' values, so the results are the same bits.
-template <bool ROWS>
+template <bool ROWS, int QT>
 __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, int causal,
                                               float *__restrict__ out, int ld_out, float *__restrict__ part,
                                               const float *__restrict__ qf, int ldq, const float *__restrict__ kf,
                                               int ldk, const float *__restrict__ vf, int ldv) {
+  constexpr int QB = 32 * QT;  // query rows per workgroup
   constexpr float LOG2E = 1.4426950408889634f;
   constexpr float NEG_INF = -__builtin_huge_valf();
-  __shared__ __align__(16) float xo[ATT_QB * (ATT_DH + 4)];  // partial O^T exchange, then the output tile
-  __shared__ float xm[ATT_QT * 64], xl[ATT_QT * 64];
+  __shared__ __align__(16) float xo[QB * (ATT_DH + 4)];  // partial O^T exchange, then the output tile
+  __shared__ float xm[QT * 64], xl[QT * 64];
   const int l = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = l >> 5, n = l & 31;
@@ -390,18 +394,18 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
     const int per = total / 8, rem = total % 8, xcd = id % 8, slot = id / 8;
     const int lin = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
     head = lin / nqb;
-    q0 = (lin % nqb) * ATT_QB;
+    q0 = (lin % nqb) * QB;
   }
   const int off = t_kv - t_q;  // absolute position of query row 0
-  const int kv_end = causal ? min(t_kv, off + q0 + ATT_QB) : t_kv;
+  const int kv_end = causal ? min(t_kv, off + q0 + QB) : t_kv;
   const int nblk_all = (kv_end + ATT_KVB - 1) / ATT_KVB;
   const int cs = (nblk_all + gridDim.z - 1) / gridDim.z;       // blocks per split
   const int b_begin = min(nblk_all, (int)blockIdx.z * cs);
   const int nblk = min(nblk_all, b_begin + cs);               // this workgroup: blocks [b_begin, nblk)
 
-  att_v8h qh[ATT_QT][4], ql[ATT_QT][4];
+  att_v8h qh[QT][4], ql[QT][4];
 #pragma unroll
-  for (int qt = 0; qt < ATT_QT; ++qt) {
+  for (int qt = 0; qt < QT; ++qt) {
     const size_t qrow = ((size_t)head * P.tq_pad + q0 + qt * 32 + n) * ATT_DH + 8 * h;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -429,10 +433,10 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
       }
     }
   }
-  att_v16f o[ATT_QT][2];  // O^T
-  float m[ATT_QT], lsum[ATT_QT];
+  att_v16f o[QT][2];  // O^T
+  float m[QT], lsum[QT];
 #pragma unroll
-  for (int qt = 0; qt < ATT_QT; ++qt) {
+  for (int qt = 0; qt < QT; ++qt) {
     o[qt][0] = (att_v16f){};
     o[qt][1] = (att_v16f){};
     m[qt] = NEG_INF;
@@ -460,16 +464,16 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
     }
     // both query tiles' scores first, so the softmax of one tile can run on
     // the VALU while the matrix cores work on the other
-    att_v16f s[ATT_QT];
+    att_v16f s[QT];
 #pragma unroll
-    for (int qt = 0; qt < ATT_QT; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
       s[qt] = (att_v16f){};
 #pragma unroll
       for (int k = 0; k < 4; ++k) att_mma3(cur.kh[k], cur.kl[k], qh[qt][k], ql[qt][k], s[qt]);
     }
     if constexpr (ROWS) att_split_v(vr, vb);
 #pragma unroll
-    for (int qt = 0; qt < ATT_QT; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
       // lane (h, n): s[qt][i] = score of query q0 + 32 qt + n against kv
       // row 32 b + 8 (i / 4) + 4 h + i % 4
       const int tq0 = q0 + qt * 32;
@@ -523,7 +527,7 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
   // wavefront 1 hands its partial state to wavefront 0
   if (wv == 1) {
 #pragma unroll
-    for (int qt = 0; qt < ATT_QT; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
@@ -535,7 +539,7 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
   __syncthreads();
   if (wv == 0) {
 #pragma unroll
-    for (int qt = 0; qt < ATT_QT; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
       const float m1 = xm[qt * 64 + l], l1 = xl[qt * 64 + l];
       const float mm = fmaxf(m[qt], m1);
       const float mu = mm == NEG_INF ? 0.0f : mm;
@@ -561,7 +565,7 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
   constexpr int LD = ATT_DH + 4;
   if (wv == 0) {
 #pragma unroll
-    for (int qt = 0; qt < ATT_QT; ++qt)
+    for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
@@ -571,7 +575,7 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
   }
   __syncthreads();
 #pragma unroll
-  for (int it = 0; it < ATT_QB * 16 / 128; ++it) {
+  for (int it = 0; it < QB * 16 / 128; ++it) {
     const int c = it * 128 + (int)threadIdx.x;
     const int row = c >> 4, c4 = c & 15;
     if (q0 + row < t_q) {

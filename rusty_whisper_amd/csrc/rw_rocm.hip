@@ -991,13 +991,22 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
   // with the kv length, so this one fits the layout's part buffer)
   const int nsplit = std::min(L.nsplit, attn_nsplit((size_t)(L.tq_pad / ATT_QB) * n_head, cdiv(t_kv, ATT_KVB)));
   float *part = nsplit > 1 ? (float *)(b + L.off_part) : nullptr;
-  if (rows)
-    hipLaunchKernelGGL(k_attn<true>, dim3(1, (unsigned)n_head, (unsigned)nsplit), dim3(128), 0, s, P, (int)t_q,
-                       (int)t_kv, causal ? 1 : 0, out, (int)ldo, part, q, (int)ldq, k, (int)ldk, v, (int)ldv);
+  // calls of at most 32 query rows run one 32-query tile per workgroup
+  const bool one_tile = t_q <= 32;
+  const dim3 grid(one_tile ? 1u : (unsigned)(L.tq_pad / ATT_QB), (unsigned)n_head, (unsigned)nsplit);
+  const int cz = causal ? 1 : 0;
+  if (rows && one_tile)
+    hipLaunchKernelGGL((k_attn<true, 1>), grid, dim3(128), 0, s, P, (int)t_q, (int)t_kv, cz, out, (int)ldo, part, q,
+                       (int)ldq, k, (int)ldk, v, (int)ldv);
+  else if (rows)
+    hipLaunchKernelGGL((k_attn<true, 2>), grid, dim3(128), 0, s, P, (int)t_q, (int)t_kv, cz, out, (int)ldo, part, q,
+                       (int)ldq, k, (int)ldk, v, (int)ldv);
+  else if (one_tile)
+    hipLaunchKernelGGL((k_attn<false, 1>), grid, dim3(128), 0, s, P, (int)t_q, (int)t_kv, cz, out, (int)ldo, part, q,
+                       (int)ldq, nullptr, 0, nullptr, 0);
   else
-    hipLaunchKernelGGL(k_attn<false>, dim3((unsigned)(L.tq_pad / ATT_QB), (unsigned)n_head, (unsigned)nsplit),
-                       dim3(128), 0, s, P, (int)t_q, (int)t_kv, causal ? 1 : 0, out, (int)ldo, part, q, (int)ldq,
-                       nullptr, 0, nullptr, 0);
+    hipLaunchKernelGGL((k_attn<false, 2>), grid, dim3(128), 0, s, P, (int)t_q, (int)t_kv, cz, out, (int)ldo, part, q,
+                       (int)ldq, nullptr, 0, nullptr, 0);
   LAUNCH_TRY("k_attn");
   if (part) {
     const size_t nz = t_q * (size_t)n_head * ATT_DH;
@@ -1121,8 +1130,8 @@ static int run_beam_self_attention(rw_decoder *const *beams, size_t nb, int l, c
   LAUNCH_TRY("k_attn_split_beams");
   const int nsplit = std::min(L.nsplit, attn_nsplit((size_t)(L.tq_pad / ATT_QB) * heads, cdiv(t_kv, ATT_KVB)));
   float *part = nsplit > 1 ? (float *)(b + L.off_part) : nullptr;
-  hipLaunchKernelGGL(k_attn<false>, dim3((unsigned)(L.tq_pad / ATT_QB), (unsigned)heads, (unsigned)nsplit), dim3(128),
-                     0, s, P, 1, (int)t_kv, 1, att, (int)d->n, part, nullptr, 0, nullptr, 0, nullptr, 0);
+  hipLaunchKernelGGL((k_attn<false, 1>), dim3(1, (unsigned)heads, (unsigned)nsplit), dim3(128), 0, s, P, 1, (int)t_kv,
+                     1, att, (int)d->n, part, nullptr, 0, nullptr, 0, nullptr, 0);
   LAUNCH_TRY("k_attn");
   if (part) {
     hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)cdiv((size_t)heads * ATT_DH, 256)), dim3(256), 0, s, part, nsplit,
