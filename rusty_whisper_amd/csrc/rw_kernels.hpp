@@ -932,6 +932,7 @@ __device__ inline void gemv_fold_oct(const uint8_t *orec, int a_off, int h, int 
                                      float (&acc)[NG][4], float (&accm)[NG][4]) {
   constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR, SO = ZO + 16, DO = SO + 32, PO = DO + 32;
   constexpr int OFF = DT == 2 ? 8 : DT == 6 ? 16 : 0;
+  constexpr int VR = MR < 4 ? MR : 4;  // rows v of 4h + v that some lane holds
 #pragma unroll
   for (int b8 = 0; b8 < OCT; ++b8) {
     const uint8_t *rec = orec + b8 * REC;
@@ -969,14 +970,16 @@ __device__ inline void gemv_fold_oct(const uint8_t *orec, int a_off, int h, int 
       const uint32_t dw = (b8 >> 1) == 0 ? x.d[j].x : (b8 >> 1) == 1 ? x.d[j].y : (b8 >> 1) == 2 ? x.d[j].z : x.d[j].w;
       const float db = h2f((uint16_t)(dw >> (16 * (b8 & 1))));
       const float dav[4] = {da.x, da.y, da.z, da.w};
+      // rows 4h + v: with fewer than 4 rows no lane holds a row v >= MR, so
+      // those sums are not folded (they stay 0 and are never stored)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[j][v] = __builtin_fmaf(dav[v] * db, (float)(s[v] + sdv[v]), acc[j][v]);
+      for (int v = 0; v < VR; ++v) acc[j][v] = __builtin_fmaf(dav[v] * db, (float)(s[v] + sdv[v]), acc[j][v]);
       if (has_min(DT)) {
         const uint32_t mw = (b8 >> 1) == 0 ? x.m[j].x : (b8 >> 1) == 1 ? x.m[j].y : (b8 >> 1) == 2 ? x.m[j].z : x.m[j].w;
         const float mb = h2f((uint16_t)(mw >> (16 * (b8 & 1))));
         const float pav[4] = {pa.x, pa.y, pa.z, pa.w};
 #pragma unroll
-        for (int v = 0; v < 4; ++v) accm[j][v] = __builtin_fmaf(mb, pav[v], accm[j][v]);
+        for (int v = 0; v < VR; ++v) accm[j][v] = __builtin_fmaf(mb, pav[v], accm[j][v]);
       }
     }
   }
