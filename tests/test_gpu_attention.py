@@ -146,3 +146,37 @@ def test_repeated_calls_are_bitwise_stable():
     a = A.attention(q, k, v, 2, False)
     b = A.attention(q, k, v, 2, False)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_query_rows_do_not_depend_on_the_call_shape():
+    """The same query rows against the same keys, in three call shapes: 100
+    query rows (K and V split into planes first, two 32-query tiles per
+    workgroup), 40 rows (one query block: K and V read as f32 rows and split
+    in the kernel, two tiles) and 20 rows (f32 rows, one tile).  A query
+    row's result is the same bits in all three, and matches the oracle."""
+    q, k, v = inputs(100, 300, 256, seed=21)
+    full = A.attention(q, k, v, 4, False)
+    for t in (40, 20):
+        part = A.attention(q[:t], k, v, 4, False)
+        assert np.array_equal(part.view(np.uint32), full[:t].view(np.uint32)), t
+    check(full, q, k, v, 4, False)
+
+
+@pytest.mark.parametrize("t_q", [1, 5, 33])
+def test_decoding_shapes_with_strided_rows(torch, t_q):
+    """Decoding-step shapes (a few query rows, causal, aligned to the end of
+    the keys) read through row strides wider than n: K and V are loaded as
+    f32 rows by the attention kernel itself."""
+    t_kv, n, heads = 77, 256, 4
+    rng = np.random.default_rng(t_q)
+    kv = rng.standard_normal((t_kv, 3 * n)).astype(np.float32)
+    qf = rng.standard_normal((t_q, 2 * n)).astype(np.float32)
+    dk = torch.from_numpy(kv).to("cuda:0")
+    dq = torch.from_numpy(qf).to("cuda:0")
+    out = torch.full((t_q, n + 64), 7.0, device="cuda:0")
+    A.attention_dev(dq[:, :n], dk[:, :n], dk[:, 2 * n:], t_q, t_kv, n, heads, True, out,
+                    ldq=2 * n, ldk=3 * n, ldv=3 * n, ldo=n + 64)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.all(got[:, n:] == 7.0)
+    check(got[:, :n], qf[:, :n], kv[:, :n], kv[:, 2 * n:], heads, True)
