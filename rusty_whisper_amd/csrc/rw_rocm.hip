@@ -509,8 +509,17 @@ static int gemv_need(const rw_weight *w, bool single = false) {
   const int ks = gemv_ks(w, single);
   return ks * (int)cdiv(w->noct, ks);
 }
-static int gemv_cap(int m, int need) {
-  int cap = (int)((size_t)GEMV_LDS_CAP / ((size_t)OCT * gemv_rec_bytes(m)));
+// A single or set launch of at most GEMV_LAT_WGS workgroups (the latency
+// form's candidates, one workgroup per CU) may hold twice that, so that the
+// records of 5 rows over a 4-way split k = 5120 (20 octets) fit at once and
+// the launch takes the latency form.
+#ifndef GEMV_LDS_CAP_LAT
+#define GEMV_LDS_CAP_LAT 65536
+#endif
+constexpr int GEMV_LAT_WGS = 256;  // 4 wavefronts each: one per SIMD of 256 CUs
+static int gemv_cap(int m, int need, int wgs = 1 << 30) {
+  const size_t bytes = wgs <= GEMV_LAT_WGS ? GEMV_LDS_CAP_LAT : GEMV_LDS_CAP;
+  int cap = (int)(bytes / ((size_t)OCT * gemv_rec_bytes(m)));
   if (cap < 4) cap = 4;
   return need < cap ? need : cap;
 }
@@ -537,7 +546,6 @@ static GemvItem gemv_item(const rw_weight *w, const float *a, const float *bias,
 #define GEMV_PD_LAT 3
 #endif
 constexpr int GEMV_PD = GEMV_PD_LAT;
-constexpr int GEMV_LAT_WGS = 256;  // 4 wavefronts each: one per SIMD of 256 CUs
 static bool gemv_latency_form(const GemvSet &one, int wgs, int cap_oct) {
   if (wgs > GEMV_LAT_WGS) return false;
   for (int i = 0; i < one.count; ++i) {
@@ -601,7 +609,7 @@ static int run_product(const rw_weight *w, size_t m, const float *bias, float *o
     one.it[0].qsa = av.sa;
     one.count = 1;
     one.end[0] = gemv_wgs(w, gemv_ks(w, true), false);
-    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, one.end[0], gemv_cap((int)m, gemv_need(w, true)), s);
+    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, one.end[0], gemv_cap((int)m, gemv_need(w, true), one.end[0]), s);
     LAUNCH_TRY("k_gemv");
   } else {
     return run_gemm(&w, &bias, &out, 1, av, (int)m, s);
@@ -619,7 +627,7 @@ static int run_matmul(const rw_weight *w, const float *a, size_t m, const float 
     one.it[0] = gemv_item(w, a, bias, out, true);
     one.count = 1;
     one.end[0] = gemv_wgs(w, gemv_ks(w, true), false);
-    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, one.end[0], gemv_cap((int)m, gemv_need(w, true)), s);
+    RW_DISPATCH_GEMV(w, m, nullptr, nullptr, one, one.end[0], gemv_cap((int)m, gemv_need(w, true), one.end[0]), s);
     LAUNCH_TRY("k_gemv");
     return RW_OK;
   }
@@ -663,7 +671,7 @@ static int run_matmul_set(const rw_weight *const *w, size_t count, const float *
       need = std::max(need, gemv_need(w[i], true));
     }
     set.count = (int)count;
-    RW_DISPATCH_GEMV(w[0], m, nullptr, nullptr, set, wgs, gemv_cap((int)m, need), s);
+    RW_DISPATCH_GEMV(w[0], m, nullptr, nullptr, set, wgs, gemv_cap((int)m, need, wgs), s);
     LAUNCH_TRY("k_gemv");
     return RW_OK;
   }
