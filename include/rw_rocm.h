@@ -106,6 +106,20 @@ int rw_rocm_weight_info(const rw_weight *w, int *dtype, size_t *n, size_t *k, si
 int rw_rocm_matmul_t_q(const rw_weight *w, const float *a, size_t m, size_t k, const float *bias,
                        float *out);
 
+/* The dense f32 tier: out[m, n] = a[m, k] b[n, k]^T (+ bias[n] when bias
+ * != NULL), host pointers, synchronous, on the calling thread's current
+ * device.  Replaces tensor::matmul_t (src/tensor.rs:194-238) and, with a
+ * bias, linear_w's Dense arm (src/quant.rs:1054-1063): every element is the
+ * reference's tensor::dot (8 lane accumulators, products and sums rounded
+ * separately, lanes and tail summed from -0.0) plus the bias, so results
+ * are bit-identical.  m == 0 is valid and writes nothing. */
+int rw_rocm_matmul_t_f32(const float *a, size_t m, size_t k, const float *b, size_t n, const float *bias,
+                         float *out);
+/* The same with device pointers (a, b, bias, out on the current device),
+ * queued on `stream` without waiting.  No reference counterpart as such. */
+int rw_rocm_matmul_t_f32_dev(const float *a, size_t m, size_t k, const float *b, size_t n, const float *bias,
+                             float *out, void *stream);
+
 /* Device-resident form of rw_rocm_matmul_t_q: a, bias and out are device
  * pointers on the weight's device; the work is queued on `stream` (a
  * hipStream_t; NULL = the default stream) and the call returns without

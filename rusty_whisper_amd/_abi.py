@@ -57,6 +57,10 @@ _SIGNATURES = {
                                      C.c_void_p]),
     "rw_rocm_matmul_t_q_dev": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p,
                                          C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]),
+    "rw_rocm_matmul_t_f32": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p,
+                                       C.c_void_p]),
+    "rw_rocm_matmul_t_f32_dev": (C.c_int, [C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p, C.c_size_t, C.c_void_p,
+                                           C.c_void_p, C.c_void_p]),
     "rw_rocm_matmul_workspace_size": (C.c_size_t, [C.c_size_t, C.c_size_t]),
     "rw_rocm_matmul_t_q_dev_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p,
                                                  C.c_void_p, C.c_void_p]),
@@ -250,6 +254,26 @@ def matmul_prequant_multi_dev(weights, workspace, m: int, outs, biases=None, str
     oarr = (C.c_void_p * max(cnt, 1))(*[_ptr(o) for o in outs])
     barr = None if biases is None else (C.c_void_p * max(cnt, 1))(*[_ptr(b) for b in biases])
     check(lib().rw_rocm_matmul_prequant_multi_dev(warr, cnt, _ptr(workspace), m, barr, oarr, stream))
+
+
+def matmul_t_f32(a: np.ndarray, b: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
+    """The dense f32 tier on the device: a[m, k] b[n, k]^T (+ bias), host arrays."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    m, k = a.shape
+    n = b.shape[0]
+    if b.shape[1] != k:
+        raise ValueError(f"inner dims: {k} vs {b.shape[1]}")
+    bb = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    out = np.empty((m, n), np.float32)
+    check(lib().rw_rocm_matmul_t_f32(a.ctypes.data, m, k, b.ctypes.data, n, None if bb is None else bb.ctypes.data,
+                                     out.ctypes.data))
+    return out
+
+
+def matmul_t_f32_dev(a, m: int, k: int, b, n: int, out, bias=None, stream: int | None = None) -> None:
+    """Device pointers (ints or torch tensors), queued on `stream`."""
+    check(lib().rw_rocm_matmul_t_f32_dev(_ptr(a), m, k, _ptr(b), n, _ptr(bias), _ptr(out), stream))
 
 
 def workspace_size(m: int, k: int) -> int:

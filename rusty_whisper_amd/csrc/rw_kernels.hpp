@@ -3,6 +3,7 @@
 // Kernels (the arithmetic of src/quant.rs, restated for CDNA4):
 //   k_repack        ggml blocks -> resident planes (once per weight)
 //   k_dequant       planes -> f32 rows, bit-exact with dequant_row_scalar
+//   k_matmul_t_f32  the dense f32 tier (tensor::matmul_t), bit-exact
 //                   (src/quant.rs:528-537)
 //   k_quantize      f32 activations -> int8 blocks + d_a + sums, bit-exact
 //                   with quantize_acts_i8 (src/quant.rs:691-716)
@@ -355,6 +356,72 @@ __global__ __launch_bounds__(256) void k_repack(const uint8_t *__restrict__ raw,
     for (int e = 0; e < 32; ++e) x |= ((h >> e) & 1u) << qh_bit(e);
     qh[si] = x;
   }
+}
+
+// ---------------------------------------------------------- k_matmul_t_f32
+
+// The dense f32 tier, C[m, n] = A[m, k] B[n, k]^T (+ bias), with every
+// element formed exactly as tensor::dot does (src/tensor.rs:104-129; dot4 at
+// 132-158 is the same per row): 8 lane accumulators from +0, acc[l] =
+// acc[l] + a[p+l]*b[p+l] with the product and the sum rounded separately,
+// over p < k8 = k - k % 8; the tail k8..k summed from -0.0; the lanes summed
+// from -0.0 in order, plus the tail; then + bias[j] (add_bias,
+// src/tensor.rs:262-272).  So results are bit-identical to the reference's.
+// A workgroup computes a 32 x 32 tile from 32-wide k slices of A and B staged
+// in LDS; each thread owns 2 x 2 outputs.
+__global__ __launch_bounds__(256) void k_matmul_t_f32(const float *__restrict__ a, const float *__restrict__ b,
+                                                      const float *__restrict__ bias, float *__restrict__ c,
+                                                      int m, int n, int k) {
+  __shared__ float As[32][33], Bs[32][33];
+  const int t = threadIdx.x, tx = t & 15, ty = t >> 4;
+  const int i0 = blockIdx.y * 32, j0 = blockIdx.x * 32;
+  const int k8 = k - k % 8;
+  float acc[2][2][8];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int v = 0; v < 2; ++v)
+#pragma unroll
+      for (int l = 0; l < 8; ++l) acc[u][v][l] = 0.0f;
+  for (int p0 = 0; p0 < k8; p0 += 32) {
+    // 4 values per thread per tile; past k8 (or past m, n) they are +0, whose
+    // products (+0) leave every accumulator as it is
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int idx = t + 256 * e, r = idx >> 5, q = idx & 31, p = p0 + q;
+      As[r][q] = (i0 + r < m && p < k8) ? a[(size_t)(i0 + r) * k + p] : 0.0f;
+      Bs[r][q] = (j0 + r < n && p < k8) ? b[(size_t)(j0 + r) * k + p] : 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q0 = 0; q0 < 32; q0 += 8)
+#pragma unroll
+      for (int l = 0; l < 8; ++l) {
+        const float a0 = As[2 * ty][q0 + l], a1 = As[2 * ty + 1][q0 + l];
+        const float b0 = Bs[2 * tx][q0 + l], b1 = Bs[2 * tx + 1][q0 + l];
+        acc[0][0][l] = __fadd_rn(acc[0][0][l], __fmul_rn(a0, b0));
+        acc[0][1][l] = __fadd_rn(acc[0][1][l], __fmul_rn(a0, b1));
+        acc[1][0][l] = __fadd_rn(acc[1][0][l], __fmul_rn(a1, b0));
+        acc[1][1][l] = __fadd_rn(acc[1][1][l], __fmul_rn(a1, b1));
+      }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      const int i = i0 + 2 * ty + u, j = j0 + 2 * tx + v;
+      if (i < m && j < n) {
+        float tail = -0.0f;
+        for (int p = k8; p < k; ++p) tail = __fadd_rn(tail, __fmul_rn(a[(size_t)i * k + p], b[(size_t)j * k + p]));
+        float s = -0.0f;
+#pragma unroll
+        for (int l = 0; l < 8; ++l) s = __fadd_rn(s, acc[u][v][l]);
+        s = __fadd_rn(s, tail);
+        if (bias) s = __fadd_rn(s, bias[j]);
+        c[(size_t)i * n + j] = s;
+      }
+    }
 }
 
 // -------------------------------------------------------------- k_dequant

@@ -1585,6 +1585,65 @@ int rw_rocm_matmul_t_q(const rw_weight *w, const float *a, size_t m, size_t k, c
   return RW_OK;
 }
 
+// ------------------------------------------------------ dense f32 tier
+
+static int check_dense_args(const float *a, size_t m, size_t k, const float *b, size_t n, const float *out) {
+  if (m && (!a || !out)) return fail(RW_EINVAL, "a or out is NULL");
+  if (!b) return fail(RW_EINVAL, "b is NULL");
+  if (k == 0 || n == 0) return fail(RW_EINVAL, "k and n must be positive");
+  // grid: n / 32 tiles along x, m / 32 along y (at most 65535)
+  if (cdiv(m, 32) > 65535 || n > ((size_t)1 << 31) - 32 || k > ((size_t)1 << 31) - 1)
+    return fail(RW_EINVAL, "shape [%zu, %zu] x [%zu, %zu]^T too large", m, k, n, k);
+  return RW_OK;
+}
+
+static int launch_matmul_t_f32(const float *a, size_t m, size_t k, const float *b, size_t n, const float *bias,
+                               float *out, hipStream_t s) {
+  hipLaunchKernelGGL(k_matmul_t_f32, dim3((unsigned)cdiv(n, 32), (unsigned)cdiv(m, 32)), dim3(256), 0, s, a, b, bias,
+                     out, (int)m, (int)n, (int)k);
+  LAUNCH_TRY("k_matmul_t_f32");
+  return RW_OK;
+}
+
+int rw_rocm_matmul_t_f32_dev(const float *a, size_t m, size_t k, const float *b, size_t n, const float *bias,
+                             float *out, void *stream) {
+  int rc = check_dense_args(a, m, k, b, n, out);
+  if (rc || m == 0) return rc;
+  return launch_matmul_t_f32(a, m, k, b, n, bias, out, (hipStream_t)stream);
+}
+
+int rw_rocm_matmul_t_f32(const float *a, size_t m, size_t k, const float *b, size_t n, const float *bias,
+                         float *out) {
+  int rc = check_dense_args(a, m, k, b, n, out);
+  if (rc || m == 0) return rc;
+  int dev;
+  HIP_TRY(hipGetDevice(&dev));
+  rc = check_device(dev);
+  if (rc) return rc;
+  CtxGuard g;
+  rc = ctx_acquire(dev, &g.c);
+  if (rc) return rc;
+  Ctx *c = g.c;
+  const size_t off_b = align_up(m * k * 4, 256), off_o = align_up(off_b + n * k * 4, 256);
+  const size_t off_bias = align_up(off_o + m * n * 4, 256), total = align_up(off_bias + n * 4, 256);
+  rc = ctx_reserve(c, total);
+  if (rc) return rc;
+  char *buf = (char *)c->buf;
+  float *da = (float *)buf, *db = (float *)(buf + off_b), *dout = (float *)(buf + off_o);
+  float *dbias = bias ? (float *)(buf + off_bias) : nullptr;
+  HIP_TRY(hipMemcpyAsync(da, a, m * k * 4, hipMemcpyHostToDevice, c->stream));
+  HIP_TRY(hipMemcpyAsync(db, b, n * k * 4, hipMemcpyHostToDevice, c->stream));
+  if (bias) HIP_TRY(hipMemcpyAsync(dbias, bias, n * 4, hipMemcpyHostToDevice, c->stream));
+  rc = launch_matmul_t_f32(da, m, k, db, n, dbias, dout, c->stream);
+  if (rc) {
+    (void)hipStreamSynchronize(c->stream);
+    return rc;
+  }
+  HIP_TRY(hipMemcpyAsync(out, dout, m * n * 4, hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return RW_OK;
+}
+
 size_t rw_rocm_grouped_workspace_size(const rw_linear *items, size_t count) {
   if (!items) return 0;
   return group_plan(items, count).total;

@@ -94,6 +94,17 @@ PYBIND11_MODULE(_rw_quant, m) {
       },
       py::arg("a"), py::arg("b"));
   m.def(
+      "matmul_t",
+      [](const F32 &a, const F32 &b) {
+        rw::Tensor x = to_tensor(a), w = to_tensor(b), y;
+        {
+          py::gil_scoped_release nogil;
+          y = rw::matmul_t(x, w);
+        }
+        return to_numpy(y);
+      },
+      py::arg("a"), py::arg("b"));
+  m.def(
       "linear_w",
       [](const F32 &x, const rw::Weight &w, std::optional<F32> b) {
         std::vector<float> bias;

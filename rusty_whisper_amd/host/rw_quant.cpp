@@ -125,9 +125,26 @@ Tensor matmul_t_q(const Tensor &a, const QTensor &b) {
   return out;
 }
 
+// tensor::matmul_t (src/tensor.rs:194-238) with linear_w's optional bias
+static Tensor dense_product(const Tensor &a, const Tensor &b, const std::vector<float> *bias, const char *what) {
+  if (a.shape.size() != 2 || b.shape.size() != 2) throw Panic("matmul_t takes 2-D tensors");
+  size_t m = a.shape[0], k = a.shape[1], n = b.shape[0];
+  if (k != b.shape[1])  // tensor.rs:200
+    throw Panic("matmul_t inner dims: " + std::to_string(k) + " vs " + std::to_string(b.shape[1]));
+  if (bias && bias->size() != n)  // tensor.rs:266 (add_bias asserts cols == bias.len())
+    throw Panic("bias length " + std::to_string(bias->size()) + " != " + std::to_string(n));
+  Tensor out = Tensor::zeros({m, n});
+  if (m == 0) return out;
+  check(rw_rocm_matmul_t_f32(a.data.data(), m, k, b.data.data(), n, bias ? bias->data() : nullptr,
+                             out.data.data()),
+        what);
+  return out;
+}
+
+Tensor matmul_t(const Tensor &a, const Tensor &b) { return dense_product(a, b, nullptr, "matmul_t"); }
+
 Tensor linear_w(const Tensor &x, const Weight &w, const std::vector<float> *b) {
-  if (!w.is_quant())
-    throw Panic("linear_w: dense weights are outside the device path (use tensor::matmul_t)");
+  if (!w.is_quant()) return dense_product(x, w.dense(), b, "linear_w");
   const QTensor &q = w.quant();
   size_t m = x.shape.at(0), k = x.shape.at(1);
   size_t n = q.shape.at(0);

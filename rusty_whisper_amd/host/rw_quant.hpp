@@ -7,6 +7,7 @@
 //   QTensor                    src/quant.rs:495-640 (new, row_f32, to_dense)
 //   Weight                     src/quant.rs:643-675
 //   matmul_t_q                 src/quant.rs:754-1051
+//   matmul_t                   src/tensor.rs:194-238 (the dense f32 tier)
 //   linear_w                   src/quant.rs:1054-1063
 // Where the reference panics (assert!/panic!), this mirror throws rw::Panic
 // with the same message.  A QTensor uploads its blocks to the device once, on
@@ -97,9 +98,13 @@ class Weight {
 // C = A[m,k] x B^T with B quantized [n,k]; src/quant.rs:754-1051
 Tensor matmul_t_q(const Tensor &a, const QTensor &b);
 
-// y = x W^T + b; src/quant.rs:1054-1063.  The Quant arm runs on the device.
-// The Dense arm is tensor::matmul_t (dense f32 weights), which is not part of
-// the quantized path: it throws Panic, and callers keep their CPU matmul_t.
+// C = A[m,k] x B^T with B dense f32 [n,k]; src/tensor.rs:194-238, on the
+// device, bit-identical to the reference (tensor::dot's order and roundings)
+Tensor matmul_t(const Tensor &a, const Tensor &b);
+
+// y = x W^T + b; src/quant.rs:1054-1063.  Both arms run on the device: Quant
+// through matmul_t_q, Dense through matmul_t; the bias is added as add_bias
+// does (src/tensor.rs:262-272).
 Tensor linear_w(const Tensor &x, const Weight &w, const std::vector<float> *b);
 
 }  // namespace rw

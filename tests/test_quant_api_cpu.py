@@ -30,8 +30,11 @@ def test_dense_weight_accessors():
     w = Q.Weight.Dense(np.arange(6, dtype=np.float32).reshape(2, 3))
     assert not w.is_quant() and w.shape() == [2, 3]
     assert w.row_f32(1).tolist() == [3.0, 4.0, 5.0]
-    with pytest.raises(Q.Panic, match="outside the device path"):
-        Q.linear_w(np.zeros((1, 3), np.float32), w)
+    # the Dense arm checks shapes as tensor::matmul_t and add_bias do (before any device work)
+    with pytest.raises(Q.Panic, match="matmul_t inner dims: 4 vs 3"):
+        Q.linear_w(np.zeros((1, 4), np.float32), w)
+    with pytest.raises(Q.Panic, match="bias length 3 != 2"):
+        Q.linear_w(np.zeros((1, 3), np.float32), w, np.zeros(3, np.float32))
     wq = Q.Weight.Quant([4, 32], 8, np.zeros(4 * 34, np.uint8))
     with pytest.raises(Q.Panic, match="expected dense weight, found quantized"):
         wq.dense()
