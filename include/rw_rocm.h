@@ -263,8 +263,8 @@ int rw_rocm_block_dots(const rw_weight *w, const int8_t *qa, size_t m, int32_t *
  * below 65504.  RW_EINVAL for other head sizes, n_state % n_head != 0,
  * causal with t_q > t_kv, or rows not 16-byte aligned.
  *
- * _dev: device pointers, row strides ld* in floats (>= n_state, multiples
- * of 4 for q, k and out), queued on `stream`; the workspace (NULL: one kept
+ * _dev: device pointers (16-byte aligned), row strides ld* in floats
+ * (>= n_state, multiples of 4), queued on `stream`; the workspace (NULL: one kept
  * per (device, stream)) holds rw_rocm_attention_workspace_size bytes.
  * rw_rocm_attention: host arrays, dense rows, synchronous. */
 size_t rw_rocm_attention_workspace_size(size_t t_q, size_t t_kv, size_t n_state);
@@ -371,10 +371,15 @@ int rw_rocm_decoder_forward_beams_dev(rw_decoder *const *beams, size_t n_beams, 
 
 /* log_softmax (src/transcribe.rs:482-486) and top_k (src/transcribe.rs:672-
  * 685) of every row of logits [rows, n_vocab] (device): ids[rows * k] and
- * logprobs[rows * k] (device) get each row's k largest log-probs, with the
- * reference's rules: exactly -inf is skipped, equal log-probs keep the
- * earlier ids and are listed later id first; NaN is never picked.  A row
- * with fewer than k candidates ends with id 0xFFFFFFFF and -inf.  1 <= k <=
+ * logprobs[rows * k] (device) get the list the reference's insertion scan
+ * keeps: exactly -inf is skipped; an entry is inserted ahead of equal
+ * log-probs while the list has room or it beats the last entry, and the
+ * list is cut to k, so of the entries tied at the k-th log-prob those
+ * admitted while there was room stay, oldest pushed out first; the list runs
+ * by log-prob, equal ones later id first.  A row holding NaN or +inf, or
+ * only -inf, has NaN log-probs throughout (as in the reference), and its
+ * list is ids min(k, n_vocab) - 1 .. 0 with NaN.  A row with fewer than k
+ * candidates ends with id 0xFFFFFFFF and -inf.  1 <= k <=
  * 16, n_vocab <= 131072, rows <= 65535.  The log-sum-exp is summed in tree
  * order, so a log-prob can differ from the reference's in its last bit.
  * `workspace` (>= rw_rocm_logits_topk_workspace_size bytes; NULL = a buffer

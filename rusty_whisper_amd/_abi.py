@@ -482,6 +482,12 @@ class Decoder:
             lib().rw_rocm_decoder_free(self.handle)
             self.handle = None
 
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
 
 def decoder_forward_beams(beams, tokens, hidden, stream: int | None = None) -> None:
     """One beam-search step: beam i (a Decoder forked from one decoder)
@@ -501,12 +507,6 @@ def logits_topk_dev(logits, rows: int, n_vocab: int, k: int, ids, logprobs, stre
 
 def logits_topk_workspace_size(rows: int, n_vocab: int, k: int) -> int:
     return lib().rw_rocm_logits_topk_workspace_size(rows, n_vocab, k)
-
-    def __del__(self):
-        try:
-            self.free()
-        except Exception:
-            pass
 
 
 MODEL_PARSE_ONLY = 1

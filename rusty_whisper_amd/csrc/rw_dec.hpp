@@ -105,18 +105,28 @@ __device__ inline bool topk_before(float v, int i, float bv, int bi) { return v 
 
 // log_softmax of each row (src/transcribe.rs:482-486: the maximum, lse =
 // max + ln(sum exp(v - max)), lp = v - lse) and its top_k
-// (src/transcribe.rs:672-685).  top_k keeps the k largest log-probs, skips
-// exactly -inf, and among equal log-probs keeps the earlier ids; it lists
-// them by log-prob, equal ones later id first (its insertion order).  The
-// selection order is therefore (lp desc, id asc), and NaN is never picked.
+// (src/transcribe.rs:672-685).  top_k scans the log-probs in id order,
+// skips exactly -inf, and inserts (lp, id) ahead of every entry with an
+// equal log-prob while the list has room or lp beats its last entry, then
+// truncates to k.  With v* the k-th largest log-prob and g the number of
+// larger ones, that keeps every entry above v*, and of the entries equal to
+// v* those admitted (fewer than k entries >= v* precede them in id order)
+// minus the oldest ones pushed out later: the last k - g admitted.  The
+// list runs by log-prob, equal ones later id first.
 // Three launches over chunks of TOPK_CHUNK logits (rows x chunks
 // workgroups): k_topk_stats (each chunk's maximum and sum of exp(v - max)),
 // k_topk_chunk (the row's lse from those partials, in one fixed order, then
-// the chunk's k first entries in the selection order, from registers) and
-// k_topk_merge (per row, the k first of all chunks' picks, reordered for
-// the output).  Every chunk's picks hold that chunk's members of the row's
-// answer, so the merge is exact.  The sum runs in tree order, so lse (and
-// every lp) can differ from the reference's sequential sum in its last bit.
+// the chunk's first 2k - 1 entries in the order (lp desc, id asc)) and
+// k_topk_merge (per row, v* and g from the chunks' picks, the admitted
+// entries equal to v* in id order, and the list in the reference's order).
+// A chunk holds at most g <= k - 1 entries above v*, so its first 2k - 1
+// picks hold those and its first k entries equal to v*, which include every
+// one of them the scan can admit: the merge is exact.
+// A row holding NaN or +inf, or only -inf, has a NaN lse (as the reference
+// computes it), so every log-prob is NaN; the scan then admits ids
+// 0 .. k - 1, each ahead of the last, and keeps them with NaN log-probs.
+// The sum runs in tree order, so lse (and every lp) can differ from the
+// reference's sequential sum in its last bit.
 constexpr int TOPK_CHUNK = 2048;  // logits per workgroup (8 per thread)
 constexpr int TOPK_MAX_CHUNKS = 64;
 
@@ -135,10 +145,12 @@ __global__ __launch_bounds__(256) void k_topk_stats(const float *__restrict__ lo
     mx = fmaxf(mx, v[j]);
   }
   mx = block_fmax(mx, sf);
-  float sum = 0.0f;  // an all -inf chunk (suppressed tokens) adds nothing
+  // an all -inf chunk (suppressed tokens) adds nothing; NaN, and +inf
+  // (inf - inf), make the sum NaN as in the reference
+  float sum = 0.0f;
 #pragma unroll
   for (int j = 0; j < TOPK_CHUNK / 256; ++j)
-    if (e0 + j * 256 + t < e1 && v[j] > -__builtin_huge_valf()) sum += expf(v[j] - mx);
+    if (e0 + j * 256 + t < e1 && v[j] != -__builtin_huge_valf()) sum += expf(v[j] - mx);
   sum = block_fsum(sum, sf);
   if (t == 0) {
     pm[(size_t)row * nc + c] = mx;
@@ -147,13 +159,16 @@ __global__ __launch_bounds__(256) void k_topk_stats(const float *__restrict__ lo
 }
 
 // the row's lse from its chunks' (maximum, sum) pairs: the maximum of the
-// maxima, then sum_c s_c exp(m_c - M) in chunk order
+// maxima, then sum_c s_c exp(m_c - M) in chunk order.  A chunk of NaNs only
+// (maximum -inf, sum NaN) still makes it NaN, and so does a row of -inf
+// only, whose reference maximum -inf gives -inf - -inf = NaN.
 __device__ inline float topk_lse(const float *pm, const float *ps, int nc) {
   float M = -__builtin_huge_valf();
   for (int c = 0; c < nc; ++c) M = fmaxf(M, pm[c]);
+  if (M == -__builtin_huge_valf()) return __builtin_nanf("");
   float S = 0.0f;
   for (int c = 0; c < nc; ++c)
-    if (pm[c] > -__builtin_huge_valf()) S += ps[c] * expf(pm[c] - M);
+    if (pm[c] > -__builtin_huge_valf() || ps[c] != ps[c]) S += ps[c] * expf(pm[c] - M);
   return M + logf(S);
 }
 
@@ -219,40 +234,94 @@ __global__ __launch_bounds__(256) void k_topk_chunk(const float *__restrict__ lo
     id[j] = e;
     lp[j] = e < e1 ? x[e] - lse : -__builtin_huge_valf();  // NaN stays NaN and is never picked
   }
-  const size_t o = ((size_t)row * nc + c) * k;
-  topk_rounds<PER>(lp, id, k, cv + o, ci + o, rv, ri);
+  const int cand = 2 * k - 1;
+  const size_t o = ((size_t)row * nc + c) * cand;
+  topk_rounds<PER>(lp, id, cand, cv + o, ci + o, rv, ri);
 }
 
-__global__ __launch_bounds__(256) void k_topk_merge(int nc, int k, const float *__restrict__ cv,
+// the block-wide smallest of one int per thread
+__device__ inline int block_imin(int v, int *scratch) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) v = min(v, __shfl_xor(v, o));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return min(min(scratch[0], scratch[1]), min(scratch[2], scratch[3]));
+}
+
+__global__ __launch_bounds__(256) void k_topk_merge(int nc, int k, int n, const float *__restrict__ pm,
+                                                    const float *__restrict__ ps, const float *__restrict__ cv,
                                                     const int *__restrict__ ci, uint32_t *__restrict__ ids,
                                                     float *__restrict__ lps) {
+  constexpr float NEG_INF = -__builtin_huge_valf();
   __shared__ float rv[4];
   __shared__ int ri[4];
   __shared__ float pick_v[TOPK_MAX];
   __shared__ int pick_i[TOPK_MAX];
+  __shared__ int adm[TOPK_MAX];
   const int row = blockIdx.x, t = threadIdx.x;
-  constexpr int PER = TOPK_MAX_CHUNKS * TOPK_MAX / 256;
+  uint32_t *oid = ids + (size_t)row * k;
+  float *olp = lps + (size_t)row * k;
+  const float lse = topk_lse(pm + (size_t)row * nc, ps + (size_t)row * nc, nc);
+  if (lse != lse) {  // every log-prob NaN: ids min(k, n) - 1 .. 0
+    const int kk = min(k, n);
+    if (t < k) {
+      oid[t] = t < kk ? (uint32_t)(kk - 1 - t) : 0xFFFFFFFFu;
+      olp[t] = t < kk ? __builtin_nanf("") : NEG_INF;
+    }
+    return;
+  }
+  constexpr int PER = (TOPK_MAX_CHUNKS * (2 * TOPK_MAX - 1) + 255) / 256;
   float lp[PER];
   int id[PER];
-  const int total = nc * k;
+  const int total = nc * (2 * k - 1);
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const int e = j * 256 + t;
-    lp[j] = e < total ? cv[(size_t)row * total + e] : -__builtin_huge_valf();
+    lp[j] = e < total ? cv[(size_t)row * total + e] : NEG_INF;
     id[j] = e < total ? ci[(size_t)row * total + e] : INT32_MAX;
   }
+  // the k first in the order (lp desc, id asc): their values are the k
+  // largest log-probs, so the last is v*
   const int got = topk_rounds<PER>(lp, id, k, pick_v, pick_i, rv, ri);
   __syncthreads();
+  int g = got, a = 0;
+  if (got == k) {
+    const float vs = pick_v[k - 1];
+    g = 0;
+    while (g < k && pick_v[g] > vs) ++g;
+    // the entries equal to v* in id order, while fewer than k entries >= v*
+    // precede them (i earlier ones equal to v*, plus the larger ones before)
+    int prev = -1;
+    for (int i = 0; i < k; ++i) {
+      int best = INT32_MAX;
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (lp[j] == vs && id[j] > prev && id[j] < best) best = id[j];
+      best = block_imin(best, ri);
+      if (best == INT32_MAX) break;  // uniform
+      int before = i;
+      for (int r = 0; r < g; ++r) before += pick_i[r] < best;
+      if (before >= k) break;
+      if (t == 0) adm[a] = best;
+      ++a;
+      prev = best;
+    }
+    __syncthreads();
+  }
   if (t == 0) {
-    // equal log-probs: later id first
-    for (int a = 1; a < got; ++a)
-      for (int b = a; b > 0 && pick_v[b] == pick_v[b - 1] && pick_i[b] > pick_i[b - 1]; --b) {
-        const int ti = pick_i[b];
-        pick_i[b] = pick_i[b - 1], pick_i[b - 1] = ti;
+    // the entries above v* (all of them), equal log-probs later id first
+    for (int x = 1; x < g; ++x)
+      for (int y = x; y > 0 && pick_v[y] == pick_v[y - 1] && pick_i[y] > pick_i[y - 1]; --y) {
+        const int ti = pick_i[y];
+        pick_i[y] = pick_i[y - 1], pick_i[y - 1] = ti;
       }
-    for (int r = 0; r < k; ++r) {
-      ids[(size_t)row * k + r] = r < got ? (uint32_t)pick_i[r] : 0xFFFFFFFFu;
-      lps[(size_t)row * k + r] = r < got ? pick_v[r] : -__builtin_huge_valf();
+    for (int r = 0; r < g; ++r) oid[r] = (uint32_t)pick_i[r], olp[r] = pick_v[r];
+    if (got == k) {
+      // then the last k - g admitted entries equal to v*, later id first
+      for (int r = g; r < k; ++r) oid[r] = (uint32_t)adm[a - 1 - (r - g)], olp[r] = pick_v[k - 1];
+    } else {
+      for (int r = got; r < k; ++r) oid[r] = 0xFFFFFFFFu, olp[r] = NEG_INF;
     }
   }
 }

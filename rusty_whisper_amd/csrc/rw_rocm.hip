@@ -956,8 +956,8 @@ static int check_attn_args(const float *q, size_t ldq, const float *k, size_t ld
   if (!q || !out || (t_kv && (!k || !v))) return fail(RW_EINVAL, "q, k, v or out is NULL");
   if (ldq < n_state || ldk < n_state || ldv < n_state || ldo < n_state)
     return fail(RW_EINVAL, "a row stride is smaller than n_state");
-  if (ldq % 4 || ldk % 4 || ldo % 4 || ((uintptr_t)q | (uintptr_t)k | (uintptr_t)out) % 16)
-    return fail(RW_EINVAL, "q, k and out rows must be 16-byte aligned");
+  if (ldq % 4 || ldk % 4 || ldv % 4 || ldo % 4 || ((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) % 16)
+    return fail(RW_EINVAL, "q, k, v and out rows must be 16-byte aligned");
   return RW_OK;
 }
 
@@ -2123,7 +2123,7 @@ struct TopkLayout {
 static TopkLayout topk_layout(size_t rows, size_t n_vocab, size_t k) {
   TopkLayout L{};
   L.nc = (int)cdiv(n_vocab, TOPK_CHUNK);
-  const size_t np = rows * L.nc, nk = np * k;
+  const size_t np = rows * L.nc, nk = np * (2 * k - 1);  // 2k - 1 picks per chunk
   L.off_pm = 0;
   L.off_ps = align_up(np * 4, 256);
   L.off_cv = align_up(L.off_ps + np * 4, 256);
@@ -2166,7 +2166,8 @@ int rw_rocm_logits_topk_dev(const float *logits, size_t rows, size_t n_vocab, si
   LAUNCH_TRY("k_topk_stats");
   hipLaunchKernelGGL(k_topk_chunk, grid, dim3(256), 0, s, logits, (int)n_vocab, (int)k, pm, ps, cv, ci);
   LAUNCH_TRY("k_topk_chunk");
-  hipLaunchKernelGGL(k_topk_merge, dim3((unsigned)rows), dim3(256), 0, s, L.nc, (int)k, cv, ci, ids, logprobs);
+  hipLaunchKernelGGL(k_topk_merge, dim3((unsigned)rows), dim3(256), 0, s, L.nc, (int)k, (int)n_vocab, pm, ps, cv,
+                     ci, ids, logprobs);
   LAUNCH_TRY("k_topk_merge");
   return RW_OK;
 }

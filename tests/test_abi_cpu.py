@@ -95,3 +95,19 @@ def test_last_error_truncates_safely():
     buf = C.create_string_buffer(8)
     n = A.lib().rw_rocm_last_error(buf, 8)
     assert n > 7 and len(buf.value) == 7
+
+
+def test_owning_classes_free_on_collection():
+    """Every binding class that owns device memory (has free()) releases it
+    when collected: __del__ is a method of the class itself, not a function
+    nested elsewhere in the module."""
+    import ast
+    import inspect
+
+    tree = ast.parse(inspect.getsource(A))
+    for node in ast.walk(tree):
+        if isinstance(node, ast.FunctionDef) and node.name != "__del__":
+            nested = [n.name for n in ast.walk(node) if isinstance(n, ast.FunctionDef) and n.name == "__del__"]
+            assert not nested, f"__del__ nested in function {node.name}"
+    for cls in (A.DeviceWeight, A.Decoder, A.Group, A.Model):
+        assert "free" in vars(cls) and "__del__" in vars(cls), cls.__name__

@@ -9,12 +9,13 @@ import pytest
 from rusty_whisper_amd import _abi as A
 
 
-def _call(t_q, t_kv, n_state, n_head, causal, ldq=None, q_off=0):
+def _call(t_q, t_kv, n_state, n_head, causal, ldq=None, q_off=0, ldv=None, v_off=0):
     q = np.zeros(max(t_q * (ldq or n_state) + 16, 1), np.float32)
     k = np.zeros(max(t_kv * n_state, 1), np.float32)
+    v = np.zeros(max(t_kv * (ldv or n_state) + 16, 1), np.float32)
     out = np.zeros(max(t_q * n_state, 1), np.float32)
     return A.lib().rw_rocm_attention_dev(q.ctypes.data + q_off, ldq or n_state, k.ctypes.data, n_state,
-                                         k.ctypes.data, n_state, t_q, t_kv, n_state, n_head, causal,
+                                         v.ctypes.data + v_off, ldv or n_state, t_q, t_kv, n_state, n_head, causal,
                                          out.ctypes.data, n_state, None, 0, None)
 
 
@@ -35,6 +36,11 @@ def test_rejects_short_or_misaligned_rows():
     assert _call(4, 4, 128, 2, 0, ldq=130) == A.RW_EINVAL
     assert "16-byte aligned" in A.last_error()
     assert _call(4, 4, 128, 2, 0, q_off=4) == A.RW_EINVAL
+    assert "16-byte aligned" in A.last_error()
+    # v is read with 16-byte loads too
+    assert _call(4, 4, 128, 2, 0, ldv=130) == A.RW_EINVAL
+    assert "16-byte aligned" in A.last_error()
+    assert _call(4, 4, 128, 2, 0, v_off=8) == A.RW_EINVAL
     assert "16-byte aligned" in A.last_error()
 
 

@@ -46,3 +46,42 @@ def test_log_softmax_against_float64():
     assert np.max(diff) - np.min(diff) <= 2 * np.max(np.spacing(np.abs(got[fin])))
     assert np.all(got[~fin] == -np.inf)
     assert abs(np.exp(got[fin].astype(np.float64)).sum() - 1.0) < fin.sum() * 2.0 ** -24
+
+
+def _top_k_by_rank(lps, k):
+    """The kept list described by ranks instead of the scan: v* is the k-th
+    largest log-prob and g the count above it; every entry above v* stays,
+    and of the entries equal to v* those with fewer than k entries >= v*
+    before them in id order are admitted, the last k - g of them kept.
+    Listed by log-prob, equal ones later id first."""
+    fin = [(v, i) for i, v in enumerate(lps.tolist()) if v != -np.inf]
+    if len(fin) <= k:
+        kept = fin
+    else:
+        vs = sorted((v for v, _ in fin), reverse=True)[k - 1]
+        above = [(v, i) for v, i in fin if v > vs]
+        adm, seen = [], 0
+        for v, i in fin:
+            if v == vs and seen < k:
+                adm.append((v, i))
+            seen += v >= vs
+        kept = above + adm[len(adm) - (k - len(above)):]
+    return sorted(kept, key=lambda e: (-e[0], -e[1]))
+
+
+def test_top_k_tied_entries_pushed_out_by_larger_ones():
+    assert top_k(np.array([-1.0, -1.0, -0.5], np.float32), 2) == [(-0.5, 2), (-1.0, 1)]
+    rng = np.random.default_rng(8)
+    for _ in range(300):
+        lps = rng.integers(-4, 1, 40).astype(np.float32)
+        lps[rng.random(40) < 0.2] = -np.inf
+        for k in (1, 2, 3, 5, 8):
+            assert top_k(lps, k) == _top_k_by_rank(lps, k)
+
+
+def test_top_k_of_nan_log_probs():
+    # a NaN or +inf logit, or -inf only, gives NaN log-probs throughout
+    for row in ([0.0, np.nan, 1.0, 2.0], [np.inf, 0.0, 1.0, 2.0], [-np.inf] * 4):
+        lp = log_softmax(np.array(row, np.float32))
+        assert np.all(np.isnan(lp))
+        assert [i for _, i in top_k(lp, 3)] == [2, 1, 0]

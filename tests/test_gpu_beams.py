@@ -6,12 +6,12 @@
   from repeated values test the tie rules exactly, since equal logits give
   equal log-probs whatever the log-sum-exp), log-probs within the reference's
   own log-sum-exp error (its sequential f32 sum: n 2^-24 of the sum) plus one
-  rounding.
+  rounding; rows whose log-sum-exp is NaN give NaN log-probs.
 * rw_rocm_decoder_forward_beams_dev: one step of several forked beams at once
   against each beam stepped alone through rw_rocm_decoder_forward_hidden_dev
   (within 1e-5 of the row's norm: the products see more rows and the
   attention's kv split is chosen for all beams together) and against the
-  oracle decoder (the decoder tests' 5e-3 bar); the beams' caches then hold
+  oracle decoder (the decoder tests' 4e-3 bar); the beams' caches then hold
   the same rows (a second step agrees too).
 """
 import numpy as np
@@ -50,7 +50,9 @@ def check_rows(logits, k, ids, lps, exact_lp=False):
         got_ids = [int(i) for i in ids[r] if i != 0xFFFFFFFF]
         assert got_ids == [i for _, i in want], (r, got_ids[:8], want[:8])
         assert np.all(ids[r][len(want):] == 0xFFFFFFFF) and np.all(lps[r][len(want):] == -np.inf)
-        if want:
+        if want and np.isnan(want[0][0]):  # a NaN log-sum-exp: every log-prob NaN
+            assert np.all(np.isnan(lps[r][:len(want)]))
+        elif want:
             wl = np.array([v for v, _ in want], np.float64)
             n = np.isfinite(logits[r]).sum()
             tol = n * 2.0 ** -24 * 1.0 + 2 * np.spacing(np.abs(wl).max())
@@ -85,6 +87,51 @@ def test_topk_ties_and_short_rows(torch):
     for k in (4, 16):
         ids, lps = device_topk(torch, logits, k)
         check_rows(logits, k, ids, lps)
+
+
+def test_topk_tied_entries_pushed_out_by_larger_ones(torch):
+    """The reference's scan inserts ahead of equal entries and cuts the list
+    at k, so a later, larger log-prob pushes out the earliest id of a tied
+    group at the cut-off (src/transcribe.rs:672-685)."""
+    ids, lps = device_topk(torch, np.array([[0.0, 0.0, 0.5]], np.float32), 2)
+    assert ids[0].tolist() == [2, 1]
+    # across chunks: five entries tied at the cut-off, three larger ones
+    # arriving between them; the scan admits ids 5, 100, 3000 and 9000 and
+    # keeps the last two of them
+    row = np.full((1, 51866), -20.0, np.float32)
+    row[0, [5, 100, 3000, 9000, 20000]] = 1.0
+    row[0, [2100, 40000, 51000]] = 2.0
+    ids, lps = device_topk(torch, row, 5)
+    assert ids[0].tolist() == [51000, 40000, 2100, 9000, 3000]
+    check_rows(row, 5, ids, lps)
+    # random sparse rows of a few tied values over many chunks
+    rng = np.random.default_rng(13)
+    for k in (2, 5, 16):
+        rows = np.full((6, 51866), -np.inf, np.float32)
+        rows[:3] = -30.0
+        for r in range(6):
+            at = rng.choice(51866, 60, replace=False)
+            rows[r, at] = rng.integers(0, 6, 60).astype(np.float32)
+        ids, lps = device_topk(torch, rows, k)
+        check_rows(rows, k, ids, lps)
+
+
+def test_topk_nan_log_sum_exp_rows(torch):
+    """A NaN or +inf logit, or a row of -inf only, makes the reference's
+    log-sum-exp NaN and so every log-prob; its scan then keeps ids
+    min(k, n) - 1 .. 0."""
+    rows = np.random.default_rng(17).standard_normal((4, 5000)).astype(np.float32)
+    rows[0, 4321] = np.nan
+    rows[1, 77] = np.inf
+    rows[2, :] = -np.inf
+    rows[3, 2049] = np.nan  # in the second chunk only
+    for k in (1, 5):
+        ids, lps = device_topk(torch, rows, k)
+        assert all(ids[r].tolist() == list(range(k - 1, -1, -1)) for r in range(4))
+        check_rows(rows, k, ids, lps)
+    ids, lps = device_topk(torch, np.array([[0.0, np.nan, 1.0]], np.float32), 5)
+    assert ids[0].tolist() == [2, 1, 0, 0xFFFFFFFF, 0xFFFFFFFF]
+    assert np.all(np.isnan(lps[0][:3])) and np.all(lps[0][3:] == -np.inf)
 
 
 def test_topk_masked_chunks_and_caller_workspace(torch):
@@ -160,7 +207,9 @@ def test_beams_match_separate_steps(torch, n, n_layer, dtype, nb):
     ob.forward_hidden([1, 2, 3])
     ob.forward_hidden([7])
     want = ob.forward_hidden([3])
-    assert _rel(got[0:1], want) <= 5e-3
+    err = _rel(got[0:1], want)
+    print(f"  beam 0 vs the oracle decoder {err:.3g}", flush=True)
+    assert err <= 4e-3, err
 
 
 def _step(torch, dec, toks, n):

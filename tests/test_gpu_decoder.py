@@ -2,11 +2,13 @@
 forward_hidden, fork, reset) against the oracle's restatement of the
 reference's Decoder (oracle/decoder.py, src/decoder.rs:36-213).
 
-Bar: every step's hidden rows within 5e-3 of the oracle's, max error over
+Bar: every step's hidden rows within 4e-3 of the oracle's, max error over
 the oracle row's L2 norm -- a chain of per-product 1e-3 bars and
 attention, through every layer -- over a prompt (GEMV regime at <= 8 rows,
-GEMM regime above) and single-token steps; forks match independently
-decoded branches bit for bit."""
+GEMM regime above) and single-token steps (measured 0.8-2.6e-3); a layer
+whose q, k and v differ in dtype within 5e-3 (measured 3.2e-3); forks
+match independently decoded branches bit for bit.  Each test prints its
+errors."""
 import numpy as np
 import pytest
 
@@ -15,7 +17,8 @@ from rusty_whisper_amd import _abi as A
 from _decoder_params import decoder_params
 
 pytestmark = pytest.mark.gpu
-TOL = 5e-3
+TOL = 4e-3
+TOL_MIXED = 5e-3
 
 
 @pytest.fixture(scope="module")
@@ -129,7 +132,7 @@ def test_decoder_mixed_qkv_dtypes(torch):
     for t in (17, 250, 4):
         errs.append(rel(step(torch, d, [t], n), o.forward_hidden([t])))
     print("  errors", ["%.2g" % e for e in errs], flush=True)
-    assert max(errs) <= TOL, errs
+    assert max(errs) <= TOL_MIXED, errs
 
 
 def test_large_v3_decoder_slice_with_logits(torch):

@@ -5,8 +5,9 @@ device) against the oracle's restatement (oracle/encoder.py: src/encoder.rs
 Bar: the layer output within 2e-3 of the oracle, max error scaled by the
 oracle row's L2 norm -- each of the layer's four products carries the
 matmul path's 1e-3 bar and the residual stream carries x itself -- and the
-change the layer makes to x (output - x) within 1e-2 of the oracle's change
-on the same scale."""
+change the layer makes to x (output - x) within 3e-3 of the oracle's change
+on the same scale.  Measured on the cases below: 0.94-1.43e-3 for the
+output, 1.36-1.6e-3 for the change; the test prints both."""
 import numpy as np
 import pytest
 
@@ -75,7 +76,7 @@ def test_encoder_layer_parity(torch, t, n, dtype, variant):
     print(f"  error {e:.3g}, of the change {ed:.3g}", flush=True)
     assert np.all(np.isfinite(got))
     assert e <= 2e-3, e
-    assert ed <= 1e-2, ed
+    assert ed <= 3e-3, ed
 
 
 def test_layer_rejects_small_t_and_bad_shapes(torch):
