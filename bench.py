@@ -392,7 +392,17 @@ def time_decoder_tokens(A, synth, torch, D, stream, steps: int):
     t0 = time.perf_counter()
     dec.set_audio(enc, stream)
     torch.cuda.synchronize()
-    t_audio = (time.perf_counter() - t0) * 1e3
+    t_audio_cold = (time.perf_counter() - t0) * 1e3  # host clock, first call (workspace allocation included)
+    warm = []
+    for _ in range(7):  # later windows: HIP events on the launching stream, median
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        dec.set_audio(enc, stream)
+        e1.record()
+        torch.cuda.synchronize()
+        warm.append(e0.elapsed_time(e1))
+    t_audio = {"cold_ms": t_audio_cold, "warm_ms": statistics.median(warm)}
     hid = torch.empty(n_ctx, d, device="cuda:0")
     logits = torch.empty(1, vocab, device="cuda:0")
     tok = 50363
@@ -730,6 +740,55 @@ def leg_turbo_decoder(A, synth, torch, layers_w, steps: int, seed0: int):
     }
 
 
+def leg_host_entry(A, W, D, reps: int = 5):
+    """The drop-in entry itself, rw_rocm_matmul_t_q (what linear_w / matmul_t_q
+    routes to, src/quant.rs:754,1054-1063): host arrays in and out, pageable
+    as a Rust Vec<f32> is; per call the activation and bias go to the device,
+    the activation is quantized, the product runs and the output comes back,
+    synchronously.  Encoder: layer 0's six linears at M = W["m"]; decode: one
+    decoder layer's ten linears plus the logits at M = D["rows"].  Host wall
+    clock, median of `reps` passes after one warm pass."""
+    import numpy as np
+
+    rng = np.random.default_rng(17)
+
+    def run(calls):
+        times = []
+        for it in range(reps + 1):
+            t0 = time.perf_counter()
+            for w, a, b in calls:
+                w.matmul(a, b)
+            if it:
+                times.append(time.perf_counter() - t0)
+        return statistics.median(times) * 1e3
+
+    m = W["m"]
+    lw = W["layers"][0]
+    enc = [(lw[name], rng.standard_normal((m, k), dtype=np.float32),
+            None if W["bias"][name] is None else W["bias"][name].cpu().numpy()) for name, n, k in W["shapes"]]
+    ems = run(enc)
+    eops = sum(2 * m * w.n * w.k for w, _, _ in enc)
+    epcie = sum(4 * m * (w.k + w.n) for w, _, _ in enc)
+    md = D["rows"]
+    dsel = list(D["items"][:10]) + [D["items"][-1]]
+    dec = [(w, rng.standard_normal((md, w.k), dtype=np.float32), None if b is None else b.cpu().numpy())
+           for (w, _, b, _, _) in dsel]
+    dms = run(dec)
+    dbytes = sum(w.n * (w.k // 32) * A.block_bytes(w.dtype) + 4 * md * (w.k + w.n) for w, _, _ in dec)
+    return {
+        "workload": "rw_rocm_matmul_t_q with pageable host arrays (PCIe copies, quantization and product per "
+                    f"call, synchronous): encoder = large-v3 layer 0's six linears at M={m}; decode = one large-v3 "
+                    f"decoder layer's ten linears plus the [51866 x 1280] logits at M={md}",
+        "encoder_ms_per_layer": round(ems, 3),
+        "encoder_TOPS": round(eops / (ems * 1e-3) / 1e12, 3),
+        "encoder_pcie_bytes": epcie,
+        "decode_ms_per_layer_and_logits": round(dms, 3),
+        "decode_GB_per_s": round(dbytes / (dms * 1e-3) / 1e9, 2),
+        "decode_calls": len(dec),
+        "note": "host wall clock around synchronous calls; the device-resident figures are the _dev entries",
+    }
+
+
 def profile_traffic(root: str):
     """HBM bytes per k_gemm launch of the headline workload, from the
     committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary (the json block of
@@ -758,6 +817,7 @@ def main() -> int:
     ap.add_argument("--no-layers", action="store_true")
     ap.add_argument("--no-legs", action="store_true", help="skip the other configurations' legs")
     ap.add_argument("--no-cold", action="store_true")
+    ap.add_argument("--no-host-entry", action="store_true", help="skip timing rw_rocm_matmul_t_q on host arrays")
     ap.add_argument("--no-kernel-timing", action="store_true",
                     help="skip the per-launch k_gemm bursts (graph replays), e.g. under a counter profiler")
     ap.add_argument("--eager", action="store_true",
@@ -908,6 +968,8 @@ def main() -> int:
             f"{t['prefill_m224']['ms']} ms ({t['prefill_m224']['value']} TOPS)")
         torch.cuda.empty_cache()
 
+    W_host = None if args.no_host_entry else {k: W[k] for k in ("layers", "shapes", "bias", "m")}
+    W_host = W_host and dict(W_host, layers=W["layers"][:1])
     del W
     torch.cuda.empty_cache()
 
@@ -943,7 +1005,8 @@ def main() -> int:
             del D1
         if not args.no_layers:
             t_audio, per_len, finite, beam = time_decoder_tokens(A, synth, torch, D, stream, 20)
-            log(f"decoder on the device: set_audio {t_audio:.2f} ms, ms per token with logits by cache length "
+            log(f"decoder on the device: set_audio {t_audio['warm_ms']:.3f} ms warm ({t_audio['cold_ms']:.2f} ms "
+                f"first call), ms per token with logits by cache length "
                 f"{ {k: round(v, 3) for k, v in per_len.items()} } (finite={finite})")
             result["decoder_tokens"] = {
                 "workload": "large-v3 decoder, one beam, Q5_0: per token the embedding, 32 layers (causal "
@@ -953,7 +1016,10 @@ def main() -> int:
                 "ms_per_token_by_cache_length": {str(k): round(v, 4) for k, v in per_len.items()},
                 "note": "ms_per_token: steps 5..24 of the cache (3-token prompt, one warm step, 20 timed); the "
                         "other lengths time 4 steps ending at that many cached rows",
-                "set_audio_ms": round(t_audio, 3),
+                "set_audio_ms": round(t_audio["warm_ms"], 3),
+                "set_audio_first_call_ms": round(t_audio["cold_ms"], 3),
+                "set_audio_note": "set_audio_ms: median of 7 later calls (HIP events on the launching stream); "
+                                  "the first call also allocates the decoder's workspace (host clock)",
                 "finite": finite,
                 "beams": {
                     "workload": f"beam search step, {beam['beams']} beams forked from one decoder: "
@@ -970,6 +1036,12 @@ def main() -> int:
             }
             log(f"beam step ({beam['beams']} beams): {beam['ms_per_step']:.3f} ms, "
                 f"{beam['ms_per_step'] / beam['beams']:.3f} ms per token per beam; fork {beam['fork_ms']:.3f} ms")
+        if W_host is not None:
+            h = leg_host_entry(A, W_host, D)
+            log(f"host entry rw_rocm_matmul_t_q: encoder layer {h['encoder_ms_per_layer']} ms "
+                f"({h['encoder_TOPS']} TOPS), decoder layer + logits {h['decode_ms_per_layer_and_logits']} ms "
+                f"({h['decode_GB_per_s']} GB/s)")
+            result["host_entry"] = h
         del D
         torch.cuda.empty_cache()
     if legs:

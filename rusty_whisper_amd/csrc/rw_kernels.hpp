@@ -61,6 +61,8 @@ __device__ inline float ldg_f(const void *p) { return *(const float RW_GLOBAL_AS
 __device__ inline uint32_t ldg_u32(const void *p) { return *(const uint32_t RW_GLOBAL_AS *)p; }
 __device__ inline int32_t ldg_i32(const void *p) { return *(const int32_t RW_GLOBAL_AS *)p; }
 __device__ inline void stg_f(float *p, float v) { *(float RW_GLOBAL_AS *)(void *)p = v; }
+// streaming store (nt policy): output written once, read by a later launch
+__device__ inline void stg_f_nt(float *p, float v) { __builtin_nontemporal_store(v, (float RW_GLOBAL_AS *)(void *)p); }
 __device__ inline void stg_u32(void *p, uint32_t v) { *(uint32_t RW_GLOBAL_AS *)p = v; }
 __device__ inline void stg_u4(void *p, uint4 v) {
   *(rw_u32x4 RW_GLOBAL_AS *)p = rw_u32x4{v.x, v.y, v.z, v.w};
@@ -1642,19 +1644,11 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int
       bc = bn;
     }
   }
-  // the last nsw - s (< S) blocks are already in st[0 ..]
-#pragma unroll
-  for (int u = 0; u < S - 1; ++u)
-    if (s + u < nsw) {
-      const GemmB<TN> bn = deq(st[(u + 1) % S]);
-      mma(st[u], bc);
-      bc = bn;
-    }
-
   // The workgroup's TM x TN output tiles (32 x 32 each, tile u = TN i + j)
   // are dealt to the KW wavefronts in runs of UPW: a wavefront finishes RPW
-  // row groups x CPW column groups.  Their epilogue inputs load while the
-  // partials meet in LDS (rows and columns past the end read the last one).
+  // row groups x CPW column groups.  Their epilogue inputs are requested
+  // before the last blocks' MFMAs and land while those run and the partials
+  // meet in LDS (rows and columns past the end read the last one).
   constexpr int NU = TM * TN, UPW = (NU + KW - 1) / KW;
   static_assert(UPW < TN || UPW % TN == 0, "a run covers whole row groups");
   constexpr int RPW = UPW >= TN ? UPW / TN : 1, CPW = UPW >= TN ? TN : 1;
@@ -1683,6 +1677,15 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int
     cv[cc] = ldg_f(gp.cs + wr);
     if (OFFS) mv[cc] = offs ? ldg_f(cmp + wr) : 0.0f;
   }
+  // the last nsw - s (< S) blocks are already in st[0 ..]
+#pragma unroll
+  for (int u = 0; u < S - 1; ++u)
+    if (s + u < nsw) {
+      const GemmB<TN> bn = deq(st[(u + 1) % S]);
+      mma(st[u], bc);
+      bc = bn;
+    }
+
   float4 *red = reinterpret_cast<float4 *>(lds);
   if (KW > 1) {
 #pragma unroll
@@ -1760,13 +1763,13 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int
         for (int v = 0; v < 16; ++v) y[v] = x[v] + y[v];
       }
 #pragma unroll
-      for (int v = 0; v < 16; ++v) stg_f(o + (size_t)(8 * (v >> 2) + (v & 3)) * n, y[v]);
+      for (int v = 0; v < 16; ++v) stg_f_nt(o + (size_t)(8 * (v >> 2) + (v & 3)) * n, y[v]);
     } else if (col < n) {
 #pragma unroll
       for (int v = 0; v < 16; ++v)
         if (tg * RG + 4 * h + 8 * (v >> 2) + (v & 3) < m) {
           float *p = o + (size_t)(8 * (v >> 2) + (v & 3)) * n;
-          stg_f(p, (flags & GEMM_ACC) ? *p + y[v] : y[v]);
+          stg_f_nt(p, (flags & GEMM_ACC) ? *p + y[v] : y[v]);
         }
     }
   }
