@@ -6,9 +6,11 @@ at one 30 s window, M = 1500 rows, weights in Q5_1 -- 32 layers x {q, k, v,
 out [1280x1280], fc1 [5120x1280], fc2 [1280x5120]}, with biases where
 Whisper has them (no bias on k).  Each layer quantizes its three distinct
 inputs (the attention-block input shared by q/k/v, the attention output, the
-MLP input) and the fc1 output, then runs the six products in four GEMM
+MLP input) and fc2's input, then runs the six products in four GEMM
 launches (q, k and v read one input and share a launch, as
-rw_rocm_matmul_prequant_multi_dev allows).  Weights are seeded N(0, 0.02)
+rw_rocm_matmul_prequant_multi_dev allows).  `fused_mlp` times the same step
+with fc2's input gelu(fc1's output), as the encoder's MLP runs, quantized in
+fc1's epilogue (rw_rocm_matmul_prequant_gelu_quantize_dev).  Weights are seeded N(0, 0.02)
 quantized to Q5_1 (472 MB resident, more than the 256 MB MALL); activations
 are seeded N(0, 1) and resident in HBM before timing starts.  `value` is the
 step with the same activation buffers for every layer (warm); `cold` gives
@@ -83,6 +85,8 @@ def encoder_workload(A, synth, torch, dtype: int, m: int, seed0: int, cfg=None, 
         return t
 
     wsz = {key: A.workspace_size(m, k) for key, k in widths.items()}
+    # fc2's input workspace also takes the fused GELU + quantization's quants
+    wsz["h"] = max(wsz["h"], A.gelu_quantize_workspace_size(m, fc))
 
     def make_set():
         return dict(inputs=make_inputs(), wsp={key: torch.empty(wsz[key], dtype=torch.uint8, device=dev)
@@ -113,27 +117,39 @@ def product(A, W, lw, names, stream, bufs=None):
                                     [W["bias"][x] for x in names], stream)
 
 
-def encoder_step(A, W, stream):
+def encoder_step(A, W, stream, fused: bool = False):
+    """One step: per layer the q/k/v input, the attention output and the MLP
+    input are quantized (synthetic activations), then q/k/v (one launch), out,
+    fc1 and fc2.  fused: as the encoder runs its MLP (src/encoder.rs:161-171),
+    fc2's input is gelu(fc1's output), quantized in fc1's epilogue
+    (rw_rocm_matmul_prequant_gelu_quantize_dev); otherwise fc1 writes its f32
+    output and fc2 reads a fourth synthetic activation, quantized by its own
+    launch (every product as a separate matmul_t_q call)."""
     m, sets = W["m"], W["sets"]
+    keys = ("qkv", "attn", "mlp") if fused else ("qkv", "attn", "mlp", "h")
     for i, lw in enumerate(W["layers"]):
         bufs = sets[i % len(sets)]
-        for key in ("qkv", "attn", "mlp", "h"):
+        for key in keys:
             t = bufs["inputs"][key]
             A.quantize_dev(t, m, t.shape[1], bufs["wsp"][key], W["wsz"][key], stream)
-        for _, names in LAUNCHES:
-            product(A, W, lw, names, stream, bufs)
+        for label, names in LAUNCHES:
+            if fused and label == "fc1":
+                A.matmul_prequant_gelu_quantize_dev(lw["fc1"], bufs["wsp"]["mlp"], m, W["bias"]["fc1"],
+                                                    bufs["wsp"]["h"], W["wsz"]["h"], stream)
+            else:
+                product(A, W, lw, names, stream, bufs)
 
 
-def time_encoder(A, torch, W, steps: int, warmup: int, stream):
+def time_encoder(A, torch, W, steps: int, warmup: int, stream, fused: bool = False):
     for _ in range(warmup):
-        encoder_step(A, W, stream)
+        encoder_step(A, W, stream, fused)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(steps):
-        encoder_step(A, W, stream)
+        encoder_step(A, W, stream, fused)
     end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -169,8 +185,8 @@ def time_graph(torch, fn, steps: int, warmup: int):
     return ms
 
 
-def time_encoder_graph(A, torch, W, steps: int, warmup: int):
-    return time_graph(torch, lambda st: encoder_step(A, W, st), steps, warmup)
+def time_encoder_graph(A, torch, W, steps: int, warmup: int, fused: bool = False):
+    return time_graph(torch, lambda st: encoder_step(A, W, st, fused), steps, warmup)
 
 
 def time_gemm_kernel(A, torch, W, stream, reps: int = 3):
@@ -859,6 +875,11 @@ def main() -> int:
     ms = eager_ms if args.eager else time_encoder_graph(A, torch, W, args.steps, args.warmup)
     tops = W["ops"] / (ms * 1e-3) / 1e12
     log(f"encoder step, {'eager' if args.eager else 'graph replay'} {ms:.3f} ms  ({tops:.1f} TOPS)")
+    fms = None
+    if not args.eager:
+        fms = time_encoder_graph(A, torch, W, args.steps, args.warmup, fused=True)
+        log(f"encoder step with the MLP as the encoder runs it (fc2 on gelu(fc1), quantized in fc1's epilogue): "
+            f"{fms:.3f} ms ({W['ops'] / (fms * 1e-3) / 1e12:.1f} TOPS)")
 
     if args.no_kernel_timing:
         gemm_ms, gemm_ops, launches, per_shape = ms / (4 * len(W["layers"])), W["ops"] / (4 * len(W["layers"])), 0, {}
@@ -885,6 +906,13 @@ def main() -> int:
         "launch": "one encoder step (256 launches: per layer 4 quantizations, q/k/v in one GEMM launch, out, "
                   "fc1, fc2) captured in a HIP graph and replayed; eager_ms_per_step launches the same kernels "
                   "one by one from the host",
+        "fused_mlp": None if fms is None else {
+            "ms_per_step": round(fms, 4),
+            "TOPS": round(W["ops"] / (fms * 1e-3) / 1e12, 3),
+            "workload": "the same step with fc2's input gelu(fc1's output), as the encoder's MLP runs "
+                        "(src/encoder.rs:161-171): fc1's epilogue adds the bias, applies GELU and quantizes "
+                        "for fc2 (rw_rocm_matmul_prequant_gelu_quantize_dev), so the step has 3 quantizations and "
+                        "does the GELU work the headline step does not"},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -909,8 +937,10 @@ def main() -> int:
             "traffic": traffic,
             "traffic_source": prof_path if traffic is not None else None,
             "kernel": f"k_gemm<{args.quant}> on v_mfma_f32_32x32x16_f16 (2*M*N*K per launch)",
-            "limiter": "operand delivery from L2 into the CUs: MFMA busy about a quarter of the kernel's time, "
-                       "L2->CU operand traffic 10-25x the unique bytes (rocprofv3 counters in "
+            "limiter": "operand delivery at one wavefront per SIMD (the k loop takes the MFMA-only loop plus "
+                       "35-50% of the loads-only one), and every wavefront waiting for its first blocks and "
+                       "storing its tile at once: MFMA busy about a quarter of the kernel's time, L2->CU operand "
+                       "traffic 10-25x the unique bytes (rocprofv3 counters in "
                        "profiles/k_gemm_q5_1_large_v3_encoder_m1500.md)",
             "avg_launch_us": round(gemm_ms * 1e3, 2),
             "launch_us_by_launch": per_shape,

@@ -183,6 +183,25 @@ int rw_rocm_matmul_prequant_dev(const rw_weight *w, const void *workspace, size_
 int rw_rocm_matmul_prequant_multi_dev(const rw_weight *const *w, size_t count, const void *workspace, size_t m,
                                       const float *const *bias, float *const *out, void *stream);
 
+/* The encoder MLP's middle (src/encoder.rs:161-171, gelu src/tensor.rs:
+ * 289-305): y = gelu(a W^T + bias) from `workspace` filled by
+ * rw_rocm_quantize_dev (m rows, W's k), quantized (quantize_acts_i8) into
+ * `next_workspace` as rw_rocm_quantize_dev would leave it for y -- ready for
+ * rw_rocm_matmul_prequant_dev with the next weight (k = W's n).  y itself is
+ * never written: the product's epilogue applies the bias and GELU and
+ * quantizes each 32-column block, one more launch builds the next product's
+ * f16 operand, and that operand is bitwise the one rw_rocm_quantize_dev makes
+ * from the f32 y, so the next product's result is too.  The f32 y is never
+ * in memory (at m = 1500, n = 5120 that is 31 MB not written and read back);
+ * on large-v3 the pair costs about what the product, an f32 y and
+ * rw_rocm_quantize_dev cost.  m > 8 (the encoder shape), W's n a multiple of
+ * 32; next_workspace holds rw_rocm_gelu_quantize_workspace_size(m, n) bytes
+ * (0 for shapes it does not take). */
+size_t rw_rocm_gelu_quantize_workspace_size(size_t m, size_t n);
+int rw_rocm_matmul_prequant_gelu_quantize_dev(const rw_weight *w, const void *workspace, size_t m,
+                                              const float *bias, void *next_workspace, size_t next_len,
+                                              void *stream);
+
 /* One entry of a grouped launch: out_g[m_g, n_g] = a_g W_g^T (+ bias_g). */
 typedef struct rw_linear {
     const rw_weight *w;
@@ -289,7 +308,11 @@ int rw_rocm_attention(const float *q, const float *k, const float *v, size_t t_q
  * The workspace (NULL: one kept per (device, stream)) holds
  * rw_rocm_encoder_layer_workspace_size bytes; calls that share it must not
  * overlap.  Outputs within the products' and attention's tolerances of the
- * reference (1e-3 row-L2 per product). */
+ * reference (1e-3 row-L2 per product).  With the environment variable
+ * RW_ENCODER_MLP=fused, fc1's epilogue quantizes gelu(fc1) for fc2 (as
+ * rw_rocm_matmul_prequant_gelu_quantize_dev does) instead of writing it in
+ * f32: bitwise the same output, a few microseconds slower per large-v3
+ * layer. */
 typedef struct rw_encoder_layer {
   const float *attn_ln_w, *attn_ln_b;
   const rw_weight *q, *k, *v, *out;

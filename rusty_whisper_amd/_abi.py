@@ -53,6 +53,9 @@ _SIGNATURES = {
     "rw_rocm_weight_free": (C.c_int, [C.c_void_p]),
     "rw_rocm_weight_info": (C.c_int, [C.c_void_p, C.POINTER(C.c_int), C.POINTER(C.c_size_t),
                                       C.POINTER(C.c_size_t), C.POINTER(C.c_size_t)]),
+    "rw_rocm_gelu_quantize_workspace_size": (C.c_size_t, [C.c_size_t, C.c_size_t]),
+    "rw_rocm_matmul_prequant_gelu_quantize_dev": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p,
+                                                            C.c_void_p, C.c_size_t, C.c_void_p]),
     "rw_rocm_matmul_t_q": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p,
                                      C.c_void_p]),
     "rw_rocm_matmul_t_q_dev": (C.c_int, [C.c_void_p, C.c_void_p, C.c_size_t, C.c_size_t, C.c_void_p,
@@ -254,6 +257,18 @@ def matmul_prequant_multi_dev(weights, workspace, m: int, outs, biases=None, str
     oarr = (C.c_void_p * max(cnt, 1))(*[_ptr(o) for o in outs])
     barr = None if biases is None else (C.c_void_p * max(cnt, 1))(*[_ptr(b) for b in biases])
     check(lib().rw_rocm_matmul_prequant_multi_dev(warr, cnt, _ptr(workspace), m, barr, oarr, stream))
+
+
+def gelu_quantize_workspace_size(m: int, n: int) -> int:
+    return lib().rw_rocm_gelu_quantize_workspace_size(m, n)
+
+
+def matmul_prequant_gelu_quantize_dev(w, workspace, m: int, bias, next_workspace, next_len: int,
+                                      stream: int | None = None) -> None:
+    """gelu(a W^T + bias) from a quantized `workspace`, quantized into
+    `next_workspace` for the next product (rw_rocm_matmul_prequant_gelu_quantize_dev)."""
+    check(lib().rw_rocm_matmul_prequant_gelu_quantize_dev(w.handle, _ptr(workspace), m, _ptr(bias),
+                                                          _ptr(next_workspace), next_len, stream))
 
 
 def matmul_t_f32(a: np.ndarray, b: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:

@@ -71,14 +71,10 @@ __global__ __launch_bounds__(256) void k_layernorm(float *__restrict__ x, int n,
   for (int c = t; c < n; c += 256) yr[c] = (xr[c] - mean) * inv * w[c] + b[c];
 }
 
-// h = gelu(h), the tanh form of src/tensor.rs:289-305 in its order
+// h = gelu(h) (src/tensor.rs:289-305; rw_kernels.hpp's gelu)
 __global__ __launch_bounds__(256) void k_gelu(float *__restrict__ h, size_t n) {
   const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t < n) {
-    const float v = h[t];
-    const float inner = 0.7978846f * (v + 0.044715f * v * v * v);
-    h[t] = 0.5f * v * (1.0f + tanhf(inner));
-  }
+  if (t < n) h[t] = gelu(h[t]);
 }
 
 constexpr int TOPK_MAX = 16;  // candidates per row of the top-k kernels

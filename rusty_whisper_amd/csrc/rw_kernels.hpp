@@ -61,8 +61,6 @@ __device__ inline float ldg_f(const void *p) { return *(const float RW_GLOBAL_AS
 __device__ inline uint32_t ldg_u32(const void *p) { return *(const uint32_t RW_GLOBAL_AS *)p; }
 __device__ inline int32_t ldg_i32(const void *p) { return *(const int32_t RW_GLOBAL_AS *)p; }
 __device__ inline void stg_f(float *p, float v) { *(float RW_GLOBAL_AS *)(void *)p = v; }
-// streaming store (nt policy): output written once, read by a later launch
-__device__ inline void stg_f_nt(float *p, float v) { __builtin_nontemporal_store(v, (float RW_GLOBAL_AS *)(void *)p); }
 __device__ inline void stg_u32(void *p, uint32_t v) { *(uint32_t RW_GLOBAL_AS *)p = v; }
 __device__ inline void stg_u4(void *p, uint4 v) {
   *(rw_u32x4 RW_GLOBAL_AS *)p = rw_u32x4{v.x, v.y, v.z, v.w};
@@ -456,6 +454,19 @@ __global__ __launch_bounds__(256) void k_dequant(WeightView w, int row0, int nro
   for (int e = 0; e < QK; ++e) o[e] = __fadd_rn(__fmul_rn(d, (float)weight_q<DT>(w, g, bl, r, e)), m);
 }
 
+// gelu(t) = 0.5 t (1 + tanh(z)), z = 0.7978846 (t + 0.044715 t^3) (the tanh
+// form of src/tensor.rs:289-305, z in its order), evaluated as
+// t / (1 + e^(-2z)): the same function, since 0.5 (1 + tanh z) =
+// 1 / (1 + e^(-2z)), on the hardware's exp2 and reciprocal (a few f32
+// roundings from the exact value; the tanh form loses more than that to
+// cancellation in 1 + tanh z for negative t).  Large negative t gives -0,
+// large positive t gives t, -inf gives NaN, as the tanh form does.
+__device__ inline float gelu(float t) {
+  const float z = 0.7978846f * (t + 0.044715f * t * t * t);
+  const float e = __builtin_amdgcn_exp2f(z * -2.8853900817779268f);  // e^(-2z)
+  return t * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 // ------------------------------------------------------------- k_quantize
 
 // quantize_acts_i8 (src/quant.rs:691-716) for one 32-element block held by
@@ -711,6 +722,131 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
     }(std::make_integer_sequence<int, NP>{});
   }
   ptot = row_sum(ptot, 2);
+  if (part == 0 && lane == 0) {
+    rs[row] = ldexpf(1.0f, e - 15);
+    ps[row] = ptot;
+  }
+}
+
+// The second half of k_quantize_f16 for rows a GEMM_QUANT epilogue has
+// already quantized: q (int8, [row group][block][32 rows][32]) and each
+// block's largest |y| (am, [row group][block][32 rows]) give the row's
+// exponent e (the largest block maximum),
+// d_a = amax / 127 per block, and the f16 values q_a * (d_a * 2^(15-e)),
+// rs and ps -- every lane, pass and reduction as k_quantize_f16<NP, WPR,
+// false> runs them, so the plane is the one k_quantize_f16 writes for the
+// f32 rows those quants came from, bit for bit.
+template <int NP, int WPR>
+__global__ __launch_bounds__(256) void k_quantize_finish(const int8_t *__restrict__ q, const float *__restrict__ am,
+                                                         int m, int k, int nb, uint16_t *__restrict__ a16,
+                                                         float *__restrict__ rs, float *__restrict__ ps) {
+  static_assert(WPR == 1 || WPR == 2 || WPR == 4, "a workgroup holds whole rows");
+  __shared__ float part_max[4];
+  __shared__ float part_sum[4];
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  constexpr int WPG = 8 * WPR;
+  const int x8 = blockIdx.x & 7, j = blockIdx.x >> 3;
+  const int g = 8 * (j / WPG) + x8;
+  if (g * RG >= ((m + RG - 1) / RG) * RG) return;
+  const int r = (j % WPG) * (4 / WPR) + wv / WPR, part = wv % WPR;
+  const int row = g * RG + r;
+  const int lb = lane >> 3, lt = lane & 7;
+  const auto ro = buffer_rsrc(a16, (uint32_t)((size_t)(m + RG - 1) / RG * RG * (size_t)k * 2));
+  const uint32_t voff = (uint32_t)(a16_index(nb, g, 0, r, 4 * lt) - a16_index(nb, g, 0, 0, 0)) * 2 +
+                        (uint32_t)lb * 2048u;
+  const uint32_t gbase = (uint32_t)a16_index(nb, g, 0, 0, 0) * 2;
+  const bool live = row < m;
+  const int8_t *qr = q + act_slot(nb, g, 0, r) * QK;  // block bl at + bl * RG * QK
+  const float *ar = am + act_slot(nb, g, 0, r);        // block bl at + bl * RG
+  constexpr int CB = 8 * NP * WPR;
+  const int nch = (nb + CB - 1) / CB;
+  auto first = [&](int c, int p) __attribute__((always_inline)) { return c * CB + 8 * (p * WPR + part); };
+  uint32_t qv[NP];
+  float bam[NP];
+  auto load = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int bl = first(c, p) + lb;
+      qv[p] = 0u;
+      bam[p] = 0.0f;
+      if (bl < nb) {
+        qv[p] = ldg_u32(qr + (size_t)bl * (RG * QK) + 4 * lt);
+        bam[p] = ldg_f(ar + (size_t)bl * RG);
+      }
+    }
+  };
+  float amax = 0.0f;
+  if (live) {
+    for (int c = 0; c < nch; ++c) {
+      load(c);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) amax = max_nn(amax, bam[p]);
+    }
+    amax = max_nn(amax, __shfl_xor(amax, 8));
+    amax = max_nn(amax, __shfl_xor(amax, 16));
+    amax = max_nn(amax, __shfl_xor(amax, 32));
+  }
+  if (WPR > 1) {
+    if (lane == 0) part_max[wv] = amax;
+    __syncthreads();
+#pragma unroll
+    for (int jj = 0; jj < WPR; ++jj) amax = max_nn(amax, part_max[wv - part + jj]);
+  }
+  auto row_sum = [&](float t) __attribute__((always_inline)) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) t += __shfl_xor(t, o);
+    if (WPR > 1) {
+      if (lane == 0) part_sum[wv] = t;
+      __syncthreads();
+      t = part_sum[wv - part];
+#pragma unroll
+      for (int jj = 1; jj < WPR; ++jj) t += part_sum[wv - part + jj];
+    }
+    return t;
+  };
+  if (!live) {
+    for (int c = 0; c < nch; ++c)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const int bl = first(c, p) + lb;
+        if (bl < nb) *reinterpret_cast<uint2 *>(a16 + a16_index(nb, g, bl, r, 4 * lt)) = make_uint2(0u, 0u);
+      }
+    row_sum(0.0f);
+    if (part == 0 && lane == 0) {
+      rs[row] = 0.0f;
+      ps[row] = 0.0f;
+    }
+    return;
+  }
+  int e = 15;
+  if (amax > 0.0f && amax <= 3.4028235e38f) {
+    frexpf(amax, &e);
+    e = max(e, -110);
+  }
+  const float down = ldexpf(1.0f, 15 - e);
+  float ptot = 0.0f;
+  for (int c = 0; c < nch; ++c) {
+    if (nch > 1) load(c);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int b0 = first(c, p);
+      if (b0 >= nb) continue;  // uniform
+      const float da = __fdiv_rn(bam[p], 127.0f);
+      const float dd = da * down;
+      const int q0 = (int)(int8_t)(qv[p] & 0xff), q1 = (int)(int8_t)((qv[p] >> 8) & 0xff);
+      const int q2 = (int)(int8_t)((qv[p] >> 16) & 0xff), q3 = (int)(int8_t)(qv[p] >> 24);
+      const int bsum = sum8(q0 + q1 + q2 + q3);
+      if (lt == 0) ptot += __fmul_rn(da, (float)bsum);
+      const h2v lo2 = {(_Float16)__fmul_rn((float)q0, dd), (_Float16)__fmul_rn((float)q1, dd)};
+      const h2v hi2 = {(_Float16)__fmul_rn((float)q2, dd), (_Float16)__fmul_rn((float)q3, dd)};
+      if (b0 + lb < nb) {
+        __builtin_amdgcn_raw_buffer_store_b64(
+            (rw_u32x2){__builtin_bit_cast(uint32_t, lo2), __builtin_bit_cast(uint32_t, hi2)}, ro, voff,
+            gbase + (uint32_t)b0 * 2048u, 0);
+      }
+    }
+  }
+  ptot = row_sum(ptot);
   if (part == 0 && lane == 0) {
     rs[row] = ldexpf(1.0f, e - 15);
     ps[row] = ptot;
@@ -1121,10 +1257,7 @@ __device__ inline void gemv_epilogue(const GemvItem &I, int gw, int h, int r, in
         if (4 * h + v < mr) {
           float t = y[j][v];
           if (I.bias) t = t + bv[j];
-          if (I.flags & 1) {
-            const float inner = 0.7978846f * (t + 0.044715f * t * t * t);
-            t = 0.5f * t * (1.0f + tanhf(inner));
-          }
+          if (I.flags & 1) t = gelu(t);
           if (I.flags & 2) t = x[j][v] + t;
           stg_f(I.out + (size_t)(4 * h + v) * n + col, t);
         }
@@ -1489,19 +1622,23 @@ constexpr int GEMM_MAX_SET = 4;
 // on y = x W^T + b, and accumulation into the output (out += y, the
 // residual add of src/encoder.rs:146-148, 171-173)
 constexpr int GEMM_GELU = 1, GEMM_ACC = 2;
+// GEMM_QUANT: instead of the f32 output, quantize_acts_i8 of each output row
+// block (32 columns of a 32 x 32 tile): the int8 quants into qo and each
+// block's largest |y| into ao, both by (row group, block) as the tiles
+// produce them -- qo [mgroups][n / 32][32 rows][32], ao [mgroups][n / 32][32
+// rows] -- from which k_quantize_finish builds the next product's f16
+// operand (n % 32 == 0)
+constexpr int GEMM_QUANT = 4;
 struct GemmItem {
   GemmPlanes gp;
   const float *bias;
   float *out;
+  int8_t *qo;
+  float *ao;
   int n, ngroups, tile0, flags;
 };
 
-// gelu(t) = 0.5 t (1 + tanh(sqrt(2/pi) (t + 0.044715 t^3))), evaluated in
-// the reference's order
-__device__ inline float gelu_tanh(float t) {
-  const float inner = 0.7978846f * (t + 0.044715f * t * t * t);
-  return 0.5f * t * (1.0f + tanhf(inner));
-}
+
 struct GemmSet {
   GemmItem it[GEMM_MAX_SET];
   int count, nb, nb_pad;
@@ -1535,7 +1672,8 @@ template <int DT, int KW, int TM, bool OFFS, int TN = GEMM_TN>
 __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int m) {
   constexpr int P = GEMM_P, S = P + 1;
   constexpr int RED = KW > 1 ? KW * TM * TN * 16 * 64 * 4 : 16;
-  __shared__ __align__(16) uint8_t lds[RED];
+  constexpr int QROW = 36;  // floats per row of a GEMM_QUANT staging tile (rows 4 apart on other banks)
+  __shared__ __align__(16) uint8_t lds[RED + KW * 32 * QROW * 4];
   const int l = threadIdx.x & 63;
   const int kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = l >> 5, r = l & 31;
@@ -1750,7 +1888,36 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int
     }
     if (flags & GEMM_GELU) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) y[v] = gelu_tanh(y[v]);
+      for (int v = 0; v < 16; ++v) y[v] = gelu(y[v]);
+    }
+    if (flags & GEMM_QUANT) {
+      // The tile's 32 columns are one block of each of its 32 rows in the
+      // next product's input.  Through this wavefront's LDS tile, 8 lanes
+      // take a (row, block) with 4 elements each and quantize it as
+      // quantize_block8 (and k_quantize_f16) does.  A wavefront's LDS
+      // accesses complete in order, so its lanes read what the others wrote.
+      float *stg = reinterpret_cast<float *>(lds + RED) + kw * (32 * QROW);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) stg[(8 * (v >> 2) + 4 * h + (v & 3)) * QROW + r] = y[v];
+      const int lb = l >> 3, lt = l & 7;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int rw = lb + 8 * u, row = tg * RG + rw;
+        const float4 xv = *reinterpret_cast<const float4 *>(stg + rw * QROW + 4 * lt);
+        const float amax = max8_nn(amax4(xv));
+        const float d = __fdiv_rn(amax, 127.0f);
+        const float inv = d > 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+        const uint32_t q = (uint32_t)(round_clamp_i8(__fmul_rn(xv.x, inv)) & 0xff) |
+                           ((uint32_t)(round_clamp_i8(__fmul_rn(xv.y, inv)) & 0xff) << 8) |
+                           ((uint32_t)(round_clamp_i8(__fmul_rn(xv.z, inv)) & 0xff) << 16) |
+                           ((uint32_t)(round_clamp_i8(__fmul_rn(xv.w, inv)) & 0xff) << 24);
+        if (row < m) {
+          const size_t slot = ((size_t)tg * (size_t)(n / RG) + cg) * RG + rw;
+          stg_u32(it.qo + slot * QK + 4 * lt, q);
+          if (lt == 0) stg_f(it.ao + slot, amax);
+        }
+      }
+      continue;
     }
     // lane (h, r) holds rows 8q + 4h + e (e < 4) of column col
     float *o = out + (size_t)(tg * RG + 4 * h) * n + col;
@@ -1763,13 +1930,13 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int
         for (int v = 0; v < 16; ++v) y[v] = x[v] + y[v];
       }
 #pragma unroll
-      for (int v = 0; v < 16; ++v) stg_f_nt(o + (size_t)(8 * (v >> 2) + (v & 3)) * n, y[v]);
+      for (int v = 0; v < 16; ++v) stg_f(o + (size_t)(8 * (v >> 2) + (v & 3)) * n, y[v]);
     } else if (col < n) {
 #pragma unroll
       for (int v = 0; v < 16; ++v)
         if (tg * RG + 4 * h + 8 * (v >> 2) + (v & 3) < m) {
           float *p = o + (size_t)(8 * (v >> 2) + (v & 3)) * n;
-          stg_f_nt(p, (flags & GEMM_ACC) ? *p + y[v] : y[v]);
+          stg_f(p, (flags & GEMM_ACC) ? *p + y[v] : y[v]);
         }
     }
   }

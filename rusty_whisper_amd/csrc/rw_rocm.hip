@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -344,6 +345,42 @@ static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &
   return RW_OK;
 }
 
+// The f16 activation plane (rs, ps) of rows that a GEMM_QUANT epilogue
+// quantized into q ([m][k] int8) and am ([m][k / 32] block maxima):
+// k_quantize_finish with the NP / WPR launch_quantize gives the same k, so
+// the plane is bitwise launch_quantize's for the f32 rows.
+static int launch_quantize_finish(const int8_t *q, const float *am, size_t m, size_t k, const ActLayout &L, void *ws,
+                                  hipStream_t s) {
+  char *b = (char *)ws;
+  if (!L.f16) return fail(RW_EINVAL, "the fused quantization takes m > %d rows", GEMV_MAX_M);
+  if ((size_t)L.mgroups * RG * k * 2 >= ((size_t)1 << 32))
+    return fail(RW_EINVAL, "activation [%zu, %zu] too large for the GEMM layout's 32-bit offsets", m, k);
+  const size_t g8 = align_up((size_t)L.mgroups, 8);
+  uint16_t *a16 = (uint16_t *)(b + L.off_a16);
+  float *rs = (float *)(b + L.off_rs), *ps = (float *)(b + L.off_ps);
+#define RW_QFIN(NP, WPR)                                                                                   \
+  hipLaunchKernelGGL((k_quantize_finish<NP, WPR>), dim3((unsigned)(g8 * RG * WPR / 4)), dim3(256), 0, s, q, am, \
+                     (int)m, (int)k, L.nb, a16, rs, ps)
+  const int passes = (L.nb + 7) / 8;
+  if (passes <= 1) RW_QFIN(1, 1);
+  else if (passes <= 2) RW_QFIN(1, 2);
+  else if (passes <= 4) RW_QFIN(1, 4);
+  else if (passes <= 6) RW_QFIN(3, 2);
+  else if (passes <= 8) RW_QFIN(2, 4);
+  else if (passes <= 20) RW_QFIN(5, 4);
+  else RW_QFIN(8, 4);
+#undef RW_QFIN
+  LAUNCH_TRY("k_quantize_finish");
+  return RW_OK;
+}
+
+// Bytes after the next product's activation layout (m rows, k = n) that the
+// fused GELU + quantization keeps its int8 quants and block maxima in
+static size_t fused_quant_bytes(size_t m, size_t n) {
+  const size_t rows = cdiv(m, RG) * RG;
+  return align_up(rows * n, 256) + align_up(rows * (n / QK) * 4, 256);
+}
+
 #define RW_DISPATCH_DT(dt, FN, ...)                  \
   switch (dt) {                                      \
     case RW_Q4_0: FN<RW_Q4_0>(__VA_ARGS__); break;   \
@@ -445,7 +482,8 @@ static void launch_gemm_dt(const GemmSet &set, size_t tiles, const ActView &av, 
 // k against the quantized activation `av`.  The kernel addresses each plane
 // with 32-bit byte offsets (buffer loads), so every plane stays below 4 GiB.
 static int run_gemm(const rw_weight *const *w, const float *const *bias, float *const *out, size_t count,
-                    const ActView &av, int m, hipStream_t s, const int *flags = nullptr) {
+                    const ActView &av, int m, hipStream_t s, const int *flags = nullptr, int8_t *qo = nullptr,
+                    float *ao = nullptr) {
   const size_t lim = (size_t)1 << 32;
   if ((size_t)av.mgroups * (size_t)w[0]->nb * 2048 >= lim)
     return fail(RW_EINVAL, "activation [%d, %zu] too large for the GEMM's 32-bit offsets", m, w[0]->k);
@@ -465,6 +503,8 @@ static int run_gemm(const rw_weight *const *w, const float *const *bias, float *
     it.n = (int)w[i]->n;
     it.ngroups = w[i]->ngroups;
     it.flags = flags ? flags[i] : 0;
+    it.qo = qo;
+    it.ao = ao;
     it.tile0 = (int)tiles;
     tiles += cdiv(w[i]->ngroups, GEMM_TN);
   }
@@ -1244,7 +1284,7 @@ static LayerLayout layer_layout(size_t n, size_t f, size_t t) {
   L.off_v = align_up(L.off_k + row, 256);
   L.off_a = align_up(L.off_v + row, 256);
   L.off_h = align_up(L.off_a + row, 256);
-  L.off_att = align_up(L.off_h + t * f * 4, 256);
+  L.off_att = align_up(L.off_h + std::max(t * f * 4, fused_quant_bytes(t, f)), 256);
   L.bytes = align_up(L.off_att + L.att.bytes, 256);
   return L;
 }
@@ -1299,9 +1339,24 @@ static int run_encoder_layer(const rw_encoder_layer *E, float *x, size_t t, void
   // x + fc2(gelu(fc1(ln2(x))))
   rc = launch_quantize(x, t, n, Ln, b, s, E->mlp_ln_w, E->mlp_ln_b);
   if (rc) return rc;
-  rc = run_gemm(&E->fc1, &E->fc1_b, &hb, 1, act_view(Ln, b), m, s, &act);
-  if (rc) return rc;
-  rc = launch_quantize(hb, t, f, Lf, b, s);
+  // fc2's activation: by default fc1 writes gelu(y) in f32 and a quantize
+  // launch reads it back; RW_ENCODER_MLP=fused quantizes it in fc1's epilogue
+  // instead (int8 quants and block maxima in h's space, then the f16 plane:
+  // bitwise the same operand; measured 1-2 us per large-v3 layer slower, the
+  // epilogue's quantization costing more than the f32 round trip it saves)
+  const char *mlp = getenv("RW_ENCODER_MLP");
+  if (f % QK == 0 && mlp && !strcmp(mlp, "fused")) {
+    int8_t *qh = (int8_t *)hb;  // [row group][block][32][32], then the block maxima
+    float *ah = (float *)(b + L.off_h + align_up(cdiv(t, RG) * RG * f, 256));
+    const int fq = GEMM_GELU | GEMM_QUANT;
+    rc = run_gemm(&E->fc1, &E->fc1_b, &hb, 1, act_view(Ln, b), m, s, &fq, qh, ah);
+    if (rc) return rc;
+    rc = launch_quantize_finish(qh, ah, t, f, Lf, b, s);
+  } else {
+    rc = run_gemm(&E->fc1, &E->fc1_b, &hb, 1, act_view(Ln, b), m, s, &act);
+    if (rc) return rc;
+    rc = launch_quantize(hb, t, f, Lf, b, s);
+  }
   if (rc) return rc;
   return run_gemm(&E->fc2, &E->fc2_b, &x, 1, act_view(Lf, b), m, s, &acc);
 }
@@ -1553,6 +1608,36 @@ int rw_rocm_matmul_prequant_multi_dev(const rw_weight *const *w, size_t count, c
   }
   ActLayout L = act_layout(m, w[0]->k);
   return run_gemm(w, bias, out, count, act_view(L, (void *)workspace), (int)m, s);
+}
+
+size_t rw_rocm_gelu_quantize_workspace_size(size_t m, size_t n) {
+  if (m <= (size_t)GEMV_MAX_M || n == 0 || n % QK) return 0;
+  return align_up(act_layout(m, n).bytes, 256) + fused_quant_bytes(m, n);
+}
+
+int rw_rocm_matmul_prequant_gelu_quantize_dev(const rw_weight *w, const void *workspace, size_t m,
+                                              const float *bias, void *next_workspace, size_t next_len,
+                                              void *stream) {
+  if (!w) return fail(RW_EINVAL, "weight is NULL");
+  if (m == 0) return RW_OK;
+  if (!workspace || !next_workspace) return fail(RW_EINVAL, "workspace pointer is NULL");
+  if (m <= (size_t)GEMV_MAX_M)
+    return fail(RW_EINVAL, "m = %zu: the fused GELU + quantization takes more than %d rows", m, GEMV_MAX_M);
+  if (m > (size_t)INT32_MAX / 2) return fail(RW_EINVAL, "m = %zu is too large", m);
+  if (w->n % QK) return fail(RW_EINVAL, "n = %zu must be a multiple of %d (the next product's k)", w->n, QK);
+  const size_t need = rw_rocm_gelu_quantize_workspace_size(m, w->n);
+  if (next_len < need) return fail(RW_EINVAL, "next workspace of %zu bytes < %zu needed", next_len, need);
+  HIP_TRY(hipSetDevice(w->device));
+  hipStream_t s = (hipStream_t)stream;
+  const ActLayout Lin = act_layout(m, w->k), Lout = act_layout(m, w->n);
+  char *nx = (char *)next_workspace;
+  int8_t *q = (int8_t *)(nx + align_up(Lout.bytes, 256));
+  float *am = (float *)(nx + align_up(Lout.bytes, 256) + align_up(cdiv(m, RG) * RG * w->n, 256));
+  const int fq = GEMM_GELU | GEMM_QUANT;
+  float *none = nullptr;  // no f32 output in this mode
+  int rc = run_gemm(&w, &bias, &none, 1, act_view(Lin, (void *)workspace), (int)m, s, &fq, q, am);
+  if (rc) return rc;
+  return launch_quantize_finish(q, am, m, w->n, Lout, next_workspace, s);
 }
 
 int rw_rocm_matmul_t_q(const rw_weight *w, const float *a, size_t m, size_t k, const float *bias, float *out) {

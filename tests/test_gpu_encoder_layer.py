@@ -107,3 +107,33 @@ def test_workspace_reuse_and_repeat(torch):
     layer.run(xb, t)
     torch.cuda.synchronize()
     assert np.array_equal(xa.cpu().numpy().view(np.uint32), xb.cpu().numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("t,n,dtype,variant", [(1500, 1280, 7, ""), (200, 512, 8, ""), (37, 256, 2, ""),
+                                               (1500, 768, 8, "outliers"), (9, 384, 3, "spread")],
+                         ids=lambda x: str(x))
+def test_fused_mlp_quantization_is_bitwise_the_separate_one(torch, t, n, dtype, variant):
+    """With RW_ENCODER_MLP=fused, fc1's epilogue quantizes gelu(y) for fc2
+    (int8 quants and block maxima, then the f16 plane); the layer's output
+    equals, bit for bit, the default one with y written in f32 and quantized
+    by its own launch."""
+    import os
+
+    heads, f = n // 64, 4 * n
+    p, dev = build(torch, n, f, dtype, seed=3 * t + n, spread=variant == "spread")
+    x = np.random.default_rng(t + 1).standard_normal((t, n)).astype(np.float32)
+    if variant == "outliers":
+        x[:, np.random.default_rng(n).choice(n, size=max(1, n // 100), replace=False)] *= np.float32(20.0)
+    layer = A.EncoderLayer(heads, **dev)
+    outs = []
+    for fused in (True, False):
+        if fused:
+            os.environ["RW_ENCODER_MLP"] = "fused"
+        try:
+            xd = torch.from_numpy(x).to("cuda:0")
+            layer.run(xd, t)
+            torch.cuda.synchronize()
+        finally:
+            os.environ.pop("RW_ENCODER_MLP", None)
+        outs.append(xd.cpu().numpy())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
