@@ -1815,6 +1815,27 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int
     cv[cc] = ldg_f(gp.cs + wr);
     if (OFFS) mv[cc] = offs ? ldg_f(cmp + wr) : 0.0f;
   }
+  // GEMM_ACC: the output values this wavefront adds to, requested here with
+  // the other epilogue inputs where they fit (at most 2 tiles: 32 values per
+  // lane), so no load waits behind the epilogue's stores (stores count in
+  // the same counter); only this wavefront touches its tiles' outputs
+  constexpr bool XPRE = RPW * CPW <= 2;
+  float xpre[XPRE ? RPW : 1][XPRE ? CPW : 1][16];
+  auto load_res = [&](int rr, int cc, float (&x)[16]) __attribute__((always_inline)) {
+    const int tg = by * TM + i0 + rr, cg = bx * TN + j0 + cc, col = cg * RG + r;
+    const bool ok = tg < a.mgroups && cg < ngroups && col < n;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int row = tg * RG + 4 * h + 8 * (v >> 2) + (v & 3);
+      x[v] = ok && row < m ? ldg_f(out + (size_t)row * n + col) : 0.0f;
+    }
+  };
+  if (XPRE && (flags & GEMM_ACC)) {
+#pragma unroll
+    for (int rr = 0; rr < (XPRE ? RPW : 1); ++rr)
+#pragma unroll
+      for (int cc = 0; cc < (XPRE ? CPW : 1); ++cc) load_res(rr, cc, xpre[rr][cc]);
+  }
   // the last nsw - s (< S) blocks are already in st[0 ..]
 #pragma unroll
   for (int u = 0; u < S - 1; ++u)
@@ -1919,25 +1940,27 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int
       }
       continue;
     }
+    if (flags & GEMM_ACC) {
+      // x + y: the tile's 16 values loaded (early, or all before any store)
+      float x[16];
+      if constexpr (XPRE) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) x[v] = xpre[XPRE ? rr : 0][XPRE ? cc : 0][v];
+      } else {
+        load_res(rr, cc, x);
+      }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) y[v] = x[v] + y[v];
+    }
     // lane (h, r) holds rows 8q + 4h + e (e < 4) of column col
     float *o = out + (size_t)(tg * RG + 4 * h) * n + col;
     if (rows_full && (cg + 1) * RG <= n) {
-      if (flags & GEMM_ACC) {
-        float x[16];
-#pragma unroll
-        for (int v = 0; v < 16; ++v) x[v] = o[(size_t)(8 * (v >> 2) + (v & 3)) * n];
-#pragma unroll
-        for (int v = 0; v < 16; ++v) y[v] = x[v] + y[v];
-      }
 #pragma unroll
       for (int v = 0; v < 16; ++v) stg_f(o + (size_t)(8 * (v >> 2) + (v & 3)) * n, y[v]);
     } else if (col < n) {
 #pragma unroll
       for (int v = 0; v < 16; ++v)
-        if (tg * RG + 4 * h + 8 * (v >> 2) + (v & 3) < m) {
-          float *p = o + (size_t)(8 * (v >> 2) + (v & 3)) * n;
-          stg_f(p, (flags & GEMM_ACC) ? *p + y[v] : y[v]);
-        }
+        if (tg * RG + 4 * h + 8 * (v >> 2) + (v & 3) < m) stg_f(o + (size_t)(8 * (v >> 2) + (v & 3)) * n, y[v]);
     }
   }
 }
