@@ -728,6 +728,190 @@ __global__ __launch_bounds__(256) void k_quantize_f16(const float *__restrict__ 
   }
 }
 
+// The maximum over each quad of lanes of values that are >= +0 and not NaN
+// (integer DPP maxima, as max8_nn)
+__device__ inline float max4_nn(float b) {
+  int v = __float_as_int(b);
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false));  // quad_perm [1,0,3,2]
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false));  // quad_perm [2,3,0,1]
+  return __int_as_float(v);
+}
+// lane S of each quad's value, in every lane of the quad (DPP quad_perm)
+template <int S>
+__device__ inline float quad_bcast(float v) {
+  constexpr int CTRL = S | (S << 2) | (S << 4) | (S << 6);
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// the value of the lane N above within each row of 16 lanes: DPP row_ror
+// by 16 - N (lane i reads lane (i + N) mod 16)
+template <int N>
+__device__ inline float row_next(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + (16 - N), 0xf, 0xf, false));
+}
+
+// k_quantize_f16<NP, WPR, false> with R = 4 or 8 rows per wavefront: the
+// same plane, rs and ps, bit for bit, written in runs of R rows.  The plane
+// holds a block's 16-byte pieces of the 32 rows of a row group next to each
+// other (a16_index), so a lane that owns 8 consecutive elements of one row
+// stores 16 bytes, and the R lanes holding the same piece of R consecutive
+// rows store R x 16 contiguous bytes; k_quantize_f16's lanes store 8-byte
+// pieces of one row, 32 separate pieces per instruction, which costs the L2
+// four to eight times the write requests (2 us of the 15 us at
+// k = 5120, m = 1500).
+// A workgroup holds R rows and WPR x SW wavefronts.  Wavefront w = P SW + s
+// takes part P of each row as k_quantize_f16 deals it (blocks
+// 8 (p WPR + P) + lb, p < NP) and of those the blocks lb in
+// [LB s, LB s + LB), LB = 8 / SW, for all R rows; lane = L rr + 4 jb + q
+// (L = 64 / R lanes per row) holds elements 8q..8q+7 of block jb of a pass
+// of BP = L / 4 blocks.  The quantization of each element is
+// k_quantize_f16's.  The row's ps sums the same per-block terms in the same
+// tree: a lane's accumulator u runs over p in order as k_quantize_f16's
+// lane does; the pairs (lb, lb ^ 1), then (lb, lb ^ 2), then (lb, lb ^ 4) of
+// its shuffle tree are formed here across jb (DPP), across the
+// accumulators, or across the wavefronts s (LDS), in the same pairing; the
+// parts P are added in order.  Each quad's lanes divide for the passes
+// h = q (mod 4) and pass the results by DPP.
+template <int R, int NP, int WPR, int SW>
+__global__ __launch_bounds__(64 * WPR * SW) void k_quantize_f16_rows(const float *__restrict__ a, int m, int k, int nb,
+                                                                     uint16_t *__restrict__ a16, float *__restrict__ rs,
+                                                                     float *__restrict__ ps) {
+  static_assert(R == 4 || R == 8, "4 or 8 rows per wavefront");
+  static_assert(WPR == 2 || WPR == 4, "parts of k_quantize_f16<NP, WPR>");
+  constexpr int L = 64 / R, BP = L / 4, NW = WPR * SW, LB = 8 / SW;
+  static_assert(SW >= 1 && LB % BP == 0, "a wavefront's blocks of a group are whole passes");
+  constexpr int U = LB / BP, H = NP * U, RPG = RG / R;
+  __shared__ int smax[NW][R];
+  __shared__ float ssum[NW][R];
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int P = w / SW, s = w % SW;
+  // workgroup 8j + x runs on XCD x; the RPG workgroups of a row group all
+  // take the same x, so the group's plane lines are written through one L2
+  const int x8 = blockIdx.x & 7, j = blockIdx.x >> 3;
+  const int g = 8 * (j / RPG) + x8;
+  if (g * RG >= ((m + RG - 1) / RG) * RG) return;  // a slot past the last row group (whole workgroup)
+  const int rr = lane / L, jb = (lane % L) >> 2, q = lane & 3;
+  const int r = (j % RPG) * R + rr, row = g * RG + r;
+  const bool live = row < m;  // rows >= m of the last row group are written as zeros
+  const float *x = a + (size_t)row * k;
+  // first block of pass h: group p = h / U of part P, blocks lb = LB s + BP (h % U) + jb
+  auto blk0 = [&](int h) __attribute__((always_inline)) { return 8 * ((h / U) * WPR + P) + LB * s + BP * (h % U); };
+  float4 v[H][2];
+#pragma unroll
+  for (int h = 0; h < H; ++h) {
+    const int bl = blk0(h) + jb;
+    v[h][0] = v[h][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live && bl < nb) {
+      v[h][0] = ldg_f4(x + (size_t)bl * QK + 8 * q);
+      v[h][1] = ldg_f4(x + (size_t)bl * QK + 8 * q + 4);
+    }
+  }
+  // block maxima (in every lane of the block's quad) and the row's largest |x|
+  float bm[H];
+  int amx = 0;
+#pragma unroll
+  for (int h = 0; h < H; ++h) {
+    bm[h] = max4_nn(max_nn(amax4(v[h][0]), amax4(v[h][1])));
+    amx = max(amx, __float_as_int(bm[h]));
+  }
+  if constexpr (L == 16) {
+    amx = max(amx, __float_as_int(row_next<4>(__int_as_float(amx))));
+    amx = max(amx, __float_as_int(row_next<8>(__int_as_float(amx))));
+  } else {
+    amx = max(amx, __builtin_amdgcn_update_dpp(0, amx, 0x141, 0xf, 0xf, false));  // row_half_mirror: the other quad
+  }
+  if (lane % L == 0) smax[w][rr] = amx;
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < NW; ++u) amx = max(amx, smax[u][rr]);
+  const float amax = __int_as_float(amx);
+  int e = 15;  // zero, inf or NaN rows: no scaling
+  if (amax > 0.0f && amax <= 3.4028235e38f) {
+    frexpf(amax, &e);  // amax in [2^(e-1), 2^e)
+    e = max(e, -110);
+  }
+  const float down = ldexpf(1.0f, 15 - e);
+  constexpr int ND = (H + 3) / 4;
+  float dv[ND], iv[ND];
+#pragma unroll
+  for (int i = 0; i < ND; ++i) {
+    float b = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      if (4 * i + t < H) b = q == t ? bm[4 * i + t] : b;
+    dv[i] = __fdiv_rn(b, 127.0f);
+    iv[i] = dv[i] > 0.0f ? __fdiv_rn(1.0f, dv[i]) : 0.0f;
+  }
+  const auto ro = buffer_rsrc(a16, (uint32_t)((size_t)(m + RG - 1) / RG * RG * (size_t)k * 2));
+  const uint32_t voff = (uint32_t)(a16_index(nb, 0, jb, r, 8 * q) * 2);
+  const uint32_t gbase = (uint32_t)a16_index(nb, g, 0, 0, 0) * 2;
+  float acc[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) acc[u] = 0.0f;
+  auto pass = [&](auto hc) __attribute__((always_inline)) {
+    constexpr int h = decltype(hc)::value;
+    const int b0 = blk0(h);
+    if (b0 >= nb) return;  // uniform
+    const float da = quad_bcast<h & 3>(dv[h >> 2]);
+    const float inv = quad_bcast<h & 3>(iv[h >> 2]);
+    const float dd = da * down;
+    const float xs[8] = {v[h][0].x, v[h][0].y, v[h][0].z, v[h][0].w, v[h][1].x, v[h][1].y, v[h][1].z, v[h][1].w};
+    int qv[8], sq = 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      qv[u] = round_clamp_i8(__fmul_rn(xs[u], inv));
+      sq += qv[u];
+    }
+    // the block's sum(q_a) (exact integers), times d_a
+    sq += __builtin_amdgcn_update_dpp(0, sq, 0xB1, 0xf, 0xf, false);
+    sq += __builtin_amdgcn_update_dpp(0, sq, 0x4E, 0xf, 0xf, false);
+    acc[h % U] += __fmul_rn(da, (float)sq);
+    uint32_t wd[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const h2v t2 = {(_Float16)__fmul_rn((float)qv[2 * u], dd), (_Float16)__fmul_rn((float)qv[2 * u + 1], dd)};
+      wd[u] = __builtin_bit_cast(uint32_t, t2);
+    }
+    if (b0 + jb < nb)
+      __builtin_amdgcn_raw_buffer_store_b128((rw_u32x4){wd[0], wd[1], wd[2], wd[3]}, ro, voff,
+                                             gbase + (uint32_t)b0 * 2048u, 0);
+  };
+  [&]<int... Hs>(std::integer_sequence<int, Hs...>) {
+    (pass(std::integral_constant<int, Hs>{}), ...);
+  }(std::make_integer_sequence<int, H>{});
+  // ps: pairs across jb (the block 4 lanes above, then 8 above), then
+  // across the accumulators, then across the wavefronts s, then the parts
+  float xu[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float t = acc[u];
+    if constexpr (BP == 4) {
+      t = t + row_next<4>(t);
+      t = t + row_next<8>(t);
+    } else {
+      t = t + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t), 0x104, 0xf, 0xf, false));  // row_shl:4
+    }
+    xu[u] = t;
+  }
+  float y = xu[0];
+  if constexpr (U == 2) y = xu[0] + xu[1];
+  if constexpr (U == 4) y = (xu[0] + xu[1]) + (xu[2] + xu[3]);
+  if (lane % L == 0) ssum[w][rr] = y;
+  __syncthreads();
+  if (w == 0 && lane % L == 0) {
+    auto part_total = [&](int p) __attribute__((always_inline)) {
+      const float *t = &ssum[p * SW][0];
+      if constexpr (SW == 1) return t[rr];
+      else if constexpr (SW == 2) return t[rr] + t[R + rr];
+      else return (t[rr] + t[R + rr]) + (t[2 * R + rr] + t[3 * R + rr]);
+    };
+    float tot = part_total(0);
+#pragma unroll
+    for (int p = 1; p < WPR; ++p) tot = tot + part_total(p);
+    rs[row] = live ? ldexpf(1.0f, e - 15) : 0.0f;
+    ps[row] = live ? tot : 0.0f;
+  }
+}
+
 // The second half of k_quantize_f16 for rows a GEMM_QUANT epilogue has
 // already quantized: q (int8, [row group][block][32 rows][32]) and each
 // block's largest |y| (am, [row group][block][32 rows]) give the row's

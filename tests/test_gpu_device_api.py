@@ -304,6 +304,18 @@ def test_gemm_activation_plane_bit_exact(torch, k):
     assert np.array_equal(plane[:m], want.view(np.uint16)), np.argwhere(plane[:m] != want.view(np.uint16))[:5]
     assert np.array_equal(rs[:m].view(np.uint32), want_rs.view(np.uint32))
     assert not plane[m:].any() and not rs[m:].any()  # padding rows of the last row group
+    # ps: the row's sum over blocks of d_a * sum(q_a) (the min term's
+    # activation factor), each product rounded once and summed in f32
+    off_ps = (off_rs + rows * 4 + 255) // 256 * 256
+    ps = raw[off_ps:off_ps + rows * 4].view(np.float32)
+    with np.errstate(all="ignore"):
+        q, d, s = O.quantize_acts(a)
+        terms = (d * s.astype(np.float32)).astype(np.float64)
+    fin = np.all(np.isfinite(terms), axis=1)
+    want_ps = terms.sum(axis=1)
+    tol = terms.shape[1] * 2.0 ** -23 * np.abs(terms).sum(axis=1)
+    assert np.all(np.abs(ps[:m][fin] - want_ps[fin]) <= tol[fin]), np.argwhere(np.abs(ps[:m] - want_ps) > tol)[:5]
+    assert not ps[m:].any()
 
 
 # (dtype, m, [n_i], k, [has bias]): q/k/v of the large-v3 encoder, ragged
