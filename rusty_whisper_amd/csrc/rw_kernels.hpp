@@ -1797,6 +1797,11 @@ __device__ inline void weight_f16(uint4 qb, uint32_t dmw, v8h &b0, v8h &b1) {
 }
 
 constexpr int GEMM_TN = 2, GEMM_P = 2;
+// blocks in flight for 64-row tiles (skinny launches: a few wavefronts
+// per column tile, each a chain of block loads, so latency-bound)
+#ifndef GEMM_P_SKINNY
+#define GEMM_P_SKINNY 4
+#endif
 
 // The weights of one k_gemm launch (all of one dtype and k, against one
 // quantized activation): column tiles [tile0, tile0 + cdiv(ngroups, TN)) of
@@ -1854,7 +1859,7 @@ struct GemmSet {
 // how a row is summed, so a row's result never depends on m.
 template <int DT, int KW, int TM, bool OFFS, int TN = GEMM_TN>
 __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int m) {
-  constexpr int P = GEMM_P, S = P + 1;
+  constexpr int P = TM <= 2 ? GEMM_P_SKINNY : GEMM_P, S = P + 1;
   constexpr int RED = KW > 1 ? KW * TM * TN * 16 * 64 * 4 : 16;
   constexpr int QROW = 36;  // floats per row of a GEMM_QUANT staging tile (rows 4 apart on other banks)
   __shared__ __align__(16) uint8_t lds[RED + KW * 32 * QROW * 4];
