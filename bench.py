@@ -987,6 +987,14 @@ def main() -> int:
             torch.cuda.empty_cache()
         legs["c5_turbo_encoder_m12000_q5_1"], Wt = leg_encoder(A, synth, torch, dtype, 12000, 2, 1, 5,
                                                                layers_w=W["layers"], name="turbo M=12000")
+        if not args.no_kernel_timing:
+            # k_gemm alone at M = 12000: the same per-launch-type bursts as the headline's
+            t_ms, t_ops, _, t_per = time_gemm_kernel(A, torch, Wt, stream, reps=1)
+            legs["c5_turbo_encoder_m12000_q5_1"]["k_gemm"] = {
+                "avg_launch_us": round(t_ms * 1e3, 2), "TFLOP_per_s": round(t_ops / (t_ms * 1e-3) / 1e12, 1),
+                "launch_us_by_launch": t_per,
+                "note": "per launch type, the 32 layers' launches back to back in a replayed HIP graph"}
+            log(f"turbo M=12000 k_gemm: {t_ms * 1e3:.1f} us average launch, {t_per}")
         del Wt
         torch.cuda.empty_cache()
         t = leg_turbo_decoder(A, synth, torch, W["layers"], steps, 6)
