@@ -4,7 +4,9 @@ Bars (written in each test):
   * the encoder GEMM's activation plane (m > 8) holds, bit for bit, the f16
     values f16(q_a * f32(d_a * 2^(15-e))) of quantize_acts_i8's q_a and d_a,
     with 2^(e-1) <= the row's largest |x| < 2^e (e >= -110; 15 for zero or
-    non-finite rows), and the row scales 2^(e-15);
+    non-finite rows), the row scales 2^(e-15), and the row sums
+    ps = sum over blocks of d_a * sum(q_a) within nb * 2^-23 of their
+    float64 value (relative to the sum of the terms' magnitudes);
   * one launch for several weights on one quantized input matches the
     oracle (1e-3 row-L2, and the regime's bound against the exact float64
     combination), its rows do not depend on m, and in the decode shape it
@@ -283,11 +285,14 @@ def _a16_index(m, k):
     return (g * nb + bl) * 1024 + (e >> 4) * 512 + (32 * ((e >> 3) & 1) + r) * 8 + (e & 7)
 
 
-@pytest.mark.parametrize("k", [32, 96, 416, 1024, 1280, 2048, 5120, 8224, 16384])
+@pytest.mark.parametrize("k", [32, 96, 416, 1024, 1056, 1280, 1568, 2048, 2080, 4128, 5120, 8224, 16384])
 def test_gemm_activation_plane_bit_exact(torch, k):
-    # one, two and four wavefronts per row (416: two of one pass; 1280: two
-    # of three passes; 1024, 2048 and 5120: four); 8224 and 16384 take the
-    # long-row path (the row is read twice)
+    # one, two and four wavefronts per row (416: two of one pass; 1024: four);
+    # rows of 5-20 passes store in row runs (1280: 8 rows per wavefront, two
+    # parts of three passes; 2048 and 5120: 4 rows, four parts), including
+    # ragged block counts whose last pass is partly past the row (1056, 1568,
+    # 2080, 4128: 33, 49, 65, 129 blocks); 8224 and 16384 take the long-row
+    # path (the row is read twice)
     a = np.concatenate([activations(21, k, seed=k, outliers=0.01), edge_activation_rows(k), _scale_rows(k)])
     m = a.shape[0]
     assert m > 8  # the encoder (f16) layout
