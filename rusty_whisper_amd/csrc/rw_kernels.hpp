@@ -1448,6 +1448,112 @@ __device__ inline void gemv_epilogue(const GemvItem &I, int gw, int h, int r, in
   }
 }
 
+// Activation values held in registers by gemv_tile for rows of at most 64
+// blocks: pair rb = 32 u + t / 8 of the rows' (block, row) pairs,
+// block-major (the fill's order), lane t % 8 holding elements 4 (t % 8) ..
+// + 3 of it; NUX = 2 MR passes cover every pair.
+//
+// Layernorm statistics of the MR rows from those registers: each block's 32
+// values summed by its 8 lanes in a fixed tree (DPP), the block sums of a row
+// (at most 64, through the start of LDS) then by one wavefront's 64 lanes in
+// a fixed tree.  The order depends neither on MR nor on which thread holds a
+// block, so a row's mean and inverse deviation are the same bits in every
+// launch of every row count.  Mean to ln[i], 1 / sqrt(var + 1e-5) to
+// ln[GEMV_MR_MAX + i] (src/tensor.rs:274-287).  All threads call it; it ends
+// with a barrier, after which the block sums' LDS is free.
+template <int MR, int NUX>
+__device__ inline void gemv_ln_stats_regs(const float4 (&xr)[NUX], int nb, uint8_t *lds, int t, float *ln) {
+  const int lt = t & 7, l = t & 63, wv = t >> 6;
+  const int total = MR * nb;
+  const float K = (float)(nb * QK);
+  float *sb = reinterpret_cast<float *>(lds);  // [MR][64] block sums
+  auto row_sums = [&](auto val, auto fin) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < NUX; ++u) {
+      if (32 * u + 8 * wv >= total) continue;  // the wavefront's 8 pairs of pass u are all past the end (uniform)
+      const int rb = 32 * u + (t >> 3);
+      const int row = rb - (rb / MR) * MR;
+      float v = rb < total ? val(u, row) : 0.0f;
+      v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xf, 0xf, false));
+      v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xf, 0xf, false));
+      v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xf, 0xf, false));
+      if (rb < total && lt == 0) sb[row * 64 + rb / MR] = v;
+    }
+    __syncthreads();
+    for (int i = wv; i < MR; i += 4) {
+      float a = l < nb ? sb[i * 64 + l] : 0.0f;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) a += __shfl_xor(a, o);
+      if (l == 0) fin(i, a);
+    }
+    __syncthreads();
+  };
+  row_sums([&](int u, int) __attribute__((always_inline)) { return (xr[u].x + xr[u].y) + (xr[u].z + xr[u].w); },
+           [&](int i, float a) __attribute__((always_inline)) { ln[i] = __fdiv_rn(a, K); });
+  row_sums(
+      [&](int u, int row) __attribute__((always_inline)) {
+        const float m0 = ln[row];
+        const float d0 = xr[u].x - m0, d1 = xr[u].y - m0, d2 = xr[u].z - m0, d3 = xr[u].w - m0;
+        return (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+      },
+      [&](int i, float a) __attribute__((always_inline)) {
+        ln[GEMV_MR_MAX + i] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(a, K) + 1e-5f));
+      });
+}
+
+// The records of a one-chunk launch (the whole k in LDS) from the values in
+// registers: with I.lnw the rows are layernormed first, (x - mean) * inv * w
+// + b as gemv_fill applies it; the quantization is quantize_block8's, so the
+// records are gemv_fill's bit for bit.  A block's record goes to the slots
+// of the k part that holds its octet (part pp: octets [noct pp >> lks,
+// noct (pp+1) >> lks), slots from pp * ch * OCT); the blocks past nb in the
+// last octet get zero records.  The slots' parts that no record fills are
+// gemv_zero_slots' work.
+template <int DT, int MR, int NUX>
+__device__ inline void gemv_records_regs(const GemvItem &I, int nb, int noct, int lks, int ch, uint8_t *lds, int t,
+                                         const float4 (&xr)[NUX], const float *ln) {
+  constexpr int REC = gemv_rec_bytes(MR), SO = 32 * MR + 16, DO = SO + 32, PO = DO + 32;
+  constexpr int OFF = DT == 2 ? 8 : DT == 6 ? 16 : 0;
+  const int lt = t & 7;
+  const int total = MR * nb;
+#pragma unroll
+  for (int u = 0; u < NUX; ++u) {
+    if (32 * u + 8 * (t >> 6) >= total) continue;  // uniform, as in the statistics
+    const int rb = 32 * u + (t >> 3);
+    const int lb = rb / MR, i = rb - lb * MR;
+    float4 x = xr[u];
+    if (I.lnw && rb < total) {
+      const float m0 = ln[i], v0 = ln[GEMV_MR_MAX + i];
+      const size_t e = (size_t)lb * QK + 4 * lt;
+      const float4 w4 = ldg_f4(I.lnw + e), b4 = ldg_f4(I.lnb + e);
+      x.x = (x.x - m0) * v0 * w4.x + b4.x;
+      x.y = (x.y - m0) * v0 * w4.y + b4.y;
+      x.z = (x.z - m0) * v0 * w4.z + b4.z;
+      x.w = (x.w - m0) * v0 * w4.w + b4.w;
+    }
+    const BlockQuant bq = quantize_block8(x);  // every lane of the wavefront takes part in its DPP moves
+    if (rb < total) {
+      const int o = lb >> 3;
+      int pp = 0;
+#pragma unroll
+      for (int q = 1; q < 4; ++q)
+        if (q < (1 << lks) && o >= ((noct * q) >> lks)) pp = q;
+      uint8_t *rec = lds + ((size_t)pp * ch * OCT + (lb - 8 * ((noct * pp) >> lks))) * REC;
+      *reinterpret_cast<uint32_t *>(rec + 32 * i + mfma_pos(4 * lt)) = pack_q4(bq);
+      if (lt == 0) {
+        *reinterpret_cast<int *>(rec + SO + 4 * i) = -OFF * bq.sum;
+        *reinterpret_cast<float *>(rec + DO + 4 * i) = bq.d;
+        *reinterpret_cast<float *>(rec + PO + 4 * i) = __fmul_rn(bq.d, (float)bq.sum);
+      }
+    }
+  }
+  // the last part's blocks past nb (the tail of its last octet): zero records
+  const int pl = (1 << lks) - 1, c0l = (noct * pl) >> lks;
+  const int dead = noct * OCT - nb;
+  uint4 *dz = reinterpret_cast<uint4 *>(lds + ((size_t)pl * ch * OCT + (nb - 8 * c0l)) * REC);
+  for (int z = t; z < dead * (REC / 16); z += 256) dz[z] = make_uint4(0, 0, 0, 0);
+}
+
 // One tile of k_gemv: item I's tile wt.y (every wavefront of the workgroup
 // calls it; LDS is free on entry and in use on return).  PD > 1: the
 // latency form for launches of at most one wavefront per SIMD, whose
@@ -1499,6 +1605,27 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
   // always can; fills can for Q4_0, and for Q4_1 and Q5_0 at one row (the
   // other forms would spill)
   constexpr bool EARLY = PD > 1 || GROUPED || DT == 2 || (MR == 1 && (DT == 3 || DT == 6));
+  // Activation values in registers (gemv_ln_stats_regs' layout) for rows of
+  // at most 64 blocks: the layernorm statistics come from them, and the
+  // latency form at one row (RX) builds its records from them as well, one
+  // read of the row instead of two; it requests them first of all.
+  constexpr int NUX = GROUPED ? 1 : 2 * MR;
+  constexpr bool RX = PD > 1 && !GROUPED && MR == 1;
+  const bool xin = !GROUPED && I.a != nullptr && nb <= 64 && (I.lnw != nullptr || RX);  // uniform
+  const bool regs = RX && xin;
+  float4 xr[NUX];
+  auto load_x = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < NUX; ++u) {
+      const int rb = 32 * u + (t >> 3);
+      xr[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (rb < MR * nb) {
+        const int lb = rb / MR, i = rb - lb * MR;
+        xr[u] = ldg_f4(I.a + ((size_t)i * nb + lb) * QK + 4 * (t & 7));
+      }
+    }
+  };
+  if (regs) load_x();
   GemvOct<DT, NG> ring[PD];
   GemvOct<DT, NG> &cur = ring[0];
   if (EARLY) {
@@ -1523,10 +1650,15 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
 
   // layernorm statistics of the m activation rows (single / set launches
   // with I.lnw): every workgroup computes them, in the same tree order, and
-  // keeps them in LDS for the fills
+  // keeps them in LDS for the fills; rows of at most 64 blocks from the
+  // values in registers (fixed per-block and per-row trees), longer rows by
+  // the loop below
   __shared__ float ln_s[2 * GEMV_MR_MAX];
   if constexpr (!GROUPED) {
-    if (I.lnw) {
+    if (I.lnw && xin) {
+      if (!regs) load_x();
+      gemv_ln_stats_regs<MR, NUX>(xr, nb, lds, t, ln_s);
+    } else if (I.lnw) {
       const int K = nb * QK;
       float *sred = reinterpret_cast<float *>(lds);  // [4 wavefronts][MR], before any record
       auto row_sums = [&](float (&v)[MR]) __attribute__((always_inline)) {
@@ -1560,47 +1692,15 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
         return a;
       };
       float acc_s[MR], mean[MR];
-      if (K <= 8 * 256) {
-        // one round of 8 values per thread: kept in registers for the
-        // squared deviations (the same sums, in the same order, as below)
-        float xv[MR][8];
 #pragma unroll
-        for (int i = 0; i < MR; ++i)
+      for (int i = 0; i < MR; ++i) acc_s[i] = thread_sum(I.a + (size_t)i * K, 0.0f, false);
+      row_sums(acc_s);
 #pragma unroll
-          for (int u = 0; u < 8; ++u) xv[i][u] = t + 256 * u < K ? I.a[(size_t)i * K + t + 256 * u] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < MR; ++i) {
-          float a = 0.0f;
-#pragma unroll
-          for (int u = 0; u < 8; ++u)
-            if (t + 256 * u < K) a += xv[i][u];
-          acc_s[i] = a;
-        }
-        row_sums(acc_s);
-#pragma unroll
-        for (int i = 0; i < MR; ++i) {
-          mean[i] = __fdiv_rn(acc_s[i], (float)K);
-          float a = 0.0f;
-#pragma unroll
-          for (int u = 0; u < 8; ++u)
-            if (t + 256 * u < K) {
-              const float d = xv[i][u] - mean[i];
-              a += d * d;
-            }
-          acc_s[i] = a;
-        }
-        row_sums(acc_s);
-      } else {
-#pragma unroll
-        for (int i = 0; i < MR; ++i) acc_s[i] = thread_sum(I.a + (size_t)i * K, 0.0f, false);
-        row_sums(acc_s);
-#pragma unroll
-        for (int i = 0; i < MR; ++i) {
-          mean[i] = __fdiv_rn(acc_s[i], (float)K);
-          acc_s[i] = thread_sum(I.a + (size_t)i * K, mean[i], true);
-        }
-        row_sums(acc_s);
+      for (int i = 0; i < MR; ++i) {
+        mean[i] = __fdiv_rn(acc_s[i], (float)K);
+        acc_s[i] = thread_sum(I.a + (size_t)i * K, mean[i], true);
       }
+      row_sums(acc_s);
       if (t == 0) {
 #pragma unroll
         for (int i = 0; i < MR; ++i) {
@@ -1644,9 +1744,12 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
           for (int u = 0; u < RB; ++u)
             if (z0 + 256 * u < total) reinterpret_cast<uint4 *>(base)[z0 + 256 * u] = rv[u];
         }
-      } else {
+      } else if (!regs) {
         gemv_fill<DT, MR, (PD > 1 && MR == 1 ? 8 : 4)>(I, nb, c0, c1, base, t, ln_s);
       }
+    }
+    if constexpr (RX) {
+      if (regs) gemv_records_regs<DT, MR, NUX>(I, nb, w.noct, lks, ch, lds, t, xr, ln_s);
     }
     __syncthreads();
 
