@@ -7,7 +7,12 @@
 
 Every GPU translation unit is compiled with packed-FP32 instructions
 disabled and without FP contraction (the kernels call fma explicitly where
-they want one, so results do not depend on what the compiler fuses).
+they want one, so results do not depend on what the compiler fuses), and
+with the leading kernel arguments preloaded into SGPRs at wave launch
+(gfx950 kernarg preloading; the code object keeps the prologue that loads
+them itself where the firmware does not preload): a wave's first scalar
+loads of its arguments leave the start of every launch, which the decoder's
+chains of small launches and the encoder's 256-launch step feel.
 """
 from __future__ import annotations
 
@@ -35,6 +40,7 @@ HIP_FLAGS = [
     "-shared",
     "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-result",
     "-Wno-unused-command-line-argument",
