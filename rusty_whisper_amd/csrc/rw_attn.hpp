@@ -44,6 +44,7 @@ constexpr int ATT_QB = 32 * ATT_QT;
 #define ATT_MAX_SPLIT_N 32
 #endif
 constexpr int ATT_MAX_SPLIT = ATT_MAX_SPLIT_N;  // kv runs of one (query block, head) at most
+static_assert(ATT_MAX_SPLIT < 128, "k_attn packs the run count into 7 bits");
 
 // kv index (within a 16-block) stored at position p of the v^T plane: the
 // middle quads swap (an involution)
@@ -371,11 +372,18 @@ __device__ inline void att_split_v(const AttVRaw &x, AttV &o) {
 // here as well (the P planes are unused): calls of one query block (a
 // decoding step's self-attention over its cache) then need no split launch;
 // the operands are the planes' values, so the results are the same bits.
+// The scalars and row pointers lead the arguments: the first 14 dwords
+// arrive in SGPRs when the waves start (kernarg preloading), so a decoding
+// step's attention requests its rows without first reading the argument
+// block; the planes (P) follow.  The grid comes as arguments too (gridDim
+// is read from the argument block): nx = gridDim.x, gw = causal | gridDim.z
+// << 1 | gridDim.y << 8.
 template <bool ROWS, int QT>
-__global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, int causal,
-                                              float *__restrict__ out, int ld_out, float *__restrict__ part,
-                                              const float *__restrict__ qf, int ldq, const float *__restrict__ kf,
-                                              int ldk, const float *__restrict__ vf, int ldv) {
+__global__ __launch_bounds__(128) void k_attn(int t_q, int t_kv, int gw, int nx, const float *__restrict__ qf,
+                                              int ldq, const float *__restrict__ kf, int ldk,
+                                              const float *__restrict__ vf, int ldv, float *__restrict__ out,
+                                              int ld_out, float *__restrict__ part, AttnPlanes P) {
+  const int causal = gw & 1, gz = (gw >> 1) & 127, gy = gw >> 8;
   constexpr int QB = 32 * QT;  // query rows per workgroup
   constexpr float LOG2E = 1.4426950408889634f;
   constexpr float NEG_INF = -__builtin_huge_valf();
@@ -389,7 +397,7 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
   // head's query blocks share their K and v^T planes through one L2
   int head, q0;
   {
-    const int nqb = gridDim.x, total = nqb * gridDim.y;
+    const int nqb = nx, total = nqb * gy;
     const int id = blockIdx.y * nqb + blockIdx.x;
     const int per = total / 8, rem = total % 8, xcd = id % 8, slot = id / 8;
     const int lin = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
@@ -399,7 +407,7 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
   const int off = t_kv - t_q;  // absolute position of query row 0
   const int kv_end = causal ? min(t_kv, off + q0 + QB) : t_kv;
   const int nblk_all = (kv_end + ATT_KVB - 1) / ATT_KVB;
-  const int cs = (nblk_all + gridDim.z - 1) / gridDim.z;       // blocks per split
+  const int cs = (nblk_all + gz - 1) / gz;                     // blocks per split
   const int b_begin = min(nblk_all, (int)blockIdx.z * cs);
   const int nblk = min(nblk_all, b_begin + cs);               // this workgroup: blocks [b_begin, nblk)
 
@@ -548,8 +556,8 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
       lt += __shfl_xor(lt, 32);
       const float inv = part ? 1.0f : 1.0f / (lt * ATT_PS);
       if (part && h == 0 && q0 + qt * 32 + n < t_q) {
-        const size_t pr = ((size_t)blockIdx.z * gridDim.y + head) * P.tq_pad + q0 + qt * 32 + n;
-        float *pml = part + (size_t)gridDim.z * gridDim.y * P.tq_pad * ATT_DH;
+        const size_t pr = ((size_t)blockIdx.z * gy + head) * P.tq_pad + q0 + qt * 32 + n;
+        float *pml = part + (size_t)gz * gy * P.tq_pad * ATT_DH;
         pml[2 * pr] = mm;
         pml[2 * pr + 1] = lt;
       }
@@ -579,7 +587,7 @@ __global__ __launch_bounds__(128) void k_attn(AttnPlanes P, int t_q, int t_kv, i
     const int c = it * 128 + (int)threadIdx.x;
     const int row = c >> 4, c4 = c & 15;
     if (q0 + row < t_q) {
-      float *dst = part ? part + (((size_t)blockIdx.z * gridDim.y + head) * P.tq_pad + q0 + row) * ATT_DH + 4 * c4
+      float *dst = part ? part + (((size_t)blockIdx.z * gy + head) * P.tq_pad + q0 + row) * ATT_DH + 4 * c4
                         : out + (size_t)(q0 + row) * ld_out + head * ATT_DH + 4 * c4;
       *reinterpret_cast<float4 *>(dst) = *reinterpret_cast<const float4 *>(&xo[row * LD + 4 * c4]);
     }

@@ -1598,7 +1598,8 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
     }
 
   const int span = (w.noct + KS - 1) >> lks;  // the longest part
-  const int ch = min(span, max(1, cap_oct >> lks));
+  // (the latency form holds the whole k: the host launches it only then)
+  const int ch = PD > 1 ? span : min(span, max(1, cap_oct >> lks));
   // the first octet's weights are requested before the records and the
   // layernorm statistics (so the memory latencies overlap) where its
   // registers fit beside the fill's: grouped launches copy records and
@@ -1608,7 +1609,8 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
   // Activation values in registers (gemv_ln_stats_regs' layout) for rows of
   // at most 64 blocks: the layernorm statistics come from them, and the
   // latency form at one row (RX) builds its records from them as well, one
-  // read of the row instead of two; it requests them first of all.
+  // read of the row instead of two; it requests them with its first weight
+  // octets.
   constexpr int NUX = GROUPED ? 1 : 2 * MR;
   constexpr bool RX = PD > 1 && !GROUPED && MR == 1;
   const bool xin = !GROUPED && I.a != nullptr && nb <= 64 && (I.lnw != nullptr || RX);  // uniform
@@ -1625,7 +1627,6 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
       }
     }
   };
-  if (regs) load_x();
   GemvOct<DT, NG> ring[PD];
   GemvOct<DT, NG> &cur = ring[0];
   if (EARLY) {
@@ -1633,6 +1634,7 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
     for (int u = 0; u < PD; ++u)
       if (o0 + u < min(o1, o0 + ch)) gemv_load_oct<DT, NG>(w, gw, o0 + u, rq, rd, rm, rh, vq, vs, vh, ring[u]);
   }
+  if (regs) load_x();
   // grouped launches: this lane's columns' bias, in flight with the first
   // octet (the others, and Q5_1, load it in the epilogue: registers)
   // The latency form (PD > 1) also requests the residual values of the
@@ -1809,10 +1811,19 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
 // One launch: workgroup -> (item, tile) through `wg_item` (grouped; item -1
 // = an unused slot) or, for a single or set launch, the set's item by
 // uniform compares (no runtime index into the argument).
+// The leading arguments repeat what the first item's tiles need before
+// their first memory requests (its activation rows, weight planes and
+// geometry; hdr = set count | lks << 4 | cap_oct << 8) as plain scalars:
+// the first 14
+// dwords of a launch's arguments arrive in SGPRs when its waves start
+// (kernarg preloading), so a single linear's tiles request their rows and
+// weights without waiting for the argument block (GemvSet) to be read;
+// grouped launches pass zeros.
 template <int DT, int MR, bool GROUPED, int PD = 1>
-__global__ __launch_bounds__(256, PD > 1 ? 1 : GEMV_WPE) void k_gemv(const GemvItem *__restrict__ items,
-                                                                   const int2 *__restrict__ wg_item, GemvSet one,
-                                                                   int cap_oct) {
+__global__ __launch_bounds__(256, PD > 1 ? 1 : GEMV_WPE) void k_gemv(
+    const float *a0, const uint8_t *qs0, const uint16_t *d0, const uint32_t *qh0, const uint16_t *m0, int nb0,
+    int noct0, int ngroups0, int hdr, const GemvItem *__restrict__ items, const int2 *__restrict__ wg_item,
+    GemvSet one, int cap_oct) {
   extern __shared__ __align__(16) uint8_t lds[];
   // the descriptor is wave-uniform: scalar loads from the table or kernarg
   if constexpr (GROUPED) {
@@ -1820,19 +1831,39 @@ __global__ __launch_bounds__(256, PD > 1 ? 1 : GEMV_WPE) void k_gemv(const GemvI
     if (wt.x < 0) return;                 // a slot no item uses (the whole workgroup)
     gemv_tile<DT, MR, true, PD>(items[wt.x], wt, cap_oct, lds);
   } else {
-    int ii = 0;
+    if ((hdr & 15) == 1) {
+      // one linear: its early fields from the leading scalars, so that no
+      // value merged from another item waits for the argument block's loads
+      GemvItem I = one.it[0];
+      I.a = a0;
+      I.w.qs = qs0;
+      I.w.d = d0;
+      I.w.qh = qh0;
+      I.w.m = m0;
+      I.w.nb = nb0;
+      I.w.noct = noct0;
+      I.w.nb_pad = noct0 * OCT;
+      I.w.ngroups = ngroups0;
+      I.lks = (hdr >> 4) & 3;
+      gemv_tile<DT, MR, false, PD>(I, make_int2(0, (int)blockIdx.x), hdr >> 8, lds);
+    } else {
+      // a set: the workgroup's item by uniform compares (its end[] entries
+      // and fields from the argument block; measured faster than reading
+      // the item at a computed offset)
+      int ii = 0;
 #pragma unroll
-    for (int t = 0; t + 1 < GEMV_SET; ++t)
-      if (t + 1 < one.count && (int)blockIdx.x >= one.end[t]) ii = t + 1;
-    int first = 0;
+      for (int t = 0; t + 1 < GEMV_SET; ++t)
+        if (t + 1 < one.count && (int)blockIdx.x >= one.end[t]) ii = t + 1;
+      int first = 0;
 #pragma unroll
-    for (int t = 0; t + 1 < GEMV_SET; ++t)
-      if (ii == t + 1) first = one.end[t];
-    GemvItem I = one.it[0];
+      for (int t = 0; t + 1 < GEMV_SET; ++t)
+        if (ii == t + 1) first = one.end[t];
+      GemvItem I = one.it[0];
 #pragma unroll
-    for (int t = 1; t < GEMV_SET; ++t)
-      if (ii == t) I = one.it[t];
-    gemv_tile<DT, MR, false, PD>(I, make_int2(ii, (int)blockIdx.x - first), cap_oct, lds);
+      for (int t = 1; t < GEMV_SET; ++t)
+        if (ii == t) I = one.it[t];
+      gemv_tile<DT, MR, false, PD>(I, make_int2(ii, (int)blockIdx.x - first), cap_oct, lds);
+    }
   }
 }
 
@@ -1960,43 +1991,22 @@ struct GemmSet {
 // 32 x 32 output tiles dealt to the wavefronts in turn.  KW comes from the
 // weights' shapes alone and TM changes which rows share a workgroup, not
 // how a row is summed, so a row's result never depends on m.
-template <int DT, int KW, int TM, bool OFFS, int TN = GEMM_TN>
-__global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int m) {
+// One workgroup's tile of k_gemm: item `it`'s column tile bx (of its own
+// weight) against activation row tile by.
+template <int DT, int KW, int TM, bool OFFS, int TN>
+__device__ __attribute__((always_inline)) inline void gemm_tile(const GemmItem &it, const ActView &a, int nb,
+                                                                int nb_pad, int m, int bx, int by, uint8_t *lds) {
   constexpr int P = TM <= 2 ? GEMM_P_SKINNY : GEMM_P, S = P + 1;
   constexpr int RED = KW > 1 ? KW * TM * TN * 16 * 64 * 4 : 16;
   constexpr int QROW = 36;  // floats per row of a GEMM_QUANT staging tile (rows 4 apart on other banks)
-  __shared__ __align__(16) uint8_t lds[RED + KW * 32 * QROW * 4];
   const int l = threadIdx.x & 63;
   const int kw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int h = l >> 5, r = l & 31;
-  int bx, by;
-  {
-    // XCD-aware order: consecutive workgroup ids go to different XCDs (id % 8);
-    // each XCD gets one contiguous band of the row-major tile order, so its
-    // L2 holds one band of activation rows.
-    const int nx = gridDim.x, total = nx * gridDim.y;
-    const int id = blockIdx.y * nx + blockIdx.x;
-    const int per = total / 8, rem = total % 8, xcd = id % 8, slot = id / 8;
-    const int lin = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
-    bx = lin % nx;
-    by = lin / nx;
-  }
-  // this tile's weight, selected by uniform compares (no runtime index into
-  // the argument array)
-  int wi = 0;
-#pragma unroll
-  for (int t = 1; t < GEMM_MAX_SET; ++t)
-    if (t < set.count && bx >= set.it[t].tile0) wi = t;
-  GemmItem it = set.it[0];
-#pragma unroll
-  for (int t = 1; t < GEMM_MAX_SET; ++t)
-    if (wi == t) it = set.it[t];
-  bx -= it.tile0;
   const GemmPlanes gp = it.gp;
   const float *__restrict__ bias = it.bias;
   float *__restrict__ out = it.out;
   const int n = it.n, ngroups = it.ngroups, flags = it.flags;
-  const int nb = set.nb;
+  
   const int nsw = nb > kw ? (nb - kw + KW - 1) / KW : 0;  // this wavefront's block count
 
   // operands through buffer loads: one resource per plane, a constant lane
@@ -2004,16 +2014,16 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int
   // per-lane address arithmetic in the loop); row groups past the end repeat
   // the last one
   const auto ra = buffer_rsrc(a.a16, (uint32_t)a.mgroups * (uint32_t)nb * 2048u);
-  const auto rq = buffer_rsrc(gp.q8, (uint32_t)ngroups * (uint32_t)set.nb_pad * 1024u);
-  const auto rd = buffer_rsrc(gp.dm, (uint32_t)ngroups * (uint32_t)set.nb_pad * 128u);
+  const auto rq = buffer_rsrc(gp.q8, (uint32_t)ngroups * (uint32_t)nb_pad * 1024u);
+  const auto rd = buffer_rsrc(gp.dm, (uint32_t)ngroups * (uint32_t)nb_pad * 128u);
   uint32_t aoff[TM], qoff[TN], doff[TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i) aoff[i] = (uint32_t)min(by * TM + i, a.mgroups - 1) * (uint32_t)nb * 2048u + l * 16;
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const uint32_t g = (uint32_t)min(bx * TN + j, ngroups - 1);
-    qoff[j] = g * (uint32_t)set.nb_pad * 1024u + r * 32 + 16 * h;
-    doff[j] = g * (uint32_t)set.nb_pad * 128u + r * 4;
+    qoff[j] = g * (uint32_t)nb_pad * 1024u + r * 32 + 16 * h;
+    doff[j] = g * (uint32_t)nb_pad * 128u + r * 4;
   }
   auto load = [&](GemmStage<TM, TN> &st, int s) __attribute__((always_inline)) {
     const uint32_t bl = (uint32_t)(kw + s * KW);
@@ -2254,6 +2264,56 @@ __global__ __launch_bounds__(64 * KW, 1) void k_gemm(GemmSet set, ActView a, int
       for (int v = 0; v < 16; ++v)
         if (tg * RG + 4 * h + 8 * (v >> 2) + (v & 3) < m) stg_f(o + (size_t)(8 * (v >> 2) + (v & 3)) * n, y[v]);
     }
+  }
+}
+
+// The leading arguments repeat the activation plane, the first weight's
+// planes and the launch's geometry (hdr = the set's count; nx, ny = the
+// grid) as plain
+// scalars: the first 14 dwords arrive in SGPRs when the waves start
+// (kernarg preloading), so a one-weight launch requests its first operand
+// blocks without first reading the argument block.
+template <int DT, int KW, int TM, bool OFFS, int TN = GEMM_TN>
+__global__ __launch_bounds__(64 * KW, 1) void k_gemm(const uint16_t *a16, const uint8_t *q80, const uint32_t *dm0,
+                                                      int nb, int nb_pad, int mgroups, int ngroups0, int m, int hdr,
+                                                      int nx, int ny, GemmSet set, ActView a) {
+  constexpr int RED = KW > 1 ? KW * TM * TN * 16 * 64 * 4 : 16;
+  constexpr int QROW = 36;
+  __shared__ __align__(16) uint8_t lds[RED + KW * 32 * QROW * 4];
+  int bx, by;
+  {
+    // XCD-aware order: consecutive workgroup ids go to different XCDs (id % 8);
+    // each XCD gets one contiguous band of the row-major tile order, so its
+    // L2 holds one band of activation rows.
+    const int total = nx * ny;  // the grid (gridDim would be read from the argument block)
+    const int id = blockIdx.y * nx + blockIdx.x;
+    const int per = total / 8, rem = total % 8, xcd = id % 8, slot = id / 8;
+    const int lin = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+    bx = lin % nx;
+    by = lin / nx;
+  }
+  ActView av = a;
+  av.a16 = a16;
+  av.mgroups = mgroups;
+  av.nb = nb;
+  if (hdr == 1) {
+    GemmItem it = set.it[0];
+    it.gp.q8 = q80;
+    it.gp.dm = dm0;
+    it.ngroups = ngroups0;
+    gemm_tile<DT, KW, TM, OFFS, TN>(it, av, nb, nb_pad, m, bx, by, lds);
+  } else {
+    // this tile's weight, selected by uniform compares (no runtime index
+    // into the argument array)
+    int wi = 0;
+#pragma unroll
+    for (int t = 1; t < GEMM_MAX_SET; ++t)
+      if (t < hdr && bx >= set.it[t].tile0) wi = t;
+    GemmItem it = set.it[0];
+#pragma unroll
+    for (int t = 1; t < GEMM_MAX_SET; ++t)
+      if (wi == t) it = set.it[t];
+    gemm_tile<DT, KW, TM, OFFS, TN>(it, av, nb, nb_pad, m, bx - it.tile0, by, lds);
   }
 }
 

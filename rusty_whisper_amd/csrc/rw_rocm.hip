@@ -415,7 +415,9 @@ static int gemm_kw(size_t tiles, int nb) {
 template <int DT, int KW, int TM, bool OFFS, int TN = GEMM_TN>
 static void launch_gemm_tm(const GemmSet &set, size_t tiles, const ActView &av, int m, hipStream_t s) {
   dim3 grid((unsigned)tiles, (unsigned)cdiv(av.mgroups, TM));
-  hipLaunchKernelGGL((k_gemm<DT, KW, TM, OFFS, TN>), grid, dim3(64 * KW), 0, s, set, av, m);
+  const GemmPlanes &g0 = set.it[0].gp;
+  hipLaunchKernelGGL((k_gemm<DT, KW, TM, OFFS, TN>), grid, dim3(64 * KW), 0, s, av.a16, g0.q8, g0.dm, set.nb,
+                     set.nb_pad, av.mgroups, set.it[0].ngroups, m, set.count, (int)grid.x, (int)grid.y, set, av);
 }
 
 // A skinny launch (64-row tiles that still give fewer than GEMM_TN1_BELOW
@@ -606,14 +608,23 @@ template <int DT, int MR>
 static void launch_gemv_mr(const GemvItem *items, const int2 *wg_item, const GemvSet &one, int wgs, int cap_oct,
                            hipStream_t s) {
   const size_t lds = gemv_lds_bytes(MR, cap_oct);
+  // k_gemv's leading scalars: the first item's rows, planes and geometry
+  // (zeros for a grouped launch, whose items are in the device table)
+  const GemvItem &f = one.it[0];
+  const int hdr = items ? 0 : one.count | f.lks << 4 | cap_oct << 8;
+#define RW_GEMV_HEAD                                                                                             \
+  f.a, (const uint8_t *)f.w.qs, (const uint16_t *)f.w.d, (const uint32_t *)f.w.qh, (const uint16_t *)f.w.m, f.w.nb, \
+      f.w.noct, f.w.ngroups, hdr
   if (items)
-    hipLaunchKernelGGL((k_gemv<DT, MR, true>), dim3((unsigned)wgs), dim3(256), lds, s, items, wg_item, one, cap_oct);
+    hipLaunchKernelGGL((k_gemv<DT, MR, true>), dim3((unsigned)wgs), dim3(256), lds, s, nullptr, nullptr, nullptr,
+                       nullptr, nullptr, 0, 0, 0, 0, items, wg_item, one, cap_oct);
   else if (gemv_latency_form(one, wgs, cap_oct))
-    hipLaunchKernelGGL((k_gemv<DT, MR, false, GEMV_PD>), dim3((unsigned)wgs), dim3(256), lds, s, items,
-                       wg_item, one, cap_oct);
+    hipLaunchKernelGGL((k_gemv<DT, MR, false, GEMV_PD>), dim3((unsigned)wgs), dim3(256), lds, s, RW_GEMV_HEAD,
+                       items, wg_item, one, cap_oct);
   else
-    hipLaunchKernelGGL((k_gemv<DT, MR, false>), dim3((unsigned)wgs), dim3(256), lds, s, items, wg_item, one,
-                       cap_oct);
+    hipLaunchKernelGGL((k_gemv<DT, MR, false>), dim3((unsigned)wgs), dim3(256), lds, s, RW_GEMV_HEAD, items,
+                       wg_item, one, cap_oct);
+#undef RW_GEMV_HEAD
 }
 
 // one k_gemv launch: `items` (device) + `wg_item` (device) for a group, or
@@ -1050,18 +1061,19 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
   const bool one_tile = t_q <= 32;
   const dim3 grid(one_tile ? 1u : (unsigned)(L.tq_pad / ATT_QB), (unsigned)n_head, (unsigned)nsplit);
   const int cz = causal ? 1 : 0;
+  const int gw = cz | nsplit << 1 | n_head << 8;  // k_attn's packed grid
   if (rows && one_tile)
-    hipLaunchKernelGGL((k_attn<true, 1>), grid, dim3(128), 0, s, P, (int)t_q, (int)t_kv, cz, out, (int)ldo, part, q,
-                       (int)ldq, k, (int)ldk, v, (int)ldv);
+    hipLaunchKernelGGL((k_attn<true, 1>), grid, dim3(128), 0, s, (int)t_q, (int)t_kv, gw, (int)grid.x, q, (int)ldq, k,
+                       (int)ldk, v, (int)ldv, out, (int)ldo, part, P);
   else if (rows)
-    hipLaunchKernelGGL((k_attn<true, 2>), grid, dim3(128), 0, s, P, (int)t_q, (int)t_kv, cz, out, (int)ldo, part, q,
-                       (int)ldq, k, (int)ldk, v, (int)ldv);
+    hipLaunchKernelGGL((k_attn<true, 2>), grid, dim3(128), 0, s, (int)t_q, (int)t_kv, gw, (int)grid.x, q, (int)ldq, k,
+                       (int)ldk, v, (int)ldv, out, (int)ldo, part, P);
   else if (one_tile)
-    hipLaunchKernelGGL((k_attn<false, 1>), grid, dim3(128), 0, s, P, (int)t_q, (int)t_kv, cz, out, (int)ldo, part, q,
-                       (int)ldq, nullptr, 0, nullptr, 0);
+    hipLaunchKernelGGL((k_attn<false, 1>), grid, dim3(128), 0, s, (int)t_q, (int)t_kv, gw, (int)grid.x, q, (int)ldq,
+                       nullptr, 0, nullptr, 0, out, (int)ldo, part, P);
   else
-    hipLaunchKernelGGL((k_attn<false, 2>), grid, dim3(128), 0, s, P, (int)t_q, (int)t_kv, cz, out, (int)ldo, part, q,
-                       (int)ldq, nullptr, 0, nullptr, 0);
+    hipLaunchKernelGGL((k_attn<false, 2>), grid, dim3(128), 0, s, (int)t_q, (int)t_kv, gw, (int)grid.x, q, (int)ldq,
+                       nullptr, 0, nullptr, 0, out, (int)ldo, part, P);
   LAUNCH_TRY("k_attn");
   if (part) {
     const size_t nz = t_q * (size_t)n_head * ATT_DH;
@@ -1185,8 +1197,8 @@ static int run_beam_self_attention(rw_decoder *const *beams, size_t nb, int l, c
   LAUNCH_TRY("k_attn_split_beams");
   const int nsplit = std::min(L.nsplit, attn_nsplit((size_t)(L.tq_pad / ATT_QB) * heads, cdiv(t_kv, ATT_KVB)));
   float *part = nsplit > 1 ? (float *)(b + L.off_part) : nullptr;
-  hipLaunchKernelGGL((k_attn<false, 1>), dim3(1, (unsigned)heads, (unsigned)nsplit), dim3(128), 0, s, P, 1, (int)t_kv,
-                     1, att, (int)d->n, part, nullptr, 0, nullptr, 0, nullptr, 0);
+  hipLaunchKernelGGL((k_attn<false, 1>), dim3(1, (unsigned)heads, (unsigned)nsplit), dim3(128), 0, s, 1, (int)t_kv,
+                     1 | nsplit << 1 | heads << 8, 1, nullptr, 0, nullptr, 0, nullptr, 0, att, (int)d->n, part, P);
   LAUNCH_TRY("k_attn");
   if (part) {
     hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)cdiv((size_t)heads * ATT_DH, 256)), dim3(256), 0, s, part, nsplit,
