@@ -1563,7 +1563,7 @@ __device__ inline void gemv_records_regs(const GemvItem &I, int nb, int noct, in
 // in the same order whatever PD, so the results do not depend on it.
 template <int DT, int MR, bool GROUPED, int PD>
 __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I, int2 wt, int cap_oct,
-                                                                uint8_t *lds) {
+                                                                uint8_t *lds, int lnf = -1) {
   constexpr int REC = gemv_rec_bytes(MR), ZO = 32 * MR;
   constexpr int QB = DT == 8 ? 32 : 16;  // qs bytes per row-block
   constexpr int NG = gemv_ng(GROUPED);
@@ -1613,8 +1613,14 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
   // octets.
   constexpr int NUX = GROUPED ? 1 : 2 * MR;
   constexpr bool RX = PD > 1 && !GROUPED && MR == 1;
-  const bool xin = !GROUPED && I.a != nullptr && nb <= 64 && (I.lnw != nullptr || RX);  // uniform
+  // lnf: whether the rows are layernormed, when the caller knows it without
+  // reading the item (-1: from I.lnw)
+  const bool has_ln = lnf >= 0 ? lnf != 0 : I.lnw != nullptr;
+  const bool xin = !GROUPED && I.a != nullptr && nb <= 64 && (has_ln || RX);  // uniform
   const bool regs = RX && xin;
+  // the latency form requests them with its first octets when that needs
+  // nothing from the argument block (lnf known)
+  const bool x_early = PD > 1 && xin && (regs || lnf >= 0);
   float4 xr[NUX];
   auto load_x = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -1634,7 +1640,7 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
     for (int u = 0; u < PD; ++u)
       if (o0 + u < min(o1, o0 + ch)) gemv_load_oct<DT, NG>(w, gw, o0 + u, rq, rd, rm, rh, vq, vs, vh, ring[u]);
   }
-  if (regs) load_x();
+  if (x_early) load_x();
   // grouped launches: this lane's columns' bias, in flight with the first
   // octet (the others, and Q5_1, load it in the epilogue: registers)
   // The latency form (PD > 1) also requests the residual values of the
@@ -1657,10 +1663,10 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
   // the loop below
   __shared__ float ln_s[2 * GEMV_MR_MAX];
   if constexpr (!GROUPED) {
-    if (I.lnw && xin) {
-      if (!regs) load_x();
+    if (has_ln && xin) {
+      if (!x_early) load_x();
       gemv_ln_stats_regs<MR, NUX>(xr, nb, lds, t, ln_s);
-    } else if (I.lnw) {
+    } else if (has_ln) {
       const int K = nb * QK;
       float *sred = reinterpret_cast<float *>(lds);  // [4 wavefronts][MR], before any record
       auto row_sums = [&](float (&v)[MR]) __attribute__((always_inline)) {
@@ -1813,7 +1819,8 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
 // uniform compares (no runtime index into the argument).
 // The leading arguments repeat what the first item's tiles need before
 // their first memory requests (its activation rows, weight planes and
-// geometry; hdr = set count | lks << 4 | cap_oct << 8) as plain scalars:
+// geometry; hdr = set count | lks << 4 | layernorm << 6 | cap_oct << 8)
+// as plain scalars:
 // the first 14
 // dwords of a launch's arguments arrive in SGPRs when its waves start
 // (kernarg preloading), so a single linear's tiles request their rows and
@@ -1845,7 +1852,7 @@ __global__ __launch_bounds__(256, PD > 1 ? 1 : GEMV_WPE) void k_gemv(
       I.w.nb_pad = noct0 * OCT;
       I.w.ngroups = ngroups0;
       I.lks = (hdr >> 4) & 3;
-      gemv_tile<DT, MR, false, PD>(I, make_int2(0, (int)blockIdx.x), hdr >> 8, lds);
+      gemv_tile<DT, MR, false, PD>(I, make_int2(0, (int)blockIdx.x), (hdr >> 8) & 255, lds, (hdr >> 6) & 1);
     } else {
       // a set: the workgroup's item by uniform compares (its end[] entries
       // and fields from the argument block; measured faster than reading

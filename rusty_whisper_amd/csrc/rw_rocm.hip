@@ -611,7 +611,9 @@ static void launch_gemv_mr(const GemvItem *items, const int2 *wg_item, const Gem
   // k_gemv's leading scalars: the first item's rows, planes and geometry
   // (zeros for a grouped launch, whose items are in the device table)
   const GemvItem &f = one.it[0];
-  const int hdr = items ? 0 : one.count | f.lks << 4 | cap_oct << 8;
+  static_assert(GEMV_LDS_CAP_LAT / (OCT * gemv_rec_bytes(1)) < 256 && GEMV_LDS_CAP / (OCT * gemv_rec_bytes(1)) < 256,
+                "k_gemv's header holds cap_oct in 8 bits");
+  const int hdr = items ? 0 : one.count | f.lks << 4 | (f.lnw ? 1 : 0) << 6 | cap_oct << 8;
 #define RW_GEMV_HEAD                                                                                             \
   f.a, (const uint8_t *)f.w.qs, (const uint16_t *)f.w.d, (const uint32_t *)f.w.qh, (const uint16_t *)f.w.m, f.w.nb, \
       f.w.noct, f.w.ngroups, hdr
