@@ -1012,6 +1012,8 @@ static int check_attn_args(const float *q, size_t ldq, const float *k, size_t ld
     return fail(RW_EINVAL, "head size %zu unsupported (the kernel takes %d)", n_state / (size_t)n_head, ATT_DH);
   if (causal && t_q > t_kv) return fail(RW_EINVAL, "causal attention needs t_q <= t_kv (%zu > %zu)", t_q, t_kv);
   if (t_q > (1u << 24) || t_kv > (1u << 24)) return fail(RW_EINVAL, "sequence too long");
+  // k_attn packs its grid's y extent (heads, times 8 beams at most) above 8 bits of one int
+  if (n_head >= (1 << 19)) return fail(RW_EINVAL, "n_head %d too large", n_head);
   if (t_q == 0) return RW_OK;
   if (!q || !out || (t_kv && (!k || !v))) return fail(RW_EINVAL, "q, k, v or out is NULL");
   if (ldq < n_state || ldk < n_state || ldv < n_state || ldo < n_state)
@@ -1131,6 +1133,7 @@ static int check_decoder_params(const rw_decoder_params *P) {
   const size_t n = P->token_embedding->k;
   if (P->n_head <= 0 || n != (size_t)P->n_head * ATT_DH)
     return fail(RW_EINVAL, "n_state %zu != 64 * n_head (%d)", n, P->n_head);
+  if (P->n_head >= (1 << 19)) return fail(RW_EINVAL, "n_head %d too large", P->n_head);
   const size_t f = P->layers[0].fc1 ? P->layers[0].fc1->n : 0;
   for (int l = 0; l < P->n_layer; ++l) {
     const rw_decoder_layer &L = P->layers[l];
