@@ -1448,10 +1448,10 @@ __device__ inline void gemv_epilogue(const GemvItem &I, int gw, int h, int r, in
   }
 }
 
-// Activation values held in registers by gemv_tile for rows of at most 64
-// blocks: pair rb = 32 u + t / 8 of the rows' (block, row) pairs,
-// block-major (the fill's order), lane t % 8 holding elements 4 (t % 8) ..
-// + 3 of it; NUX = 2 MR passes cover every pair.
+// Activation values held in registers by gemv_tile: pair rb = 32 u + t / 8
+// of the rows' (block, row) pairs, block-major (the fill's order), lane t % 8
+// holding elements 4 (t % 8) .. + 3 of it; NUX passes cover every pair (rows
+// of at most 64 blocks, or 160 in the one-row latency form).
 //
 // Layernorm statistics of the MR rows from those registers: each block's 32
 // values summed by its 8 lanes in a fixed tree (DPP), the block sums of a row
@@ -1611,13 +1611,16 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
   // latency form at one row (RX) builds its records from them as well, one
   // read of the row instead of two; it requests them with its first weight
   // octets.
-  constexpr int NUX = GROUPED ? 1 : 2 * MR;
+  // (the one-row latency form holds rows of up to 160 blocks, k = 5120:
+  // the decoder's fc2 input too; statistics from registers need <= 64)
   constexpr bool RX = PD > 1 && !GROUPED && MR == 1;
+  constexpr int NUX = GROUPED ? 1 : RX ? 5 : 2 * MR;
   // lnf: whether the rows are layernormed, when the caller knows it without
   // reading the item (-1: from I.lnw)
   const bool has_ln = lnf >= 0 ? lnf != 0 : I.lnw != nullptr;
-  const bool xin = !GROUPED && I.a != nullptr && nb <= 64 && (has_ln || RX);  // uniform
-  const bool regs = RX && xin;
+  const bool stats_regs = !GROUPED && I.a != nullptr && nb <= 64 && has_ln;  // uniform
+  const bool regs = RX && I.a != nullptr && nb <= 32 * NUX;
+  const bool xin = stats_regs || regs;
   // the latency form requests them with its first octets when that needs
   // nothing from the argument block (lnf known)
   const bool x_early = PD > 1 && xin && (regs || lnf >= 0);
@@ -1663,7 +1666,7 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
   // the loop below
   __shared__ float ln_s[2 * GEMV_MR_MAX];
   if constexpr (!GROUPED) {
-    if (has_ln && xin) {
+    if (stats_regs) {
       if (!x_early) load_x();
       gemv_ln_stats_regs<MR, NUX>(xr, nb, lds, t, ln_s);
     } else if (has_ln) {
