@@ -44,6 +44,14 @@ def test_rejects_short_or_misaligned_rows():
     assert "16-byte aligned" in A.last_error()
 
 
+def test_rejects_head_counts_past_the_packed_grid():
+    # k_attn carries its grid's head extent (times up to 8 beams) above 8 bits
+    # of one int argument
+    assert _call(0, 0, (1 << 19) * 64, 1 << 19, 0) == A.RW_EINVAL
+    assert "too large" in A.last_error()
+    assert _call(0, 0, ((1 << 19) - 1) * 64, (1 << 19) - 1, 0) == A.RW_OK  # an empty call within the bound
+
+
 def test_empty_query_is_a_noop():
     assert _call(0, 4, 128, 2, 0) == A.RW_OK
 
