@@ -73,6 +73,26 @@ def test_decoder_parity(torch, n, n_layer, dtype, prompt):
     assert max(errs) <= TOL, errs
 
 
+def test_decoder_wide_rows(torch):
+    """n = 2560 (40 heads), fc 10240: rows of 80 blocks (layernorm statistics
+    over more than 64 blocks, the one-row form's records from its
+    registers after them) and fc2 over 320 blocks (longer than the one-row
+    form's registers hold: its fill), in a 3-row prompt and single-token
+    steps, against the oracle."""
+    n, heads, n_audio = 2560, 40, 64
+    p = decoder_params(n=n, f=4 * n, n_layer=1, n_vocab=300, n_ctx=16, dtype=6, seed=2560)
+    enc = np.random.default_rng(2560).standard_normal((n_audio, n)).astype(np.float32)
+    print("decoder n=2560 fc=10240: 1 layer, Q5_0", flush=True)
+    d = device_decoder(torch, p, heads, n_audio)
+    d.set_audio(torch.from_numpy(enc).to("cuda:0"))
+    o = OD(p, heads, enc)
+    errs = [rel(step(torch, d, [5, 6, 7], n), o.forward_hidden([5, 6, 7]))]
+    for t in (17, 250, 4):
+        errs.append(rel(step(torch, d, [t], n), o.forward_hidden([t])))
+    print("  errors", ["%.2g" % e for e in errs], flush=True)
+    assert max(errs) <= TOL, errs
+
+
 def test_fork_and_reset(torch):
     n, heads = 128, 2
     p = decoder_params(n=n, f=512, n_layer=2, n_vocab=300, n_ctx=16, dtype=8, seed=4)
