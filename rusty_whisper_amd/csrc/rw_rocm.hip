@@ -829,7 +829,15 @@ static GroupPlan group_plan(const rw_linear *items, size_t count) {
                   (int)P.qmap.size()};
     std::vector<int2> slots, qslots;
     int pos[8] = {}, qpos[8] = {};
-    for (size_t j = j0; j < j1; ++j) {
+    // Workgroups start in slot order as earlier ones end.  Those of k-split
+    // items (two or four wavefront sets along k, which meet at the end) run
+    // the longest, so their slots come first and the launch's last round
+    // holds the shorter ones.
+    std::vector<size_t> place(j1 - j0);
+    for (size_t j = j0; j < j1; ++j) place[j - j0] = j;
+    std::stable_sort(place.begin(), place.end(),
+                     [&](size_t x, size_t y) { return gemv_ks(items[P.order[x]].w) > gemv_ks(items[P.order[y]].w); });
+    for (const size_t j : place) {
       const rw_weight *w = items[P.order[j]].w;
       const int m = (int)items[P.order[j]].m;
       const int x0 = place_runs((int)j, gemv_wgs(w, gemv_ks(w), true), pos, slots);
