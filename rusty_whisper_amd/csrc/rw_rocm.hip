@@ -526,7 +526,10 @@ static int run_gemm(const rw_weight *const *w, const float *const *bias, float *
 
 // The split of a row's octets over wavefronts depends on the weight and the
 // launch form only.  Grouped launches have workgroups to spare and split
-// while every wavefront keeps at least 4 octets; a single linear's launch
+// while every wavefront keeps at least 6 octets: each workgroup copies its
+// items' records for the whole k into LDS, so k = 5120 in two parts of 10
+// octets instead of four of 5 halves those copies (large-v3 decoder set,
+// M = 5: 5.02-5.08 -> 5.17-5.28 TB/s on one box); a single linear's launch
 // is short of workgroups at decode sizes and splits while every wavefront
 // keeps 2, which halves its latency.  The two forms then differ only by the
 // f32 reassociation of the parts' sums.  Single and set launches also give
@@ -537,7 +540,7 @@ static int run_gemm(const rw_weight *const *w, const float *const *bias, float *
 #define GEMV_SINGLE_KEEP 2
 #endif
 static int gemv_ks(const rw_weight *w, bool single = false) {
-  const int keep = single ? GEMV_SINGLE_KEEP : 4;
+  const int keep = single ? GEMV_SINGLE_KEEP : 6;
   int ks = 1;
   while (ks < 4 && w->noct / (2 * ks) >= keep) ks *= 2;
   return ks;
