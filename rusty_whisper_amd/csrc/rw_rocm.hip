@@ -327,7 +327,10 @@ static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &
     } else {
       // rows of 5-20 passes: the same kernels' arithmetic with 4 or 8 rows
       // per wavefront, whose stores write whole runs of the plane (m = 1500:
-      // 5.5 -> 5.1 us at k = 1280, 15.2 -> 13.2 us at k = 5120, cold inputs)
+      // 5.5 -> 5.1 us at k = 1280, 15.2 -> 13.2 us at k = 5120, cold inputs);
+      // at k = 5120 two wavefronts per part, each with half of its blocks,
+      // 8 per workgroup (10.28 -> 9.85 us with inputs in the MALL; 8 rows
+      // per wavefront and 16 wavefronts per workgroup 10.59 us)
 #define RW_QF16R(R, NP, WPR, SW)                                                                             \
   hipLaunchKernelGGL((k_quantize_f16_rows<R, NP, WPR, SW>), dim3((unsigned)(g8 * (RG / R))), dim3(64 * WPR * SW), \
                      0, s, a, (int)m, (int)k, L.nb, a16, rs, ps)
@@ -336,7 +339,7 @@ static int launch_quantize(const float *a, size_t m, size_t k, const ActLayout &
       else if (passes <= 4) RW_QF16(1, 4, false);
       else if (passes <= 6) RW_QF16R(8, 3, 2, 4);
       else if (passes <= 8) RW_QF16R(4, 2, 4, 1);
-      else if (passes <= 20) RW_QF16R(4, 5, 4, 1);
+      else if (passes <= 20) RW_QF16R(4, 5, 4, 2);
       else RW_QF16(8, 4, false);
 #undef RW_QF16R
     }
