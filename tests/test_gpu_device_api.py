@@ -88,10 +88,10 @@ def test_prequant_matches_fused_bitwise(torch, dtype, m):
     assert rel_row_l2(fused, O.matmul_emul(a, dtype, raw, n)) <= ROW_L2_TOL
 
 
-# (dtype, m, n, k, bias): every k split (k = 384 -> 2, 768 / 1280 -> 1,
-# 5120 -> 4), ragged n, an m = 0 entry, two entries that share a launch, and
-# one large enough in k (m = 8) that its activations pass through LDS in
-# several chunks
+# (dtype, m, n, k, bias): every k split of a grouped launch (k up to 2816
+# -> 1 wavefront set, 5120 -> 2, 16384 -> 4), ragged n, an m = 0 entry, two
+# entries that share a launch, and one large enough in k (m = 8) that its
+# activations pass through LDS in several chunks
 GROUP = [
     (7, 5, 1280, 1280, True),
     (6, 5, 96, 5120, False),
