@@ -2096,12 +2096,13 @@ __device__ __attribute__((always_inline)) inline void gemm_tile(const GemmItem &
   }
   // The workgroup's TM x TN output tiles (32 x 32 each, tile u = TN i + j)
   // are dealt to the KW wavefronts in runs of UPW: a wavefront finishes RPW
-  // row groups x CPW column groups.  Their epilogue inputs are requested
-  // before the last blocks' MFMAs and land while those run and the partials
-  // meet in LDS (rows and columns past the end read the last one).
+  // row groups x CPW column groups (whole rows of tiles, or UPW tiles of one
+  // row).  Their epilogue inputs are requested before the last blocks' MFMAs
+  // and land while those run and the partials meet in LDS (rows and columns
+  // past the end read the last one).
   constexpr int NU = TM * TN, UPW = (NU + KW - 1) / KW;
-  static_assert(UPW < TN || UPW % TN == 0, "a run covers whole row groups");
-  constexpr int RPW = UPW >= TN ? UPW / TN : 1, CPW = UPW >= TN ? TN : 1;
+  static_assert(UPW >= TN ? UPW % TN == 0 : TN % UPW == 0, "a run covers whole rows of tiles or part of one");
+  constexpr int RPW = UPW >= TN ? UPW / TN : 1, CPW = UPW >= TN ? TN : UPW;
   const int u0 = KW > 1 ? kw * UPW : 0;  // first tile of this wavefront
   const int i0 = u0 / TN, j0 = UPW >= TN ? 0 : u0 % TN;
   // OFFS: some weight of the launch has rows with an offset (GemmPlanes::cm;

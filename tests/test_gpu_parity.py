@@ -297,6 +297,28 @@ def test_gemm_k_splits(dtype, m, k, n):
     assert np.array_equal(w.matmul(a[:9], bias).view(np.uint32), got[:9].view(np.uint32))
 
 
+def test_gemm_k_split_on_a_tall_ragged_input():
+    # the 4-way k split at encoder height: 1500 rows (a partial last row
+    # group), 129 blocks (uneven over the 4 wavefronts), 900 columns (an odd
+    # number of weight row groups, the last one partial), 128-row tiles.
+    # Rows 0..8 are bitwise an m = 9 call's (64-row, 32-column tiles, the
+    # same k split); a sample of rows, the last row group's among them,
+    # against the oracle
+    m, k, n, dtype = 1500, 4128, 900, 7
+    a = activations(m, k, seed=41, outliers=0.01)
+    raw = weights(dtype, n, k, seed=43)
+    bias = np.random.default_rng(45).standard_normal(n).astype(np.float32)
+    w = A.DeviceWeight(dtype, n, k, raw)
+    got = w.matmul(a, bias)
+    assert np.all(np.isfinite(got))
+    assert np.array_equal(w.matmul(a[:9], bias).view(np.uint32), got[:9].view(np.uint32))
+    rows = np.unique(np.concatenate([np.random.default_rng(47).choice(m - 32, 24, replace=False),
+                                     np.arange(m - 28, m, 9), [m - 1]]))
+    ref = O.matmul_emul(a[rows], dtype, raw, n, bias=bias)
+    assert rel_row_l2(got[rows], ref) <= ROW_L2_TOL
+    check_combine(got[rows], a[rows], dtype, raw, n, bias)
+
+
 @pytest.mark.parametrize("m", [5, 70])
 def test_nonfinite_input_stays_in_its_row(m):
     # an inf activation makes its own row non-finite (as in the reference:
