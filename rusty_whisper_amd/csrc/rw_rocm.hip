@@ -790,8 +790,13 @@ struct GroupPlan {
 // item all run on the XCD of the item's first run, so that run finds the
 // records in its L2 (2 us less for the large-v3 decoder set at M = 5 than
 // with the parts placed on their own; every run of an item on one XCD was
-// 15% slower).  Unused slots map to item -1.
-constexpr int GEMV_RUN = 8;
+// 15% slower; runs of 16 rather than 8 or 4: 5.27-5.33 against 5.23-5.26
+// and 5.08-5.12 TB/s at M = 5, one box; 32 no better).  Unused slots map to
+// item -1.
+#ifndef GEMV_RUN_SLOTS
+#define GEMV_RUN_SLOTS 16
+#endif
+constexpr int GEMV_RUN = GEMV_RUN_SLOTS;
 
 
 // Returns the XCD of the item's first run.  With `xcd` >= 0 every run goes
