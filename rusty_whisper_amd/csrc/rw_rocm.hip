@@ -842,8 +842,8 @@ static GroupPlan group_plan(const rw_linear *items, size_t count) {
     int pos[8] = {}, qpos[8] = {};
     // Workgroups start in slot order as earlier ones end.  Those of k-split
     // items (two or four wavefront sets along k, which meet at the end) run
-    // the longest, so their slots come first and the launch's last round
-    // holds the shorter ones.
+    // the longest, so their slots come first and the workgroups that start
+    // last, once the resident slots have turned over, are shorter ones.
     std::vector<size_t> place(j1 - j0);
     for (size_t j = j0; j < j1; ++j) place[j - j0] = j;
     std::stable_sort(place.begin(), place.end(),
