@@ -21,7 +21,10 @@
  * or loses precision to f16 subnormals whatever the block scales are) with
  * exact products and f32 accumulation on the matrix cores: within
  * 2^-10 * sum|a||w| plus f32 accumulation error of the exact result, far
- * inside the 1e-3 (row-L2) agreement with the reference CPU path.
+ * inside the 1e-3 (row-L2) agreement with the reference CPU path.  So the
+ * exact per-block integer sums S are formed on the product path for m <= 8
+ * only; for m > 8 the validation entry rw_rocm_block_dots (below) forms them,
+ * bit for bit, off the product path.
  *
  * Conventions (the crate's existing C ABI, src/wasm.rs:25-110, returns an
  * i32 status and keeps error text separately):
