@@ -1106,8 +1106,13 @@ struct GemvItem {
   const float *lnw, *lnb;  // single / set launches: layernorm the rows of `a` first (or NULL)
   int n;
   int lks;    // log2 of the number of wavefronts that split a row's octets
-  int flags;  // GEMM_GELU, GEMM_ACC: the GEMM's epilogue options
+  int flags;  // GEMM_GELU, GEMM_ACC: the GEMM's epilogue options; GEMV_REC_OUT
 };
+// Single and set launches: also write the outputs' activation records to
+// `rec` ([n / 32][gemv_rec_bytes(m)], the layout k_gemv_records writes), for
+// a next product of the same dtype whose item reads them (a == NULL, rec
+// set) instead of quantizing these rows in every workgroup.
+constexpr int GEMV_REC_OUT = 8;
 
 // Up to GEMV_SET linears of one dtype that read one activation, launched
 // together without a device table: workgroups [end[t-1], end[t]) run item t.
@@ -1416,9 +1421,55 @@ __device__ inline void gemv_load_residual(const GemvItem &I, int gw, int h, int 
                                                                    : 0.0f;
   }
 }
-template <bool PRE, int NG, bool PREX = false>
+// The records of one block of the outputs a wavefront holds (GEMV_REC_OUT):
+// lanes 32 h + r hold column r of block g for rows 4 h + v, so a row's block
+// is one half of the wavefront; quantized as quantize_block8 quantizes the
+// same 32 values (the largest |x| as integer maxima, NaN skipped, the
+// correctly rounded d = amax / 127 and 1 / d, the exact sum of the quants),
+// so the records are k_gemv_records' for these rows bit for bit.  Every lane
+// of the wavefront calls it (the shuffles); off = the next product's offset
+// term (Q4_0 8, Q5_0 16, else 0).
+__device__ inline void gemv_records_out(const GemvItem &I, int g, int h, int r, int mr, const float (&tv)[4],
+                                        int off) {
+  const int REC = gemv_rec_bytes(mr), ZO = 32 * mr, SO = ZO + 16, DO = SO + 32, PO = DO + 32;
+  uint8_t *rec = I.rec + (size_t)g * REC;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    if (v >= mr) break;  // no row 4 h + v of either half (uniform)
+    int a = __float_as_int(fmaxf(fabsf(tv[v]), 0.0f));
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) a = max(a, __shfl_xor(a, o));
+    const float d = __fdiv_rn(__int_as_float(a), 127.0f);
+    const float inv = d > 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+    const int q = round_clamp_i8(__fmul_rn(tv[v], inv));
+    int sum = q;
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) sum += __shfl_xor(sum, o);
+    const int i = 4 * h + v;
+    if (i < mr) {
+      rec[32 * i + mfma_pos(r)] = (uint8_t)(q & 0xff);
+      if (r == 0) {
+        stg_u32(rec + SO + 4 * i, (uint32_t)(-off * sum));
+        stg_f(reinterpret_cast<float *>(rec + DO + 4 * i), d);
+        stg_f(reinterpret_cast<float *>(rec + PO + 4 * i), __fmul_rn(d, (float)sum));
+      }
+    }
+  }
+  if (h == 0 && r == 0) {
+    stg_u4(rec + ZO, make_uint4(0, 0, 0, 0));
+    for (int z = mr; z < 8; ++z) {
+      stg_u32(rec + SO + 4 * z, 0u);
+      stg_u32(rec + DO + 4 * z, 0u);
+      stg_u32(rec + PO + 4 * z, 0u);
+    }
+  }
+}
+
+// RO: the kernel may be asked for the outputs' records (GEMV_REC_OUT;
+// single and set launches of 2-8 rows, the only ones the host asks).
+template <bool PRE, int NG, bool PREX, bool RO>
 __device__ inline void gemv_epilogue(const GemvItem &I, int gw, int h, int r, int mr, const float (&y)[NG][4],
-                                     const float (&bv_in)[NG], const float (&x_in)[NG][4]) {
+                                     const float (&bv_in)[NG], const float (&x_in)[NG][4], int off) {
   const int n = I.n;
   float bv[NG], x[NG][4];
 #pragma unroll
@@ -1445,6 +1496,22 @@ __device__ inline void gemv_epilogue(const GemvItem &I, int gw, int h, int r, in
           if (I.flags & 2) t = x[j][v] + t;
           stg_f(I.out + (size_t)(4 * h + v) * n + col, t);
         }
+    if constexpr (RO) {
+      // the same values for every lane (the host asks for records only
+      // where n is a multiple of 256: every lane's column exists)
+      if ((I.flags & GEMV_REC_OUT) && gw + j < I.w.ngroups) {
+        float tv[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          float t = y[j][v];
+          if (I.bias) t = t + bv[j];
+          if (I.flags & 1) t = gelu(t);
+          if (I.flags & 2) t = x[j][v] + t;
+          tv[v] = t;
+        }
+        gemv_records_out(I, gw + j, h, r, mr, tv, off);
+      }
+    }
   }
 }
 
@@ -1621,6 +1688,13 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
   const bool stats_regs = !GROUPED && I.a != nullptr && nb <= 64 && has_ln;  // uniform
   const bool regs = RX && I.a != nullptr && nb <= 32 * NUX;
   const bool xin = stats_regs || regs;
+  // the outputs' records for a next product (GEMV_REC_OUT), and its offset term
+  constexpr bool RO = !GROUPED && MR > 1;
+  constexpr int OFFR = DT == 2 ? 8 : DT == 6 ? 16 : 0;
+  // records written by the previous product's epilogue (GEMV_REC_OUT) are
+  // copied whole, as a grouped launch copies k_gemv_records' output
+  // (2-8 rows only, as the host passes them)
+  const bool rin = !GROUPED && MR > 1 && I.a == nullptr && I.rec != nullptr;  // uniform
   // the latency form requests them with its first octets when that needs
   // nothing from the argument block (lnf known)
   const bool x_early = PD > 1 && xin && (regs || lnf >= 0);
@@ -1740,7 +1814,7 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
       const int c0 = ((w.noct * pp) >> lks) + cc, c1 = min((w.noct * (pp + 1)) >> lks, c0 + ch);
       if (c0 >= c1) continue;
       uint8_t *base = lds + pp * ch * OCT * REC;
-      if constexpr (GROUPED) {
+      if (GROUPED || rin) {
         // RB loads per thread in flight at a time (as many as the
         // registers beside the first octet's allow)
         constexpr int RB = DT == 2 || DT == 6 ? 4 : DT == 7 ? 1 : 2;
@@ -1794,7 +1868,7 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
     for (int v = 0; v < 4; ++v) y[j][v] = has_min(DT) ? acc[j][v] + accm[j][v] : acc[j][v];
 
   if (KS == 1) {
-    gemv_epilogue<PRE, NG, PREX>(I, gw, h, r, MR, y, bv, xres);
+    gemv_epilogue<PRE, NG, PREX, RO>(I, gw, h, r, MR, y, bv, xres, OFFR);
     return;
   }
   __syncthreads();  // the activation LDS is reused for the partial sums
@@ -1813,7 +1887,7 @@ __device__ __attribute__((always_inline)) inline void gemv_tile(const GemvItem I
         for (int p = 1; p < KS; ++p) tt = tt + red[((wv + p) * 4 * NG + 4 * j + v) * 64 + l];
         y[j][v] = tt;
       }
-    gemv_epilogue<PRE, NG, PREX>(I, gw, h, r, MR, y, bv, xres);
+    gemv_epilogue<PRE, NG, PREX, RO>(I, gw, h, r, MR, y, bv, xres, OFFR);
   }
 }
 

@@ -718,12 +718,17 @@ static int launch_layernorm(float *x, size_t rows, size_t n, const float *w, con
 // quantized, inside that launch; `flags` (GEMM_GELU, GEMM_ACC) go to every
 // linear's epilogue.  `tmp` ([m, k] f32, or NULL) takes the layernormed rows
 // where the GEMM's quantizer cannot fold the layernorm (k > 8192).
+// rec_out / rec_in (decode sizes, one linear): the product also writes its
+// outputs' activation records (GEMV_REC_OUT), or reads its rows as records
+// another product wrote instead of quantizing `a`.
 static int run_matmul_set(const rw_weight *const *w, size_t count, const float *a, size_t m,
                           const float *const *bias, float *const *out, void *ws, hipStream_t s,
                           const float *lnw = nullptr, const float *lnb = nullptr, int flags = 0,
-                          float *tmp = nullptr) {
+                          float *tmp = nullptr, uint8_t *rec_out = nullptr, uint8_t *rec_in = nullptr) {
   if (m == 0) return RW_OK;
   if (count < 1 || count > (size_t)GEMV_SET) return fail(RW_EINVAL, "a set holds 1 to %d linears", GEMV_SET);
+  if ((rec_out || rec_in) && (count != 1 || m < 2 || m > GEMV_MAX_M))
+    return fail(RW_EINVAL, "activation records pass between single linears of 2 to %d rows", GEMV_MAX_M);
   if (m <= GEMV_MAX_M) {
     GemvSet set{};
     int wgs = 0, need = 0;
@@ -732,6 +737,14 @@ static int run_matmul_set(const rw_weight *const *w, size_t count, const float *
       set.it[i].lnw = lnw;
       set.it[i].lnb = lnb;
       set.it[i].flags = flags;
+      if (rec_out) {
+        set.it[i].rec = rec_out;
+        set.it[i].flags |= GEMV_REC_OUT;
+      }
+      if (rec_in) {
+        set.it[i].a = nullptr;
+        set.it[i].rec = rec_in;
+      }
       wgs += gemv_wgs(w[i], gemv_ks(w[i], true), false);
       set.end[i] = wgs;
       need = std::max(need, gemv_need(w[i], true));
@@ -756,8 +769,9 @@ static int run_matmul_set(const rw_weight *const *w, size_t count, const float *
 
 // one linear (count 1) with the options of run_matmul_set
 static int run_linear(const rw_weight *w, const float *a, size_t m, const float *bias, float *out, void *ws,
-                      hipStream_t s, const float *lnw, const float *lnb, int flags, float *tmp) {
-  return run_matmul_set(&w, 1, a, m, &bias, &out, ws, s, lnw, lnb, flags, tmp);
+                      hipStream_t s, const float *lnw, const float *lnb, int flags, float *tmp,
+                      uint8_t *rec_out = nullptr, uint8_t *rec_in = nullptr) {
+  return run_matmul_set(&w, 1, a, m, &bias, &out, ws, s, lnw, lnb, flags, tmp, rec_out, rec_in);
 }
 
 // ------------------------------------------------- grouped decode GEMV
@@ -1176,7 +1190,7 @@ static int check_decoder_params(const rw_decoder_params *P) {
 // of one token each, whose self-attention runs as n_tok * n_head heads and
 // whose new key / value rows pass through kn, vn)
 struct DecScratch {
-  size_t off_tok, off_x, off_cur, off_q, off_a, off_h, off_kn, off_vn, off_act, off_att, bytes;
+  size_t off_tok, off_x, off_cur, off_q, off_a, off_h, off_kn, off_vn, off_act, off_att, off_rec, bytes;
   AttnLayout self_att, cross_att;
 };
 static DecScratch dec_scratch(const rw_decoder *d, size_t n_tok, bool beams = false) {
@@ -1194,7 +1208,10 @@ static DecScratch dec_scratch(const rw_decoder *d, size_t n_tok, bool beams = fa
   S.off_vn = align_up(S.off_kn + (beams ? row : 0), 256);
   S.off_act = align_up(S.off_vn + (beams ? row : 0), 256);
   S.off_att = align_up(S.off_act + act_layout(n_tok, std::max(d->n, d->f)).bytes, 256);
-  S.bytes = align_up(S.off_att + std::max(S.self_att.bytes, S.cross_att.bytes), 256);
+  S.off_rec = align_up(S.off_att + std::max(S.self_att.bytes, S.cross_att.bytes), 256);
+  // fc2's activation records, written by fc1 (decode sizes)
+  const size_t rec = n_tok <= (size_t)GEMV_MAX_M ? align_up(d->f, 256) / QK * gemv_rec_bytes((int)n_tok) : 0;
+  S.bytes = align_up(S.off_rec + rec, 256);
   return S;
 }
 
@@ -1298,9 +1315,17 @@ static int decoder_forward(rw_decoder *const *dec, size_t nb, bool beams, size_t
     RW_TRY(run_attention(q, n, nullptr, n, nullptr, n, n_tok, d->n_audio, d->p.n_head, 0, att, n, S.cross_att, aws,
                          s, &cp));
     RW_TRY(run_linear(L.cout, att, n_tok, L.cout_b, x, act, s, nullptr, nullptr, GEMM_ACC, nullptr));
-    // MLP
-    RW_TRY(run_linear(L.fc1, x, n_tok, L.fc1_b, h, act, s, L.mlp_ln_w, L.mlp_ln_b, GEMM_GELU, cur));
-    RW_TRY(run_linear(L.fc2, h, n_tok, L.fc2_b, x, act, s, nullptr, nullptr, GEMM_ACC, nullptr));
+    // MLP.  For 2-8 rows fc1's epilogue also writes fc2's activation records
+    // (the values fc2 would quantize in each of its workgroups; whole octets
+    // of blocks, one dtype), and fc2 copies them: the 5-beam step 3.42 ->
+    // 3.21 ms, the same bits.  One row keeps fc2's fill from the values it
+    // loads into registers (2.03 against 2.05 ms per token with records)
+    uint8_t *rec = n_tok >= 2 && n_tok <= (size_t)GEMV_MAX_M && L.fc1->n % (OCT * QK) == 0 &&
+                           L.fc1->dtype == L.fc2->dtype
+                       ? (uint8_t *)(b + S.off_rec)
+                       : nullptr;
+    RW_TRY(run_linear(L.fc1, x, n_tok, L.fc1_b, h, act, s, L.mlp_ln_w, L.mlp_ln_b, GEMM_GELU, cur, rec));
+    RW_TRY(run_linear(L.fc2, h, n_tok, L.fc2_b, x, act, s, nullptr, nullptr, GEMM_ACC, nullptr, nullptr, rec));
   }
   return launch_layernorm(x, n_tok, n, d->p.ln_w, d->p.ln_b, hidden, s, nullptr);
 }
