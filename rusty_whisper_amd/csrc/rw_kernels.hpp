@@ -1429,6 +1429,24 @@ __device__ inline void gemv_load_residual(const GemvItem &I, int gw, int h, int 
 // so the records are k_gemv_records' for these rows bit for bit.  Every lane
 // of the wavefront calls it (the shuffles); off = the next product's offset
 // term (Q4_0 8, Q5_0 16, else 0).
+// Over each 32-lane half of the wavefront, in every lane of it: the integer
+// maximum (MAX) or the sum, by DPP moves within 16-lane rows (pairs, quads,
+// half-row and row mirrors), row 0's (2's) total into row 1 (3) by
+// row_bcast:15, and lanes 31 and 63 read back.  Maxima and integer sums are
+// exact, so the order does not matter.
+template <bool MAX>
+__device__ inline int half_reduce32(int v) {
+  auto op = [](int a, int b) __attribute__((always_inline)) { return MAX ? max(a, b) : a + b; };
+  v = op(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false));   // quad_perm [1,0,3,2]
+  v = op(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false));   // quad_perm [2,3,0,1]
+  v = op(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false));  // row_half_mirror
+  v = op(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xf, 0xf, false));  // row_mirror
+  // rows 1 and 3 only (rows 0 and 2 add 0 / take the maximum with 0: values >= 0)
+  v = op(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+  const int lo = __builtin_amdgcn_readlane(v, 31), hi = __builtin_amdgcn_readlane(v, 63);
+  return (threadIdx.x & 32) ? hi : lo;
+}
+
 __device__ inline void gemv_records_out(const GemvItem &I, int g, int h, int r, int mr, const float (&tv)[4],
                                         int off) {
   const int REC = gemv_rec_bytes(mr), ZO = 32 * mr, SO = ZO + 16, DO = SO + 32, PO = DO + 32;
@@ -1436,15 +1454,11 @@ __device__ inline void gemv_records_out(const GemvItem &I, int g, int h, int r, 
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     if (v >= mr) break;  // no row 4 h + v of either half (uniform)
-    int a = __float_as_int(fmaxf(fabsf(tv[v]), 0.0f));
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) a = max(a, __shfl_xor(a, o));
+    const int a = half_reduce32<true>(__float_as_int(fmaxf(fabsf(tv[v]), 0.0f)));
     const float d = __fdiv_rn(__int_as_float(a), 127.0f);
     const float inv = d > 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
     const int q = round_clamp_i8(__fmul_rn(tv[v], inv));
-    int sum = q;
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) sum += __shfl_xor(sum, o);
+    const int sum = half_reduce32<false>(q);
     const int i = 4 * h + v;
     if (i < mr) {
       rec[32 * i + mfma_pos(r)] = (uint8_t)(q & 0xff);
