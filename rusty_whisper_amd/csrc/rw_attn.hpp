@@ -597,8 +597,16 @@ __global__ __launch_bounds__(128) void k_attn(int t_q, int t_kv, int gw, int nx,
 // Merge nsplit runs of k_attn: out = sum_z O_z 2^(m_z - m) / (2^12 sum_z l_z
 // 2^(m_z - m)), m the largest run maximum (runs that saw nothing have
 // m = -inf and weigh 0).  One thread per (query, head, d).
+// (defined with the decode GEMV: one query row's block of the output as the
+// next product's activation record)
+__device__ void combine_records(uint8_t *rec, int row, int col, int mr, float x, int off);
+
+// With rec: also each query row's 32-column blocks of the output as
+// activation records of the next product (its offset term `rec_off`), for
+// 2-8 query rows; a wavefront holds one (row, head), two blocks.
 __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ part, int nsplit, int n_head,
-                                                      int tq_pad, int t_q, float *__restrict__ out, int ld_out) {
+                                                      int tq_pad, int t_q, float *__restrict__ out, int ld_out,
+                                                      uint8_t *__restrict__ rec, int rec_off) {
   constexpr float LOG2E = 1.4426950408889634f;
   constexpr float NEG_INF = -__builtin_huge_valf();
   const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -632,7 +640,9 @@ __global__ __launch_bounds__(256) void k_attn_combine(const float *__restrict__ 
       den += lz[z] * w;
     }
   }
-  out[(size_t)q * ld_out + head * ATT_DH + d] = num / (den * ATT_PS);
+  const float y = num / (den * ATT_PS);
+  out[(size_t)q * ld_out + head * ATT_DH + d] = y;
+  if (rec) combine_records(rec, q, head * ATT_DH + d, t_q, y, rec_off);  // whole wavefronts (uniform)
 }
 
 #endif  // __HIPCC__

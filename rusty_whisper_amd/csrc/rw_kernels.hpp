@@ -1447,6 +1447,35 @@ __device__ inline int half_reduce32(int v) {
   return (threadIdx.x & 32) ? hi : lo;
 }
 
+// k_attn_combine's records: this lane's output x is element col % 32 of
+// block col / 32 of row `row`, and each 32-lane half of the wavefront holds
+// one such block; quantized as gemv_records_out quantizes a block.  Every
+// lane of the wavefront calls it.
+__device__ void combine_records(uint8_t *rec_base, int row, int col, int mr, float x, int off) {
+  const int REC = gemv_rec_bytes(mr), ZO = 32 * mr, SO = ZO + 16, DO = SO + 32, PO = DO + 32;
+  const int e = col & 31;
+  uint8_t *rec = rec_base + (size_t)(col >> 5) * REC;
+  const int a = half_reduce32<true>(__float_as_int(fmaxf(fabsf(x), 0.0f)));
+  const float d = __fdiv_rn(__int_as_float(a), 127.0f);
+  const float inv = d > 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+  const int q = round_clamp_i8(__fmul_rn(x, inv));
+  const int sum = half_reduce32<false>(q);
+  rec[32 * row + mfma_pos(e)] = (uint8_t)(q & 0xff);
+  if (e == 0) {
+    stg_u32(rec + SO + 4 * row, (uint32_t)(-off * sum));
+    stg_f(reinterpret_cast<float *>(rec + DO + 4 * row), d);
+    stg_f(reinterpret_cast<float *>(rec + PO + 4 * row), __fmul_rn(d, (float)sum));
+    if (row == 0) {
+      stg_u4(rec + ZO, make_uint4(0, 0, 0, 0));
+      for (int z = mr; z < 8; ++z) {
+        stg_u32(rec + SO + 4 * z, 0u);
+        stg_u32(rec + DO + 4 * z, 0u);
+        stg_u32(rec + PO + 4 * z, 0u);
+      }
+    }
+  }
+}
+
 __device__ inline void gemv_records_out(const GemvItem &I, int g, int h, int r, int mr, const float (&tv)[4],
                                         int off) {
   const int REC = gemv_rec_bytes(mr), ZO = 32 * mr, SO = ZO + 16, DO = SO + 32, PO = DO + 32;

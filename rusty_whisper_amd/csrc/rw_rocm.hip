@@ -1056,9 +1056,14 @@ static int check_attn_args(const float *q, size_t ldq, const float *k, size_t ld
   return RW_OK;
 }
 
+// rec (2-8 query rows): where the kv is split, the merge also writes the
+// output rows' activation records for the next product (offset term
+// rec_off), and *rec_done says whether it did.
 static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk, const float *v, size_t ldv,
                          size_t t_q, size_t t_kv, int n_head, int causal, float *out, size_t ldo, const AttnLayout &L,
-                         void *ws, hipStream_t s, const AttnPlanes *kv_split = nullptr) {
+                         void *ws, hipStream_t s, const AttnPlanes *kv_split = nullptr, uint8_t *rec = nullptr,
+                         int rec_off = 0, bool *rec_done = nullptr) {
+  if (rec_done) *rec_done = false;
   char *b = (char *)ws;
   uint16_t *qh = (uint16_t *)(b + L.off_qh), *ql = (uint16_t *)(b + L.off_ql);
   uint16_t *kh = (uint16_t *)(b + L.off_kh), *kl = (uint16_t *)(b + L.off_kl);
@@ -1114,9 +1119,11 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
   LAUNCH_TRY("k_attn");
   if (part) {
     const size_t nz = t_q * (size_t)n_head * ATT_DH;
+    const bool with_rec = rec && t_q >= 2 && t_q <= (size_t)GEMV_MAX_M;
     hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)cdiv(nz, 256)), dim3(256), 0, s, part, nsplit, n_head,
-                       L.tq_pad, (int)t_q, out, (int)ldo);
+                       L.tq_pad, (int)t_q, out, (int)ldo, with_rec ? rec : nullptr, rec_off);
     LAUNCH_TRY("k_attn_combine");
+    if (rec_done) *rec_done = with_rec;
   }
   return RW_OK;
 }
@@ -1209,8 +1216,10 @@ static DecScratch dec_scratch(const rw_decoder *d, size_t n_tok, bool beams = fa
   S.off_act = align_up(S.off_vn + (beams ? row : 0), 256);
   S.off_att = align_up(S.off_act + act_layout(n_tok, std::max(d->n, d->f)).bytes, 256);
   S.off_rec = align_up(S.off_att + std::max(S.self_att.bytes, S.cross_att.bytes), 256);
-  // fc2's activation records, written by fc1 (decode sizes)
-  const size_t rec = n_tok <= (size_t)GEMV_MAX_M ? align_up(d->f, 256) / QK * gemv_rec_bytes((int)n_tok) : 0;
+  // activation records passed between products (decode sizes): fc2's from
+  // fc1, cross-out's from the cross-attention's merge
+  const size_t rec =
+      n_tok <= (size_t)GEMV_MAX_M ? align_up(std::max(d->f, d->n), 256) / QK * gemv_rec_bytes((int)n_tok) : 0;
   S.bytes = align_up(S.off_rec + rec, 256);
   return S;
 }
@@ -1243,7 +1252,7 @@ static int run_beam_self_attention(rw_decoder *const *beams, size_t nb, int l, c
   LAUNCH_TRY("k_attn");
   if (part) {
     hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)cdiv((size_t)heads * ATT_DH, 256)), dim3(256), 0, s, part, nsplit,
-                       heads, L.tq_pad, 1, att, (int)d->n);
+                       heads, L.tq_pad, 1, att, (int)d->n, nullptr, 0);
     LAUNCH_TRY("k_attn_combine");
   }
   return RW_OK;
@@ -1312,9 +1321,16 @@ static int decoder_forward(rw_decoder *const *dec, size_t nb, bool beams, size_t
     // cross-attention to the window's K/V
     RW_TRY(run_linear(L.cq, x, n_tok, L.cq_b, q, act, s, L.cross_ln_w, L.cross_ln_b, 0, cur));
     const AttnPlanes cp = d->cross->planes(l);
+    // for 2-8 rows the merge of the split kv also writes cross-out's
+    // activation records (whole octets of blocks), which cross-out copies
+    uint8_t *crec = n_tok >= 2 && n_tok <= (size_t)GEMV_MAX_M && n % (OCT * QK) == 0 ? (uint8_t *)(b + S.off_rec)
+                                                                                     : nullptr;
+    bool crec_done = false;
+    const int coff = L.cout->dtype == RW_Q4_0 ? 8 : L.cout->dtype == RW_Q5_0 ? 16 : 0;
     RW_TRY(run_attention(q, n, nullptr, n, nullptr, n, n_tok, d->n_audio, d->p.n_head, 0, att, n, S.cross_att, aws,
-                         s, &cp));
-    RW_TRY(run_linear(L.cout, att, n_tok, L.cout_b, x, act, s, nullptr, nullptr, GEMM_ACC, nullptr));
+                         s, &cp, crec, coff, &crec_done));
+    RW_TRY(run_linear(L.cout, att, n_tok, L.cout_b, x, act, s, nullptr, nullptr, GEMM_ACC, nullptr, nullptr,
+                      crec_done ? crec : nullptr));
     // MLP.  For 2-8 rows fc1's epilogue also writes fc2's activation records
     // (the values fc2 would quantize in each of its workgroups; whole octets
     // of blocks, one dtype), and fc2 copies them: the 5-beam step 3.42 ->
