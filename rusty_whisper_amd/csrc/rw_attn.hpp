@@ -378,11 +378,19 @@ __device__ inline void att_split_v(const AttVRaw &x, AttV &o) {
 // block; the planes (P) follow.  The grid comes as arguments too (gridDim
 // is read from the argument block): nx = gridDim.x, gw = causal | gridDim.z
 // << 1 | gridDim.y << 8.
+// (defined with the decode GEMV: a block of 8 lanes x 4 values as row i's
+// activation record of block bl)
+__device__ void attn_block_records(uint8_t *rec, int i, int bl, int lt, int mr, float4 x, int off, bool write);
+
+// rec (several beams' self-attention, one query row per (beam, head) plane,
+// no kv split): also the output rows' activation records for the next
+// product; rec_hd = heads per beam | offset term << 8 | beams << 16.
 template <bool ROWS, int QT>
 __global__ __launch_bounds__(128) void k_attn(int t_q, int t_kv, int gw, int nx, const float *__restrict__ qf,
                                               int ldq, const float *__restrict__ kf, int ldk,
                                               const float *__restrict__ vf, int ldv, float *__restrict__ out,
-                                              int ld_out, float *__restrict__ part, AttnPlanes P) {
+                                              int ld_out, float *__restrict__ part, AttnPlanes P,
+                                              uint8_t *__restrict__ rec, int rec_hd) {
   const int causal = gw & 1, gz = (gw >> 1) & 127, gy = gw >> 8;
   constexpr int QB = 32 * QT;  // query rows per workgroup
   constexpr float LOG2E = 1.4426950408889634f;
@@ -590,6 +598,14 @@ __global__ __launch_bounds__(128) void k_attn(int t_q, int t_kv, int gw, int nx,
       float *dst = part ? part + (((size_t)blockIdx.z * gy + head) * P.tq_pad + q0 + row) * ATT_DH + 4 * c4
                         : out + (size_t)(q0 + row) * ld_out + head * ATT_DH + 4 * c4;
       *reinterpret_cast<float4 *>(dst) = *reinterpret_cast<const float4 *>(&xo[row * LD + 4 * c4]);
+    }
+    // the one query row is threads 0-15 of the first pass: each 8 of them
+    // one 32-column block (every lane of the wavefront quantizes its values)
+    if (it == 0 && rec && threadIdx.x < 64) {
+      const int hpb = rec_hd & 255;
+      attn_block_records(rec, head / hpb, (head % hpb) * 2 + (c4 >> 3), c4 & 7, rec_hd >> 16,
+                         *reinterpret_cast<const float4 *>(&xo[row * LD + 4 * c4]), (rec_hd >> 8) & 255,
+                         q0 + row < t_q && row == 0);
     }
   }
 }

@@ -1447,6 +1447,31 @@ __device__ inline int half_reduce32(int v) {
   return (threadIdx.x & 32) ? hi : lo;
 }
 
+// k_attn's records (several beams' self-attention): the 8 lanes of each
+// 8-lane group hold 4 values each of one 32-column block, quantize_block8's
+// layout; those with `write` are block bl of row i.  Every lane of the
+// wavefront calls it.
+__device__ void attn_block_records(uint8_t *rec_base, int i, int bl, int lt, int mr, float4 x, int off, bool write) {
+  const int REC = gemv_rec_bytes(mr), ZO = 32 * mr, SO = ZO + 16, DO = SO + 32, PO = DO + 32;
+  const BlockQuant bq = quantize_block8(x);
+  if (!write) return;
+  uint8_t *rec = rec_base + (size_t)bl * REC;
+  stg_u32(rec + 32 * i + mfma_pos(4 * lt), pack_q4(bq));
+  if (lt == 0) {
+    stg_u32(rec + SO + 4 * i, (uint32_t)(-off * bq.sum));
+    stg_f(reinterpret_cast<float *>(rec + DO + 4 * i), bq.d);
+    stg_f(reinterpret_cast<float *>(rec + PO + 4 * i), __fmul_rn(bq.d, (float)bq.sum));
+    if (i == 0) {
+      stg_u4(rec + ZO, make_uint4(0, 0, 0, 0));
+      for (int z = mr; z < 8; ++z) {
+        stg_u32(rec + SO + 4 * z, 0u);
+        stg_u32(rec + DO + 4 * z, 0u);
+        stg_u32(rec + PO + 4 * z, 0u);
+      }
+    }
+  }
+}
+
 // k_attn_combine's records: this lane's output x is element col % 32 of
 // block col / 32 of row `row`, and each 32-lane half of the wavefront holds
 // one such block; quantized as gemv_records_out quantizes a block.  Every

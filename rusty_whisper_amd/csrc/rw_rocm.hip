@@ -1106,16 +1106,16 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
   const int gw = cz | nsplit << 1 | n_head << 8;  // k_attn's packed grid
   if (rows && one_tile)
     hipLaunchKernelGGL((k_attn<true, 1>), grid, dim3(128), 0, s, (int)t_q, (int)t_kv, gw, (int)grid.x, q, (int)ldq, k,
-                       (int)ldk, v, (int)ldv, out, (int)ldo, part, P);
+                       (int)ldk, v, (int)ldv, out, (int)ldo, part, P, nullptr, 0);
   else if (rows)
     hipLaunchKernelGGL((k_attn<true, 2>), grid, dim3(128), 0, s, (int)t_q, (int)t_kv, gw, (int)grid.x, q, (int)ldq, k,
-                       (int)ldk, v, (int)ldv, out, (int)ldo, part, P);
+                       (int)ldk, v, (int)ldv, out, (int)ldo, part, P, nullptr, 0);
   else if (one_tile)
     hipLaunchKernelGGL((k_attn<false, 1>), grid, dim3(128), 0, s, (int)t_q, (int)t_kv, gw, (int)grid.x, q, (int)ldq,
-                       nullptr, 0, nullptr, 0, out, (int)ldo, part, P);
+                       nullptr, 0, nullptr, 0, out, (int)ldo, part, P, nullptr, 0);
   else
     hipLaunchKernelGGL((k_attn<false, 2>), grid, dim3(128), 0, s, (int)t_q, (int)t_kv, gw, (int)grid.x, q, (int)ldq,
-                       nullptr, 0, nullptr, 0, out, (int)ldo, part, P);
+                       nullptr, 0, nullptr, 0, out, (int)ldo, part, P, nullptr, 0);
   LAUNCH_TRY("k_attn");
   if (part) {
     const size_t nz = t_q * (size_t)n_head * ATT_DH;
@@ -1226,8 +1226,13 @@ static DecScratch dec_scratch(const rw_decoder *d, size_t n_tok, bool beams = fa
 
 // One self-attention over several beams' caches (one new row each): the
 // planes of beam b, head h are head b * n_head + h of one k_attn launch.
+// rec: without a kv split, k_attn also writes the output rows' activation
+// records for the next product (offset term rec_off); *rec_done says
+// whether it did.
 static int run_beam_self_attention(rw_decoder *const *beams, size_t nb, int l, const float *q, const float *kn,
-                                   const float *vn, float *att, const AttnLayout &L, void *ws, hipStream_t s) {
+                                   const float *vn, float *att, const AttnLayout &L, void *ws, hipStream_t s,
+                                   uint8_t *rec = nullptr, int rec_off = 0, bool *rec_done = nullptr) {
+  if (rec_done) *rec_done = false;
   const rw_decoder *d = beams[0];
   const int n_head = d->p.n_head, heads = (int)nb * n_head;
   const size_t n_past = d->n_past, t_kv = n_past + 1;
@@ -1247,9 +1252,12 @@ static int run_beam_self_attention(rw_decoder *const *beams, size_t nb, int l, c
   LAUNCH_TRY("k_attn_split_beams");
   const int nsplit = std::min(L.nsplit, attn_nsplit((size_t)(L.tq_pad / ATT_QB) * heads, cdiv(t_kv, ATT_KVB)));
   float *part = nsplit > 1 ? (float *)(b + L.off_part) : nullptr;
+  const bool with_rec = rec && !part && nb >= 2 && nb <= (size_t)GEMV_MAX_M;
   hipLaunchKernelGGL((k_attn<false, 1>), dim3(1, (unsigned)heads, (unsigned)nsplit), dim3(128), 0, s, 1, (int)t_kv,
-                     1 | nsplit << 1 | heads << 8, 1, nullptr, 0, nullptr, 0, nullptr, 0, att, (int)d->n, part, P);
+                     1 | nsplit << 1 | heads << 8, 1, nullptr, 0, nullptr, 0, nullptr, 0, att, (int)d->n, part, P,
+                     with_rec ? rec : nullptr, n_head | rec_off << 8 | (int)nb << 16);
   LAUNCH_TRY("k_attn");
+  if (rec_done) *rec_done = with_rec;
   if (part) {
     hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)cdiv((size_t)heads * ATT_DH, 256)), dim3(256), 0, s, part, nsplit,
                        heads, L.tq_pad, 1, att, (int)d->n, nullptr, 0);
@@ -1312,12 +1320,19 @@ static int decoder_forward(rw_decoder *const *dec, size_t nb, bool beams, size_t
         for (int i = 0; i < 3; ++i) RW_TRY(run_matmul(w3[i], cur, n_tok, b3[i], o3[i], act, s));
       }
     }
+    // several beams: where their self-attention runs unsplit it also writes
+    // out's activation records (whole octets of blocks), which out copies
+    uint8_t *orec = n_tok >= 2 && n_tok <= (size_t)GEMV_MAX_M && n % (OCT * QK) == 0 ? (uint8_t *)(b + S.off_rec)
+                                                                                     : nullptr;
+    bool orec_done = false;
+    const int ooff = L.out->dtype == RW_Q4_0 ? 8 : L.out->dtype == RW_Q5_0 ? 16 : 0;
     if (beams)
-      RW_TRY(run_beam_self_attention(dec, nb, l, q, kn, vn, att, S.self_att, aws, s));
+      RW_TRY(run_beam_self_attention(dec, nb, l, q, kn, vn, att, S.self_att, aws, s, orec, ooff, &orec_done));
     else
       RW_TRY(run_attention(q, n, d->self_k(l), n, d->self_v(l), n, n_tok, t_kv, d->p.n_head, 1, att, n, S.self_att,
                            aws, s));
-    RW_TRY(run_linear(L.out, att, n_tok, L.out_b, x, act, s, nullptr, nullptr, GEMM_ACC, nullptr));
+    RW_TRY(run_linear(L.out, att, n_tok, L.out_b, x, act, s, nullptr, nullptr, GEMM_ACC, nullptr, nullptr,
+                      orec_done ? orec : nullptr));
     // cross-attention to the window's K/V
     RW_TRY(run_linear(L.cq, x, n_tok, L.cq_b, q, act, s, L.cross_ln_w, L.cross_ln_b, 0, cur));
     const AttnPlanes cp = d->cross->planes(l);
