@@ -170,78 +170,6 @@ struct BeamCaches {
   float *v[ATT_MAX_BEAMS];  // and value cache
 };
 
-// The beams' planes in one launch: workgroups [0, wq) split q (the beams'
-// new rows, q [nb][n], scaled by 1/8; one query row per beam), [wq, wq + wk)
-// the keys, the rest v^T.  Key / value row r < n_past comes from beam b's
-// cache, row n_past from the step's new rows (kn, vn [nb][n]), which are also
-// stored into the caches at row n_past (each value by one thread).
-__global__ __launch_bounds__(256) void k_attn_split_beams(const float *__restrict__ q, const float *__restrict__ kn,
-                                                          const float *__restrict__ vn, BeamCaches C, int nb,
-                                                          int n_head, int n_past, AttnPlanes P, int wq, int wk) {
-  const int bx = blockIdx.x;
-  const int n = n_head * ATT_DH, t_kv = n_past + 1, heads = nb * n_head;
-  if (bx < wq) {
-    // plane head' = b * n_head + h of row 0 is q + b * n + h * 64, which is
-    // where att_split_rows reads head' of a one-row input
-    const size_t idx = (size_t)bx * 256 + threadIdx.x;
-    if (idx < (size_t)heads * P.tq_pad * 8)
-      att_split_rows(idx, q, n, 1, P.tq_pad, 0.125f, const_cast<uint16_t *>(P.qh), const_cast<uint16_t *>(P.ql));
-  } else if (bx < wq + wk) {
-    const size_t idx = (size_t)(bx - wq) * 256 + threadIdx.x;
-    if (idx >= (size_t)heads * P.tkv_pad * 8) return;
-    const int c = (int)(idx & 7);
-    const size_t hr = idx >> 3;  // head' * tkv_pad + row
-    const int row = (int)(hr % P.tkv_pad), hd = (int)(hr / P.tkv_pad);
-    const int b = hd / n_head, h = hd % n_head;
-    float v[8];
-    if (row < t_kv) {
-      const float *src = row < n_past ? C.k[b] + (size_t)row * n : kn + (size_t)b * n;
-      const float4 *s4 = reinterpret_cast<const float4 *>(src + h * ATT_DH + c * 8);
-      const float4 a = s4[0], e = s4[1];
-      v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = e.x, v[5] = e.y, v[6] = e.z, v[7] = e.w;
-      if (row == n_past) {
-        float4 *d4 = reinterpret_cast<float4 *>(C.k[b] + (size_t)n_past * n + h * ATT_DH + c * 8);
-        d4[0] = a;
-        d4[1] = e;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = 0.0f;
-    }
-    uint16_t h8[8], l8[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) att_split(v[j], h8[j], l8[j]);
-    const size_t o = hr * ATT_DH + c * 8;
-    *reinterpret_cast<uint4 *>(const_cast<uint16_t *>(P.kh) + o) = *reinterpret_cast<const uint4 *>(h8);
-    *reinterpret_cast<uint4 *>(const_cast<uint16_t *>(P.kl) + o) = *reinterpret_cast<const uint4 *>(l8);
-  } else {
-    const size_t idx = (size_t)(bx - wq - wk) * 256 + threadIdx.x;
-    const int nc = P.tkv_pad / 8;
-    const int d = (int)(idx % ATT_DH);
-    const size_t hc = idx / ATT_DH;
-    const int cc = (int)(hc % nc), hd = (int)(hc / nc);
-    if (hd >= heads) return;
-    const int b = hd / n_head, h = hd % n_head;
-    uint16_t h8[8], l8[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int p = cc * 8 + e;
-      const int kv = (p & ~15) | attn_vpos(p & 15);
-      float x = 0.0f;
-      if (kv < n_past) {
-        x = C.v[b][(size_t)kv * n + h * ATT_DH + d];
-      } else if (kv == n_past) {
-        x = vn[(size_t)b * n + h * ATT_DH + d];
-        C.v[b][(size_t)n_past * n + h * ATT_DH + d] = x;
-      }
-      att_split(x, h8[e], l8[e]);
-    }
-    const size_t o = ((size_t)hd * ATT_DH + d) * P.tkv_pad + cc * 8;
-    *reinterpret_cast<uint4 *>(const_cast<uint16_t *>(P.vh) + o) = *reinterpret_cast<const uint4 *>(h8);
-    *reinterpret_cast<uint4 *>(const_cast<uint16_t *>(P.vl) + o) = *reinterpret_cast<const uint4 *>(l8);
-  }
-}
-
 // out rows [0, t) x columns [0, cols) = 0 (attention over no keys)
 __global__ __launch_bounds__(256) void k_attn_zero(float *__restrict__ out, int ld, int t, int cols) {
   const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -300,10 +228,12 @@ struct AttKRaw {
 struct AttVRaw {
   float x[2][2][8];
 };
+// (last: the newest kv row, t_kv - 1, comes from there instead of kf / vf)
 __device__ inline void att_load_k_raw(const float *kf, int ldk, int t_kv, int head, int blk, int h, int n,
-                                      AttKRaw &o) {
+                                      AttKRaw &o, const float *last = nullptr) {
   // lane (h, n): kv row 32 blk + n, values 8h + 16s .. + 7
-  const float *src = kf + (size_t)min(blk * ATT_KVB + n, t_kv - 1) * ldk + head * ATT_DH + 8 * h;
+  const int row = min(blk * ATT_KVB + n, t_kv - 1);
+  const float *src = (last && row == t_kv - 1 ? last : kf + (size_t)row * ldk) + head * ATT_DH + 8 * h;
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     o.x[s][0] = *reinterpret_cast<const float4 *>(src + 16 * s);
@@ -325,7 +255,7 @@ __device__ inline void att_split_k(const AttKRaw &x, bool live, AttK &o) {
   }
 }
 __device__ inline void att_load_v_raw(const float *vf, int ldv, int t_kv, int head, int blk, int h, int n,
-                                      AttVRaw &o) {
+                                      AttVRaw &o, const float *last = nullptr) {
   // lane (h, n): value d = 32 dt + n of the kv rows that the v^T plane keeps
   // at positions 32 blk + 16 s + 8 h + e (attn_vpos order within 16)
 #pragma unroll
@@ -334,8 +264,8 @@ __device__ inline void att_load_v_raw(const float *vf, int ldv, int t_kv, int he
     for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int kv = blk * ATT_KVB + 16 * s + attn_vpos(8 * h + e);
-        const float x = vf[(size_t)min(kv, t_kv - 1) * ldv + head * ATT_DH + dt * 32 + n];
+        const int kv = blk * ATT_KVB + 16 * s + attn_vpos(8 * h + e), row = min(kv, t_kv - 1);
+        const float x = (last && row == t_kv - 1 ? last : vf + (size_t)row * ldv)[head * ATT_DH + dt * 32 + n];
         o.x[dt][s][e] = kv < t_kv ? x : 0.0f;
       }
 }
@@ -382,15 +312,19 @@ __device__ inline void att_split_v(const AttVRaw &x, AttV &o) {
 // activation record of block bl)
 __device__ void attn_block_records(uint8_t *rec, int i, int bl, int lt, int mr, float4 x, int off, bool write);
 
-// rec (several beams' self-attention, one query row per (beam, head) plane,
-// no kv split): also the output rows' activation records for the next
-// product; rec_hd = heads per beam | offset term << 8 | beams << 16.
-template <bool ROWS, int QT>
+// BEAMS (with ROWS): several beams' self-attention, one query row per
+// (beam, head) plane, plane b * n_head + h; its q row is qf + b n + 64 h, its
+// K and V rows beam b's caches C.k[b], C.v[b] except the newest (row
+// t_kv - 1), which comes from the step's new rows kf, vf [beams][n] and is
+// stored into the caches at that row (by the kv split's first run).
+// rec (BEAMS, no kv split): also the output rows' activation records for
+// the next product.  rec_hd = heads per beam | offset term << 8 | beams << 16.
+template <bool ROWS, int QT, bool BEAMS = false>
 __global__ __launch_bounds__(128) void k_attn(int t_q, int t_kv, int gw, int nx, const float *__restrict__ qf,
                                               int ldq, const float *__restrict__ kf, int ldk,
                                               const float *__restrict__ vf, int ldv, float *__restrict__ out,
                                               int ld_out, float *__restrict__ part, AttnPlanes P,
-                                              uint8_t *__restrict__ rec, int rec_hd) {
+                                              uint8_t *__restrict__ rec, int rec_hd, BeamCaches C) {
   const int causal = gw & 1, gz = (gw >> 1) & 127, gy = gw >> 8;
   constexpr int QB = 32 * QT;  // query rows per workgroup
   constexpr float LOG2E = 1.4426950408889634f;
@@ -465,14 +399,30 @@ __global__ __launch_bounds__(128) void k_attn(int t_q, int t_kv, int gw, int nx,
   AttV vb;
   AttKRaw kr_cur, kr_nxt;  // ROWS: f32 K rows, split when their block comes
   AttVRaw vr;
+  // this plane's K and V rows (BEAMS: its beam's caches and new row)
+  const float *kfp = kf, *vfp = vf, *klast = nullptr, *vlast = nullptr;
+  int hkv = head;
+  if constexpr (BEAMS) {
+    const int hpb = rec_hd & 255, bb = head / hpb;
+    hkv = head - bb * hpb;
+    kfp = C.k[bb];
+    vfp = C.v[bb];
+    klast = kf + (size_t)bb * ldk;
+    vlast = vf + (size_t)bb * ldv;
+    if (blockIdx.z == 0) {  // the new row into the caches (read from kf / vf in this launch)
+      const int t = threadIdx.x & 63;
+      if (threadIdx.x < 64) C.k[bb][(size_t)(t_kv - 1) * ldk + hkv * ATT_DH + t] = klast[hkv * ATT_DH + t];
+      else C.v[bb][(size_t)(t_kv - 1) * ldv + hkv * ATT_DH + t] = vlast[hkv * ATT_DH + t];
+    }
+  }
   if (b_begin + wv < nblk) {
-    if constexpr (ROWS) att_load_k_raw(kf, ldk, t_kv, head, b_begin + wv, h, n, kr_cur);
+    if constexpr (ROWS) att_load_k_raw(kfp, ldk, t_kv, hkv, b_begin + wv, h, n, kr_cur, klast);
     else att_load_k(P, head, b_begin + wv, h, n, cur);
   }
   for (int b = b_begin + wv; b < nblk; b += 2) {
     if constexpr (ROWS) {
-      att_load_v_raw(vf, ldv, t_kv, head, b, h, n, vr);
-      if (b + 2 < nblk) att_load_k_raw(kf, ldk, t_kv, head, b + 2, h, n, kr_nxt);
+      att_load_v_raw(vfp, ldv, t_kv, hkv, b, h, n, vr, vlast);
+      if (b + 2 < nblk) att_load_k_raw(kfp, ldk, t_kv, hkv, b + 2, h, n, kr_nxt, klast);
       att_split_k(kr_cur, b * ATT_KVB + n < t_kv, cur);
     } else {
       att_load_v(P, head, b, h, n, vb);

@@ -1106,16 +1106,16 @@ static int run_attention(const float *q, size_t ldq, const float *k, size_t ldk,
   const int gw = cz | nsplit << 1 | n_head << 8;  // k_attn's packed grid
   if (rows && one_tile)
     hipLaunchKernelGGL((k_attn<true, 1>), grid, dim3(128), 0, s, (int)t_q, (int)t_kv, gw, (int)grid.x, q, (int)ldq, k,
-                       (int)ldk, v, (int)ldv, out, (int)ldo, part, P, nullptr, 0);
+                       (int)ldk, v, (int)ldv, out, (int)ldo, part, P, nullptr, 0, BeamCaches{});
   else if (rows)
     hipLaunchKernelGGL((k_attn<true, 2>), grid, dim3(128), 0, s, (int)t_q, (int)t_kv, gw, (int)grid.x, q, (int)ldq, k,
-                       (int)ldk, v, (int)ldv, out, (int)ldo, part, P, nullptr, 0);
+                       (int)ldk, v, (int)ldv, out, (int)ldo, part, P, nullptr, 0, BeamCaches{});
   else if (one_tile)
     hipLaunchKernelGGL((k_attn<false, 1>), grid, dim3(128), 0, s, (int)t_q, (int)t_kv, gw, (int)grid.x, q, (int)ldq,
-                       nullptr, 0, nullptr, 0, out, (int)ldo, part, P, nullptr, 0);
+                       nullptr, 0, nullptr, 0, out, (int)ldo, part, P, nullptr, 0, BeamCaches{});
   else
     hipLaunchKernelGGL((k_attn<false, 2>), grid, dim3(128), 0, s, (int)t_q, (int)t_kv, gw, (int)grid.x, q, (int)ldq,
-                       nullptr, 0, nullptr, 0, out, (int)ldo, part, P, nullptr, 0);
+                       nullptr, 0, nullptr, 0, out, (int)ldo, part, P, nullptr, 0, BeamCaches{});
   LAUNCH_TRY("k_attn");
   if (part) {
     const size_t nz = t_q * (size_t)n_head * ATT_DH;
@@ -1245,17 +1245,15 @@ static int run_beam_self_attention(rw_decoder *const *beams, size_t nb, int l, c
     C.k[i] = beams[i]->self_k(l);
     C.v[i] = beams[i]->self_v(l);
   }
-  const size_t nq = (size_t)heads * L.tq_pad * 8, nk = (size_t)heads * P.tkv_pad * 8;
-  const int wq = (int)cdiv(nq, 256), wk = (int)cdiv(nk, 256);
-  hipLaunchKernelGGL(k_attn_split_beams, dim3((unsigned)(wq + 2 * wk)), dim3(256), 0, s, q, kn, vn, C, (int)nb,
-                     n_head, (int)n_past, P, wq, wk);
-  LAUNCH_TRY("k_attn_split_beams");
+  // one launch: each (beam, head) plane splits its q row and its beam's
+  // cached K and V rows as it loads them, takes the newest row from kn / vn
+  // and stores it into the beam's caches
   const int nsplit = std::min(L.nsplit, attn_nsplit((size_t)(L.tq_pad / ATT_QB) * heads, cdiv(t_kv, ATT_KVB)));
   float *part = nsplit > 1 ? (float *)(b + L.off_part) : nullptr;
   const bool with_rec = rec && !part && nb >= 2 && nb <= (size_t)GEMV_MAX_M;
-  hipLaunchKernelGGL((k_attn<false, 1>), dim3(1, (unsigned)heads, (unsigned)nsplit), dim3(128), 0, s, 1, (int)t_kv,
-                     1 | nsplit << 1 | heads << 8, 1, nullptr, 0, nullptr, 0, nullptr, 0, att, (int)d->n, part, P,
-                     with_rec ? rec : nullptr, n_head | rec_off << 8 | (int)nb << 16);
+  hipLaunchKernelGGL((k_attn<true, 1, true>), dim3(1, (unsigned)heads, (unsigned)nsplit), dim3(128), 0, s, 1,
+                     (int)t_kv, 1 | nsplit << 1 | heads << 8, 1, q, (int)d->n, kn, (int)d->n, vn, (int)d->n, att,
+                     (int)d->n, part, P, with_rec ? rec : nullptr, n_head | rec_off << 8 | (int)nb << 16, C);
   LAUNCH_TRY("k_attn");
   if (rec_done) *rec_done = with_rec;
   if (part) {
